@@ -1,0 +1,57 @@
+// Shared device helpers of libvmk (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+namespace vmk {
+
+typedef _Float16 f16;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// 32x32x16 fp16 MFMA, fp32 accumulate.  Operand layout (wave64):
+//   A (32 x 16): lane l holds row l%32, k-group l/32, 8 consecutive k of that group;
+//   B (16 x 32): lane l holds column l%32, same k-group/elements as A;
+//   D (32 x 32): lane l holds column l%32 and rows 8*blk + 4*(l/32) + c in register 4*blk + c.
+// Only the pairing of A's and B's k-elements matters for the product, so callers may map the 16 k-slots of one
+// instruction onto any 16 logical k indices as long as A and B use the same map.
+__device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
+
+__device__ __forceinline__ half8 zero_h8() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
+
+__device__ __forceinline__ half8 as_h8(u32x4 u) { return __builtin_bit_cast(half8, u); }
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// 16-bit lane i (0..7) of eight 16-byte rows -> one 16-byte column (row j in 16-bit lane j).
+__device__ __forceinline__ u32x4 column8(const u32x4 (&r)[8], int i) {
+  const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+  const int w = i >> 1;
+  u32x4 o;
+  o[0] = __builtin_amdgcn_perm(r[1][w], r[0][w], sel);
+  o[1] = __builtin_amdgcn_perm(r[3][w], r[2][w], sel);
+  o[2] = __builtin_amdgcn_perm(r[5][w], r[4][w], sel);
+  o[3] = __builtin_amdgcn_perm(r[7][w], r[6][w], sel);
+  return o;
+}
+
+__device__ __forceinline__ half8 pack8(float a0, float a1, float a2, float a3, float a4, float a5, float a6,
+                                       float a7) {
+  return half8{(f16)a0, (f16)a1, (f16)a2, (f16)a3, (f16)a4, (f16)a5, (f16)a6, (f16)a7};
+}
+
+}  // namespace vmk

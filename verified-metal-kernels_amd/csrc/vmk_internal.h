@@ -1,0 +1,30 @@
+// Host-side helpers of the C-ABI entry points: argument checks and the last-error string.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <algorithm>
+
+namespace vmk {
+void set_error(const char* fmt, ...);
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline void* align_up(void* p, size_t a) { return (void*)(((uintptr_t)p + a - 1) & ~(uintptr_t)(a - 1)); }
+}  // namespace vmk
+
+// Returns 1 from the entry point with a message when a host-side precondition fails (nothing is launched).
+#define VMK_CHECK(cond, msg)                                                   \
+  do {                                                                         \
+    if (!(cond)) {                                                             \
+      ::vmk::set_error("%s: %s", __func__, msg);                               \
+      return 1;                                                                \
+    }                                                                          \
+  } while (0)
+
+// Returns 2 with the HIP error string when a launch or runtime call fails.
+#define VMK_CHECK_HIP(expr)                                                    \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess) {                                                    \
+      ::vmk::set_error("%s: %s (%s)", __func__, hipGetErrorString(e_), #expr); \
+      return 2;                                                                \
+    }                                                                          \
+  } while (0)

@@ -1,0 +1,196 @@
+// Speculative chain/tree verification on gfx950: split-K flash-decoding over the kd*G query rows of one GQA group.
+//
+// Replaces the reference's spec_verify_qperm / spec_verify_partial_mpp / spec_verify_combine Metal kernels
+// (kernels/spec_opus55_v7.py:186-199, 228-342, 344-365) behind the kernel(q, k, v, bits) contract of
+// ops/spec.py:1-3.  The draft mask is applied in registers from (B, kd, W) 32-bit words, so kd is not limited to 32.
+#include "attn_core.h"
+#include "vmk_internal.h"
+
+namespace vmk {
+
+struct SpecArgs {
+  const f16* q;            // (B, kd, Hq, 128)
+  const f16* k;            // (B, Hkv, L, 128)
+  const f16* v;
+  const uint32_t* bits;    // (B, kd, W)
+  float* part_o;           // [item][32*WR][128], item = (grp * nrb + rb) * nsplit + split
+  float* part_ml;          // [item][32*WR][2]
+  f16* out;                // (B, kd, Hq, 128)
+  int B, kd, Hq, Hkv, G, L, W;
+  int WR, WK, nrb, nsplit, chunk;
+  float sl2;               // softmax scale * log2(e)
+};
+
+// Keys of one (batch, KV head) for one split: rows of k/v, the draft mask on the last kd positions.
+struct SpecSrc {
+  const f16* kbase;
+  const f16* vbase;
+  const uint32_t* mrow;    // mask words of this lane's draft row
+  int kend, tail0, kd;
+  float sl2;
+  __device__ const f16* krow(int key) const { return kbase + (size_t)min(key, kend - 1) * 128; }
+  __device__ const f16* vrow(int key) const { return vbase + (size_t)min(key, kend - 1) * 128; }
+  __device__ bool valid(int key) const { return key < kend; }
+  __device__ void mask_scale(floatx16& s, int key0, int g) const {
+    const bool tail = key0 + kTile > tail0;           // same for the whole wave
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int key = key0 + 8 * blk + 4 * g + c;
+        bool ok = key < kend;
+        if (tail) {
+          const int j = min(max(key - tail0, 0), kd - 1);
+          const uint32_t w = mrow[j >> 5];
+          ok = ok && (key < tail0 || ((w >> (j & 31)) & 1u));
+        }
+        s[4 * blk + c] = ok ? s[4 * blk + c] * sl2 : kNegInf;
+      }
+  }
+};
+
+// One workgroup = WR x WK waves: WR row blocks of 32 rows, WK waves interleaving the key tiles of one split.
+__global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
+  __shared__ __attribute__((aligned(16))) float smem[3 * kSlotFloats];   // >= 4 transposed V tiles
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wr = wave % a.WR, wk = wave / a.WR;
+  const int item = blockIdx.x;
+  const int split = item % a.nsplit;
+  const int rb = (item / a.nsplit) % a.nrb;
+  const int grp = item / (a.nsplit * a.nrb);
+  const int b = grp / a.Hkv, h = grp % a.Hkv;
+  const int R = a.kd * a.G;
+  const int r = lane & 31, g = lane >> 5;
+  const int row = (rb * a.WR + wr) * 32 + r;             // query row i*G + gg of this GQA group
+  const bool rvalid = row < R;
+  const int rowc = rvalid ? row : 0;
+  const int di = rowc / a.G, gg = rowc % a.G;
+
+  half8 qb[8];
+  load_qt(qb, a.q + ((size_t)(b * a.kd + di) * a.Hq + h * a.G + gg) * 128, g, rvalid);
+
+  SpecSrc src;
+  const size_t kvoff = (size_t)grp * a.L * 128;
+  src.kbase = a.k + kvoff;
+  src.vbase = a.v + kvoff;
+  src.mrow = a.bits + (size_t)(b * a.kd + di) * a.W;
+  const int kbeg = split * a.chunk;
+  src.kend = min(a.L, kbeg + a.chunk);
+  src.tail0 = a.L - a.kd;
+  src.kd = a.kd;
+  src.sl2 = a.sl2;
+  const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
+
+  f16* vt = reinterpret_cast<f16*>(smem) + wave * kVTileHalfs;
+  RowState st;
+  row_state_init(st);
+  wave_walk(st, qb, vt, src, kbeg, wk, ntiles, a.WK, lane);
+
+  // Cross-wave merge: waves wk > 0 of row block wr hand their state to wave wk == 0 through LDS.
+  if (a.WK > 1) {
+    __syncthreads();
+    if (wk > 0) state_to_lds(smem + (wr * (a.WK - 1) + wk - 1) * kSlotFloats, st, lane);
+    __syncthreads();
+    if (wk == 0)
+      for (int o = 1; o < a.WK; ++o) merge_from_lds(st, smem + (wr * (a.WK - 1) + o - 1) * kSlotFloats, lane);
+  }
+  if (wk == 0) {
+    const size_t rows_wg = 32 * a.WR;
+    float* po = a.part_o + ((size_t)item * rows_wg + wr * 32) * 128;
+    float* pml = a.part_ml + ((size_t)item * rows_wg + wr * 32) * 2;
+    store_partial(po, pml, st, lane, R - (rb * a.WR + wr) * 32);
+  }
+}
+
+// LSE merge of the nsplit partials of every query row; one workgroup (128 threads = head-dims) per row.
+__global__ __launch_bounds__(128) void spec_combine_kernel(SpecArgs a) {
+  const int R = a.kd * a.G;
+  const int rowg = blockIdx.x;                 // grp * R + row
+  const int grp = rowg / R, row = rowg % R;
+  const int rb = row / (32 * a.WR), rl = row % (32 * a.WR);
+  const int d = threadIdx.x;
+  const size_t rows_wg = 32 * a.WR;
+  const size_t item0 = (size_t)(grp * a.nrb + rb) * a.nsplit;
+  float M = kNegInf;
+  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[((item0 + s) * rows_wg + rl) * 2]);
+  const float Muse = (M == kNegInf) ? 0.f : M;
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < a.nsplit; ++s) {
+    const size_t base = (item0 + s) * rows_wg + rl;
+    const float w = fast_exp2(a.part_ml[base * 2] - Muse);
+    den += w * a.part_ml[base * 2 + 1];
+    num += w * a.part_o[base * 128 + d];
+  }
+  const int b = grp / a.Hkv, h = grp % a.Hkv;
+  const int i = row / a.G, gg = row % a.G;
+  a.out[((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128 + d] = (f16)(num / den);
+}
+
+struct SpecPlan {
+  int WR, WK, nrb, nsplit, chunk;
+  size_t po_floats, pml_floats;
+};
+
+static SpecPlan spec_plan(int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t L) {
+  SpecPlan p;
+  const int64_t G = Hq / Hkv, R = kd * G;
+  if (R <= 32) { p.WR = 1; p.WK = 4; }
+  else if (R <= 64) { p.WR = 2; p.WK = 2; }
+  else { p.WR = 4; p.WK = 1; }
+  const int64_t rows_wg = 32 * p.WR;
+  p.nrb = (int)((R + rows_wg - 1) / rows_wg);
+  const int64_t base = B * Hkv * p.nrb;
+  const int64_t max_split = (L + kTile * p.WK - 1) / (kTile * p.WK);
+  int64_t ns = (1024 + base - 1) / base;
+  // Keep the fp32 partials (rows * 130 floats per split) under ~8 % of the K/V stream.
+  const int64_t cap = std::max<int64_t>(1, (int64_t)(0.08 * (double)L / (double)(p.nrb * rows_wg)));
+  ns = std::max<int64_t>(1, std::min(ns, std::min(max_split, cap)));
+  int64_t chunk = (L + ns - 1) / ns;
+  chunk = (chunk + kTile - 1) / kTile * kTile;
+  p.chunk = (int)chunk;
+  p.nsplit = (int)((L + chunk - 1) / chunk);
+  const size_t items = (size_t)base * p.nsplit;
+  p.po_floats = items * rows_wg * 128;
+  p.pml_floats = items * rows_wg * 2;
+  return p;
+}
+
+}  // namespace vmk
+
+using namespace vmk;
+
+extern "C" size_t vmk_spec_workspace_size(int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L) {
+  if (B <= 0 || kd <= 0 || Hkv <= 0 || Hq % Hkv || D != 128 || L < kd) return 0;
+  SpecPlan p = spec_plan(B, kd, Hq, Hkv, L);
+  return (p.po_floats + p.pml_floats) * sizeof(float) + 256;
+}
+
+extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out,
+                               int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W,
+                               void* workspace, size_t ws_bytes, void* stream) {
+  VMK_CHECK(q && k && v && mask_words && out, "null pointer argument");
+  VMK_CHECK(B > 0 && kd > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/batch sizes");
+  VMK_CHECK(D == 128, "only head_dim 128 is supported");
+  VMK_CHECK(L >= kd, "L must count the kd drafts (L >= kd)");
+  VMK_CHECK(W == (kd + 31) / 32, "mask must hold ceil(kd/32) 32-bit words per draft");
+  VMK_CHECK((Hq / Hkv) * kd <= 1 << 20 && B * Hkv * L <= (int64_t)1 << 40, "sizes out of range");
+  VMK_CHECK(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "tensors must be 16-byte aligned");
+  const size_t need = vmk_spec_workspace_size(B, kd, Hq, Hkv, D, L);
+  VMK_CHECK(workspace && ws_bytes >= need, "workspace too small (query vmk_spec_workspace_size)");
+  SpecPlan p = spec_plan(B, kd, Hq, Hkv, L);
+  SpecArgs a;
+  a.q = (const f16*)q; a.k = (const f16*)k; a.v = (const f16*)v; a.bits = (const uint32_t*)mask_words;
+  a.out = (f16*)out;
+  a.part_o = (float*)align_up(workspace, 256);
+  a.part_ml = a.part_o + p.po_floats;
+  a.B = (int)B; a.kd = (int)kd; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = (int)W;
+  a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;
+  a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  const unsigned items = (unsigned)(B * Hkv * p.nrb * p.nsplit);
+  hipLaunchKernelGGL(spec_partial_kernel, dim3(items), dim3(64 * p.WR * p.WK), 0, s, a);
+  VMK_CHECK_HIP(hipGetLastError());
+  hipLaunchKernelGGL(spec_combine_kernel, dim3((unsigned)(B * Hkv * kd * (Hq / Hkv))), dim3(128), 0, s, a);
+  VMK_CHECK_HIP(hipGetLastError());
+  return 0;
+}

@@ -1,0 +1,66 @@
+"""ctypes binding of libvmk.so, the C-ABI declared in include/vmk.h.
+
+The library is loaded from this directory; there is no fallback: if it is missing or the GPU is not a gfx950, every
+entry point raises.  Pointers are raw device addresses (torch `data_ptr()`), streams are HIP stream handles.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvmk.so")
+
+_lib = None
+_c_vp, _c_i64, _c_sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
+
+# name -> argument types (return type int unless listed in _RET)
+_SIGS = {
+    "vmk_version": [],
+    "vmk_last_error": [],
+    "vmk_check_device": [],
+    "vmk_debug_mfma32": [_c_vp, _c_vp, _c_vp, _c_vp],
+    "vmk_spec_workspace_size": [_c_i64] * 6,
+    "vmk_spec_verify": [_c_vp] * 5 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
+    "vmk_prefix_workspace_size": [_c_i64] * 7,
+    "vmk_prefix_decode": [_c_vp] * 7 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_workspace_size": [_c_i64] * 2,
+    "vmk_dsa_indexer_select": [_c_vp] * 6 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_sparse_mla": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_decode": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+}
+_RET = {"vmk_last_error": ctypes.c_char_p, "vmk_spec_workspace_size": _c_sz, "vmk_prefix_workspace_size": _c_sz,
+        "vmk_dsa_workspace_size": _c_sz}
+
+
+class VmkError(RuntimeError):
+    pass
+
+
+def load():
+    """Loads libvmk.so once and declares every exported symbol; raises if the file or a symbol is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise VmkError(f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, args in _SIGS.items():
+        if not hasattr(lib, name):
+            continue
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RET.get(name, ctypes.c_int)
+    _lib = lib
+    return lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def check(rc):
+    if rc != 0:
+        raise VmkError(load().vmk_last_error().decode(errors="replace") or f"libvmk error {rc}")
+
+
+def call(name, *args):
+    check(getattr(load(), name)(*args))
