@@ -221,4 +221,31 @@ __device__ __forceinline__ void store_partial(float* po, float* pml, const RowSt
   }
 }
 
+// ---- one workgroup of WR x WK waves (WR * WK <= 4, 256 threads launched): WR row blocks of 32 rows, WK waves
+// interleaving the tiles of [kbeg, kbeg + 32*ntiles).  Writes one partial (O, m, l) for the WG's 32*WR rows to
+// po (row stride 128 floats) / pml; rows >= nrows are skipped.  smem must hold 3 * kSlotFloats floats.
+// qrow(row) returns an in-bounds Q row pointer for a WG-local row (clamped by the caller for rows >= nrows).
+template <class Src, class QRow>
+__device__ __forceinline__ void attend_wg(float* smem, const Src& src, QRow qrow, int nrows, int kbeg, int ntiles,
+                                          int WR, int WK, float* po, float* pml) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wr = wave % WR, wk = wave / WR;
+  const bool active = wave < WR * WK;
+  const int row = wr * 32 + (lane & 31);
+  half8 qb[8];
+  load_qt(qb, qrow(row < nrows ? row : 0), lane >> 5, row < nrows);
+  f16* vt = reinterpret_cast<f16*>(smem) + wave * kVTileHalfs;
+  RowState st;
+  row_state_init(st);
+  if (active) wave_walk(st, qb, vt, src, kbeg, wk, ntiles, WK, lane);
+  if (WK > 1) {
+    __syncthreads();
+    if (active && wk > 0) state_to_lds(smem + (wr * (WK - 1) + wk - 1) * kSlotFloats, st, lane);
+    __syncthreads();
+    if (active && wk == 0)
+      for (int o = 1; o < WK; ++o) merge_from_lds(st, smem + (wr * (WK - 1) + o - 1) * kSlotFloats, lane);
+  }
+  if (active && wk == 0) store_partial(po + (size_t)wr * 32 * 128, pml + wr * 32 * 2, st, lane, nrows - wr * 32);
+}
+
 }  // namespace vmk

@@ -1,0 +1,225 @@
+// Shared-prefix decode on gfx950 (cascade attention).
+//
+// Replaces the reference's shpfx_main (prefix and suffix block roles) and shpfx_combine Metal kernels
+// (kernels/prefix_opus55_v8.py:28-108, 109-208, 211-261) behind the kernel(q, kp, vp, ks, vs) contract of
+// ops/prefix.py:1-4, plus optional ragged suffix lengths.
+//
+// Launch 1 (one grid, two item kinds):
+//   prefix items (KV head h, row block, split): all N*G query rows of head h against a chunk of the shared prefix;
+//     the prefix tile is staged once per workgroup for up to 128 rows, so the prefix is streamed from HBM once per
+//     row block instead of once per request;
+//   suffix items (request n, KV head h, chunk): the G rows of request n against its own suffix rows.
+// Launch 2: per output row, log-sum-exp merge of the prefix partials of its KV head and its own suffix partials.
+#include "attn_core.h"
+#include "vmk_internal.h"
+
+namespace vmk {
+
+struct PrefixArgs {
+  const f16* q;            // (N, Hq, 128)
+  const f16* kp;           // (Hkv, P, 128)
+  const f16* vp;
+  const f16* ks;           // (N, Hkv, S, 128)
+  const f16* vs;
+  const int* slens;        // (N,) or null
+  f16* out;                // (N, Hq, 128)
+  float* po_p;             // prefix partials [h][rb][split][32*WRp][128]
+  float* pml_p;
+  float* po_s;             // suffix partials [n][h][split][32][128]
+  float* pml_s;
+  int N, Hq, Hkv, G, P, S;
+  int WRp, WKp, nrb_p, nsplit_p, chunk_p;   // prefix plan
+  int nsplit_s, chunk_s;                    // suffix plan (WR = 1, WK = 4)
+  int n_prefix_items;
+  float sl2;
+};
+
+struct RangeSrc {
+  const f16* kbase;
+  const f16* vbase;
+  int kend;
+  float sl2;
+  __device__ const f16* krow(int key) const { return kbase + (size_t)min(key, kend - 1) * 128; }
+  __device__ const f16* vrow(int key) const { return vbase + (size_t)min(key, kend - 1) * 128; }
+  __device__ bool valid(int key) const { return key < kend; }
+  __device__ void mask_scale(floatx16& s, int key0, int g) const {
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int key = key0 + 8 * blk + 4 * g + c;
+        s[4 * blk + c] = key < kend ? s[4 * blk + c] * sl2 : kNegInf;
+      }
+  }
+};
+
+// Suffix length of request n, clamped to [0, S] so that a bad length can never read past its own rows.
+__device__ __forceinline__ int suffix_len(const PrefixArgs& a, int n) {
+  return a.slens ? min(max(a.slens[n], 0), a.S) : a.S;
+}
+
+__global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
+  __shared__ __attribute__((aligned(16))) float smem[3 * kSlotFloats];
+  const int item = blockIdx.x;
+  RangeSrc src;
+  src.sl2 = a.sl2;
+  if (item < a.n_prefix_items) {
+    const int split = item % a.nsplit_p;
+    const int rb = (item / a.nsplit_p) % a.nrb_p;
+    const int h = item / (a.nsplit_p * a.nrb_p);
+    const size_t off = (size_t)h * a.P * 128;
+    src.kbase = a.kp + off;
+    src.vbase = a.vp + off;
+    const int kbeg = split * a.chunk_p;
+    src.kend = min(a.P, kbeg + a.chunk_p);
+    const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
+    const int row0 = rb * a.WRp * 32;
+    const size_t rows_wg = 32 * a.WRp;
+    attend_wg(smem, src,
+              [&](int r) {
+                const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
+                return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
+              },
+              a.N * a.G - row0, kbeg, ntiles, a.WRp, a.WKp, a.po_p + (size_t)item * rows_wg * 128,
+              a.pml_p + (size_t)item * rows_wg * 2);
+  } else {
+    const int sitem = item - a.n_prefix_items;
+    const int split = sitem % a.nsplit_s;
+    const int nh = sitem / a.nsplit_s;
+    const int n = nh / a.Hkv, h = nh % a.Hkv;
+    const int kbeg = split * a.chunk_s;
+    const int sn = suffix_len(a, n);
+    if (kbeg >= sn) return;                               // whole workgroup: nothing of this suffix is here
+    const size_t off = ((size_t)n * a.Hkv + h) * a.S * 128;
+    src.kbase = a.ks + off;
+    src.vbase = a.vs + off;
+    src.kend = min(sn, kbeg + a.chunk_s);
+    const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
+    attend_wg(smem, src, [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; }, a.G, kbeg, ntiles,
+              1, 4, a.po_s + (size_t)sitem * 32 * 128, a.pml_s + (size_t)sitem * 32 * 2);
+  }
+}
+
+// One workgroup (128 threads = head-dims) per output row (n, hq): merge the prefix splits of KV head h and the
+// suffix chunks of request n.
+__global__ __launch_bounds__(128) void prefix_combine_kernel(PrefixArgs a) {
+  const int rowg = blockIdx.x;                 // n * Hq + hq
+  const int n = rowg / a.Hq, hq = rowg % a.Hq;
+  const int h = hq / a.G, gg = hq % a.G;
+  const int d = threadIdx.x;
+  const int prow = n * a.G + gg;               // row of this output among the N*G rows of KV head h
+  const int rows_p = 32 * a.WRp;
+  const int rb = prow / rows_p, rl = prow % rows_p;
+  const size_t pitem0 = ((size_t)h * a.nrb_p + rb) * a.nsplit_p;
+  const int np = a.P > 0 ? a.nsplit_p : 0;
+  const int sn = suffix_len(a, n);
+  const int ns = (sn + a.chunk_s - 1) / a.chunk_s;
+  const size_t sitem0 = ((size_t)n * a.Hkv + h) * a.nsplit_s;
+  float M = kNegInf;
+  for (int s = 0; s < np; ++s) M = fmaxf(M, a.pml_p[((pitem0 + s) * rows_p + rl) * 2]);
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.pml_s[((sitem0 + s) * 32 + gg) * 2]);
+  const float Muse = (M == kNegInf) ? 0.f : M;
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < np; ++s) {
+    const size_t base = (pitem0 + s) * rows_p + rl;
+    const float w = fast_exp2(a.pml_p[base * 2] - Muse);
+    den += w * a.pml_p[base * 2 + 1];
+    num += w * a.po_p[base * 128 + d];
+  }
+  for (int s = 0; s < ns; ++s) {
+    const size_t base = (sitem0 + s) * 32 + gg;
+    const float w = fast_exp2(a.pml_s[base * 2] - Muse);
+    den += w * a.pml_s[base * 2 + 1];
+    num += w * a.po_s[base * 128 + d];
+  }
+  a.out[(size_t)rowg * 128 + d] = (f16)(num / den);
+}
+
+struct PrefixPlan {
+  int WRp, WKp, nrb_p, nsplit_p, chunk_p, nsplit_s, chunk_s;
+  size_t po_p, pml_p, po_s, pml_s;
+  int n_prefix_items, n_items;
+};
+
+static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int64_t S) {
+  PrefixPlan p;
+  const int64_t G = Hq / Hkv, R = N * G;
+  if (R <= 32) { p.WRp = 1; p.WKp = 4; }
+  else if (R <= 64) { p.WRp = 2; p.WKp = 2; }
+  else { p.WRp = 4; p.WKp = 1; }
+  const int64_t rows_wg = 32 * p.WRp;
+  p.nrb_p = (int)((R + rows_wg - 1) / rows_wg);
+  // Prefix chunks of ~1024 keys (fewer for small P so that short prefixes still spread over the GPU).
+  int64_t chunk = 1024;
+  if (P > 0) {
+    const int64_t want = std::max<int64_t>(1, 256 / std::max<int64_t>(1, Hkv * p.nrb_p));
+    chunk = std::min<int64_t>(chunk, (P + want - 1) / want);
+    chunk = std::max<int64_t>(chunk, kTile * p.WKp);
+    chunk = (chunk + kTile - 1) / kTile * kTile;
+  }
+  p.chunk_p = (int)chunk;
+  p.nsplit_p = P > 0 ? (int)((P + chunk - 1) / chunk) : 0;
+  p.n_prefix_items = (int)(Hkv * p.nrb_p * p.nsplit_p);
+  // Suffix chunks of 512 keys (4 waves x 4 tiles); rows are only the G heads of one request.
+  int64_t cs = 512;
+  if (S < cs) cs = std::max<int64_t>(kTile, (S + kTile - 1) / kTile * kTile);
+  p.chunk_s = (int)cs;
+  p.nsplit_s = (int)((S + cs - 1) / cs);
+  p.n_items = p.n_prefix_items + (int)(N * Hkv * p.nsplit_s);
+  p.po_p = (size_t)p.n_prefix_items * rows_wg * 128;
+  p.pml_p = (size_t)p.n_prefix_items * rows_wg * 2;
+  p.po_s = (size_t)N * Hkv * p.nsplit_s * 32 * 128;
+  p.pml_s = (size_t)N * Hkv * p.nsplit_s * 32 * 2;
+  return p;
+}
+
+}  // namespace vmk
+
+using namespace vmk;
+
+extern "C" size_t vmk_prefix_workspace_size(int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int64_t S,
+                                            int64_t ragged) {
+  (void)ragged;
+  if (N <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || D != 128 || P < 0 || S < 0 || P + S <= 0) return 0;
+  PrefixPlan p = prefix_plan(N, Hq, Hkv, P, S);
+  return (p.po_p + p.pml_p + p.po_s + p.pml_s) * sizeof(float) + 4 * 256;
+}
+
+extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, const void* ks, const void* vs,
+                                 const void* slens, void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D,
+                                 int64_t P, int64_t S, int64_t ragged, void* workspace, size_t ws_bytes,
+                                 void* stream) {
+  VMK_CHECK(q && out && (P == 0 || (kp && vp)) && (S == 0 || (ks && vs)), "null pointer argument");
+  VMK_CHECK(N > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/request sizes");
+  VMK_CHECK(D == 128, "only head_dim 128 is supported");
+  VMK_CHECK(Hq / Hkv <= 32, "at most 32 query heads per KV head");
+  VMK_CHECK(P >= 0 && S >= 0 && P + S > 0, "P and S must be >= 0 with P + S > 0");
+  VMK_CHECK(!ragged || slens, "ragged=1 needs slens");
+  VMK_CHECK(P < (1 << 30) && S < (1 << 30) && N * (Hq / Hkv) < (1 << 20), "sizes out of range");
+  VMK_CHECK(aligned16(q) && aligned16(out) && (P == 0 || (aligned16(kp) && aligned16(vp))) &&
+                (S == 0 || (aligned16(ks) && aligned16(vs))),
+            "tensors must be 16-byte aligned");
+  const size_t need = vmk_prefix_workspace_size(N, Hq, Hkv, D, P, S, ragged);
+  VMK_CHECK(workspace && ws_bytes >= need, "workspace too small (query vmk_prefix_workspace_size)");
+  PrefixPlan p = prefix_plan(N, Hq, Hkv, P, S);
+  PrefixArgs a;
+  a.q = (const f16*)q; a.kp = (const f16*)kp; a.vp = (const f16*)vp; a.ks = (const f16*)ks; a.vs = (const f16*)vs;
+  a.slens = ragged ? (const int*)slens : nullptr;
+  a.out = (f16*)out;
+  a.po_p = (float*)align_up(workspace, 256);
+  a.pml_p = (float*)align_up(a.po_p + p.po_p, 256);
+  a.po_s = (float*)align_up(a.pml_p + p.pml_p, 256);
+  a.pml_s = (float*)align_up(a.po_s + p.po_s, 256);
+  a.N = (int)N; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.P = (int)P; a.S = (int)S;
+  a.WRp = p.WRp; a.WKp = p.WKp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;
+  a.nsplit_s = p.nsplit_s; a.chunk_s = p.chunk_s; a.n_prefix_items = p.n_prefix_items;
+  a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  if (p.n_items > 0) {
+    hipLaunchKernelGGL(prefix_partial_kernel, dim3((unsigned)p.n_items), dim3(256), 0, s, a);
+    VMK_CHECK_HIP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(prefix_combine_kernel, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
+  VMK_CHECK_HIP(hipGetLastError());
+  return 0;
+}

@@ -52,22 +52,15 @@ struct SpecSrc {
 // One workgroup = WR x WK waves: WR row blocks of 32 rows, WK waves interleaving the key tiles of one split.
 __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   __shared__ __attribute__((aligned(16))) float smem[3 * kSlotFloats];   // >= 4 transposed V tiles
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wr = wave % a.WR, wk = wave / a.WR;
   const int item = blockIdx.x;
   const int split = item % a.nsplit;
   const int rb = (item / a.nsplit) % a.nrb;
   const int grp = item / (a.nsplit * a.nrb);
   const int b = grp / a.Hkv, h = grp % a.Hkv;
   const int R = a.kd * a.G;
-  const int r = lane & 31, g = lane >> 5;
-  const int row = (rb * a.WR + wr) * 32 + r;             // query row i*G + gg of this GQA group
-  const bool rvalid = row < R;
-  const int rowc = rvalid ? row : 0;
-  const int di = rowc / a.G, gg = rowc % a.G;
-
-  half8 qb[8];
-  load_qt(qb, a.q + ((size_t)(b * a.kd + di) * a.Hq + h * a.G + gg) * 128, g, rvalid);
+  const int row0 = rb * a.WR * 32;                        // first query row (i*G + gg) of this workgroup
+  const int lrow = row0 + (threadIdx.x & 31) + 32 * ((threadIdx.x >> 6) % a.WR);
+  const int di = (lrow < R ? lrow : 0) / a.G;
 
   SpecSrc src;
   const size_t kvoff = (size_t)grp * a.L * 128;
@@ -80,26 +73,14 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   src.kd = a.kd;
   src.sl2 = a.sl2;
   const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
-
-  f16* vt = reinterpret_cast<f16*>(smem) + wave * kVTileHalfs;
-  RowState st;
-  row_state_init(st);
-  wave_walk(st, qb, vt, src, kbeg, wk, ntiles, a.WK, lane);
-
-  // Cross-wave merge: waves wk > 0 of row block wr hand their state to wave wk == 0 through LDS.
-  if (a.WK > 1) {
-    __syncthreads();
-    if (wk > 0) state_to_lds(smem + (wr * (a.WK - 1) + wk - 1) * kSlotFloats, st, lane);
-    __syncthreads();
-    if (wk == 0)
-      for (int o = 1; o < a.WK; ++o) merge_from_lds(st, smem + (wr * (a.WK - 1) + o - 1) * kSlotFloats, lane);
-  }
-  if (wk == 0) {
-    const size_t rows_wg = 32 * a.WR;
-    float* po = a.part_o + ((size_t)item * rows_wg + wr * 32) * 128;
-    float* pml = a.part_ml + ((size_t)item * rows_wg + wr * 32) * 2;
-    store_partial(po, pml, st, lane, R - (rb * a.WR + wr) * 32);
-  }
+  const size_t rows_wg = 32 * a.WR;
+  attend_wg(smem, src,
+            [&](int r) {
+              const int qr = row0 + r, i = qr / a.G, gg = qr % a.G;
+              return a.q + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128;
+            },
+            R - row0, kbeg, ntiles, a.WR, a.WK, a.part_o + (size_t)item * rows_wg * 128,
+            a.part_ml + (size_t)item * rows_wg * 2);
 }
 
 // LSE merge of the nsplit partials of every query row; one workgroup (128 threads = head-dims) per row.
