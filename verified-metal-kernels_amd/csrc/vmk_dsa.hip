@@ -1,0 +1,497 @@
+// DeepSeek Sparse Attention decode on gfx950: indexer -> exact top-2048 -> sparse absorbed-MLA attention.
+//
+// Replaces the reference's dsa_indexer / dsa_select / dsa_qk / dsa_pv / dsa_red Metal kernels
+// (kernels/dsa_opus55_v7.py:27-98, 100-307, 309-535, 553-605, 629-727) behind the
+// kernel(q, kv, iq, ik, w, lens) contract of ops/dsa.py:1-9.
+//
+// Workspace layout:
+//   hist   : B x 8192 uint32   per-request histogram of the top 13 bits of the score key
+//   scores : B x L    float    indexer scores
+//   po/pml : attention partials [b][head block][chunk][32][512] and [..][32][2]
+#include "attn_core.h"
+#include "vmk_internal.h"
+
+namespace vmk {
+
+constexpr int kH = 128, kDK = 576, kDC = 512, kHI = 64, kDI = 128, kTopK = 2048;
+constexpr int kBins = 8192;        // first radix digit: key bits 31..19
+constexpr int kIdxWG = 1024;       // positions per indexer workgroup (8 waves x 4 tiles of 32)
+constexpr int kChunk = 128;        // selected keys per attention workgroup
+constexpr int kNChunk = kTopK / kChunk;
+constexpr int kCand = 4096;        // LDS candidate capacity of the select kernel
+
+struct DsaArgs {
+  const f16* q;         // (B, 128, 576)
+  const f16* kv;        // (B, L, 576)
+  const f16* iq;        // (B, 64, 128)
+  const f16* ik;        // (B, L, 128)
+  const float* w;       // (B, 64)
+  const int* lens;      // (B,) or null
+  int* idx;             // (B, 2048)
+  int* cnt;             // (B,)
+  f16* out;             // (B, 128, 512)
+  uint32_t* hist;       // (B, 8192)
+  float* scores;        // (B, L)
+  float* po;            // (B, 4, kNChunk, 32, 512)
+  float* pml;           // (B, 4, kNChunk, 32, 2)
+  int B, L;
+  float sl2;            // attention scale * log2(e)
+};
+
+// Order-preserving float -> uint32 map: a < b as floats  <=>  fkey(a) < fkey(b) (NaN above +inf).
+__device__ __forceinline__ uint32_t fkey(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ int valid_len(const DsaArgs& a, int b) {
+  return a.lens ? min(max(a.lens[b], 0), a.L) : a.L;
+}
+
+// ------------------------------------------------------------------------------------------------ indexer
+// S = iq . ik^T per 32-position tile (M = 64 heads as two 32-row MFMA tiles, N = positions, K = 128 dims), then
+// score = sum_h w[h] * max(S[h], 0) in fp32, and a histogram of fkey(score) >> 19 per request.
+__global__ __launch_bounds__(512) void dsa_indexer_kernel(DsaArgs a) {
+  __shared__ uint32_t hist[kBins];
+  const int b = blockIdx.y;
+  const int n = valid_len(a, b);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, g = lane >> 5;
+  for (int i = threadIdx.x; i < kBins; i += 512) hist[i] = 0;
+
+  half8 qa[2][8];
+  float wv[2][16];
+  const f16* iqb = a.iq + (size_t)b * kHI * kDI;
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht) {
+    load_qt(qa[ht], iqb + (ht * 32 + r) * kDI, g, true);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) wv[ht][i] = a.w[b * kHI + ht * 32 + 8 * (i >> 2) + 4 * g + (i & 3)];
+  }
+  __syncthreads();
+
+  const f16* ikb = a.ik + (size_t)b * a.L * kDI;
+  const int t0 = blockIdx.x * (kIdxWG / kTile) + wave * 4;     // this wave's 4 tiles
+  const int tend = min(t0 + 4, (n + kTile - 1) / kTile);
+  auto tile_ptr = [&](int t) { return ikb + (size_t)min(t * kTile + r, n - 1) * kDI; };
+  auto compute = [&](const u32x4 (&kr)[8], int t) {
+    floatx16 s0 = floatx16{}, s1 = floatx16{};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      s0 = mfma32(qa[0][s], as_h8(kr[s]), s0);
+      s1 = mfma32(qa[1][s], as_h8(kr[s]), s1);
+    }
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) part += wv[0][i] * fmaxf(s0[i], 0.f) + wv[1][i] * fmaxf(s1[i], 0.f);
+    const float tot = part + xor32(part);
+    const int pos = t * kTile + r;
+    if (g == 0 && pos < n) {
+      a.scores[(size_t)b * a.L + pos] = tot;
+      atomicAdd(&hist[fkey(tot) >> 19], 1u);
+    }
+  };
+  if (t0 < tend) {
+    u32x4 kA[8], kB[8];
+    load_k(kA, tile_ptr(t0), g);
+    int t = t0;
+    while (true) {
+      if (t + 1 < tend) load_k(kB, tile_ptr(t + 1), g);
+      compute(kA, t);
+      if (++t >= tend) break;
+      if (t + 1 < tend) load_k(kA, tile_ptr(t + 1), g);
+      compute(kB, t);
+      if (++t >= tend) break;
+    }
+  }
+  __syncthreads();
+  uint32_t* gh = a.hist + (size_t)b * kBins;
+  for (int i = threadIdx.x; i < kBins; i += 512) {
+    const uint32_t c = hist[i];
+    if (c) atomicAdd(&gh[i], c);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ select
+// Exact top-2048 per request, one 1024-thread workgroup per request.  Radix digits of the score key: bits 31..19
+// (histogram from the indexer), 18..8 and 7..0 (LDS histograms over the candidates of the threshold bucket).
+// Compaction uses block scans over thread-contiguous position ranges, so the output order (selected positions
+// above the threshold bucket in increasing order, then the bucket's picks in increasing order, ties broken by
+// position) does not depend on scheduling, and neither do the attention sums that follow.
+
+// Block-wide (1024 threads) exclusive prefix sum of v over thread ids; *total receives the sum of all v.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;  // inclusive prefix within the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) red[wave] = x;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+  for (int w2 = 0; w2 < 16; ++w2) {
+    const uint32_t t = red[w2];
+    all += t;
+    if (w2 < wave) before += t;
+  }
+  __syncthreads();
+  *total = all;
+  return before + x - v;
+}
+
+struct SelectShared {
+  uint32_t hist[kBins];
+  uint32_t cand_key[kCand];
+  int cand_pos[kCand];
+  uint32_t red[16];
+  uint32_t thr_bin, thr_need;
+};
+
+// Finds, in hist[0..nbins) (nbins a multiple of 1024), the bin holding the need-th largest element: thr_bin, and
+// thr_need = need minus the count strictly above that bin.  Every thread of the block must call it.
+__device__ void find_threshold(SelectShared& sh, int nbins, uint32_t need) {
+  const int per = nbins / 1024;
+  const int lo = (1023 - threadIdx.x) * per;        // thread 0 owns the highest bins: a prefix scan runs top-down
+  uint32_t local = 0;
+  for (int i = 0; i < per; ++i) local += sh.hist[lo + i];
+  uint32_t total;
+  const uint32_t above = block_excl_scan(local, sh.red, &total);
+  if (above < need && above + local >= need) {
+    uint32_t acc = above;
+    for (int i = per - 1; i >= 0; --i) {
+      const uint32_t c = sh.hist[lo + i];
+      if (acc + c >= need) {
+        sh.thr_bin = lo + i;
+        sh.thr_need = need - acc;
+        break;
+      }
+      acc += c;
+    }
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void dsa_select_kernel(DsaArgs a) {
+  __shared__ SelectShared sh;
+  const int b = blockIdx.x;
+  const int n = valid_len(a, b);
+  const int tid = threadIdx.x;
+  int* idx = a.idx + (size_t)b * kTopK;
+  if (n <= kTopK) {
+    for (int i = tid; i < kTopK; i += 1024) idx[i] = i < n ? i : 0;
+    if (tid == 0) a.cnt[b] = n;
+    return;
+  }
+  const uint32_t* gh = a.hist + (size_t)b * kBins;
+  for (int i = tid; i < kBins; i += 1024) sh.hist[i] = gh[i];
+  __syncthreads();
+  find_threshold(sh, kBins, kTopK);
+  const uint32_t b1 = sh.thr_bin;
+  uint32_t need = sh.thr_need;
+  const float* sc = a.scores + (size_t)b * a.L;
+  const int per = (n + 1023) / 1024;                 // thread-contiguous position ranges
+  const int p_lo = min(n, tid * per), p_hi = min(n, p_lo + per);
+  uint32_t c_gt = 0, c_eq = 0, tot;
+  for (int p = p_lo; p < p_hi; ++p) {
+    const uint32_t bin = fkey(sc[p]) >> 19;
+    c_gt += bin > b1;
+    c_eq += bin == b1;
+  }
+  uint32_t o_gt = block_excl_scan(c_gt, sh.red, &tot);
+  uint32_t o_eq = block_excl_scan(c_eq, sh.red, &tot);
+  const uint32_t n_gt = kTopK - need;                // elements above the bucket, all selected
+  const uint32_t ncand = tot;
+  const bool in_lds = ncand <= (uint32_t)kCand;
+  for (int p = p_lo; p < p_hi; ++p) {
+    const uint32_t key = fkey(sc[p]);
+    const uint32_t bin = key >> 19;
+    if (bin > b1) {
+      if (o_gt < n_gt) idx[o_gt] = p;
+      ++o_gt;
+    }
+    else if (bin == b1 && in_lds) { sh.cand_key[o_eq] = key; sh.cand_pos[o_eq] = p; ++o_eq; }
+  }
+  // Candidate ranges: in LDS, or (too many ties for LDS) the scores again, filtered to the bucket.
+  const int cper = in_lds ? (int)((ncand + 1023) / 1024) : per;
+  const int c_lo = in_lds ? min((int)ncand, tid * cper) : p_lo;
+  const int c_hi = in_lds ? min((int)ncand, c_lo + cper) : p_hi;
+  auto for_each = [&](auto&& f) {
+    for (int i = c_lo; i < c_hi; ++i) {
+      if (in_lds) {
+        f(sh.cand_key[i], sh.cand_pos[i]);
+      } else {
+        const uint32_t key = fkey(sc[i]);
+        if ((key >> 19) == b1) f(key, i);
+      }
+    }
+  };
+  __syncthreads();
+  for (int i = tid; i < 2048; i += 1024) sh.hist[i] = 0;
+  __syncthreads();
+  for_each([&](uint32_t key, int) { atomicAdd(&sh.hist[(key >> 8) & 0x7FF], 1u); });
+  __syncthreads();
+  find_threshold(sh, 2048, need);
+  const uint32_t b2 = sh.thr_bin;
+  need = sh.thr_need;
+  sh.hist[tid] = 0;
+  __syncthreads();
+  for_each([&](uint32_t key, int) {
+    if (((key >> 8) & 0x7FF) == b2) atomicAdd(&sh.hist[key & 0xFF], 1u);
+  });
+  __syncthreads();
+  find_threshold(sh, 1024, need);
+  const uint32_t T = (b1 << 19) | (b2 << 8) | sh.thr_bin;
+  const uint32_t need_eq = sh.thr_need;
+  // Bucket picks: keys above T, then the first need_eq keys equal to T in position order.
+  uint32_t c_above = 0, c_tie = 0, above_total, tie_total;
+  for_each([&](uint32_t key, int) { c_above += key > T; c_tie += key == T; });
+  uint32_t o_above = block_excl_scan(c_above, sh.red, &above_total);
+  uint32_t o_tie = block_excl_scan(c_tie, sh.red, &tie_total);
+  // Slots: [0, n_gt) above the bucket, then the bucket's keys > T, then need_eq ties.  The guards only matter if
+  // the histogram disagreed with the scores; they keep every write inside this request's 2048 slots.
+  for_each([&](uint32_t key, int p) {
+    if (key > T) {
+      const uint32_t slot = n_gt + o_above++;
+      if (slot < (uint32_t)kTopK) idx[slot] = p;
+    } else if (key == T) {
+      const uint32_t slot = n_gt + above_total + o_tie;
+      if (o_tie < need_eq && slot < (uint32_t)kTopK) idx[slot] = p;
+      ++o_tie;
+    }
+  });
+  if (tid == 0) a.cnt[b] = kTopK;
+}
+
+// Zero-fills the per-request histograms before the indexer accumulates into them.
+__global__ __launch_bounds__(1024) void dsa_hist_zero_kernel(DsaArgs a) {
+  uint32_t* gh = a.hist + (size_t)blockIdx.x * kBins;
+  for (int i = threadIdx.x; i < kBins; i += 1024) gh[i] = 0;
+}
+
+// ------------------------------------------------------------------------------------------------ sparse MLA
+// Workgroup = (request b, block of 32 heads, chunk of 128 selected keys); 4 waves.  Wave w owns the QK head-dims
+// [128w, 128w+128) u [512+16w, 512+16w+16) and the value dims [128w, 128w+128): partial S^T tiles are summed
+// through LDS in a fixed order so every wave holds bit-identical scores, softmax state and P.
+constexpr int kSSlot = 16 * 64;    // floats of one wave's partial S^T tile
+
+__global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
+  __shared__ __attribute__((aligned(16))) f16 vts[4 * kVTileHalfs];
+  __shared__ __attribute__((aligned(16))) float sx[2][4 * kSSlot];
+  const int item = blockIdx.x;                  // (b * 4 + hb) * kNChunk + chunk
+  const int chunk = item % kNChunk;
+  const int hb = (item / kNChunk) % 4;
+  const int b = item / (kNChunk * 4);
+  const int cnt = min(a.cnt[b], kTopK);
+  const int kbeg = chunk * kChunk;
+  if (kbeg >= cnt) return;                      // whole workgroup
+  const int kend = min(cnt, kbeg + kChunk);
+  const int ntiles = (kend - kbeg + kTile - 1) / kTile;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 31, g = lane >> 5, dc = lane & 15, kg = lane >> 4;
+
+  const f16* qrow = a.q + ((size_t)b * kH + hb * 32 + r) * kDK;
+  half8 qb[9];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) qb[s] = as_h8(ld16(qrow + 128 * w + 64 * g + 8 * s));
+  qb[8] = as_h8(ld16(qrow + kDC + 16 * w + 8 * g));
+
+  const f16* kvb = a.kv + (size_t)b * a.L * kDK;
+  const int* ip = a.idx + (size_t)b * kTopK;
+  auto row_of = [&](int key) {
+    const int p = ip[min(key, kend - 1)];
+    return kvb + (size_t)min(max(p, 0), a.L - 1) * kDK;
+  };
+  auto issue = [&](u32x4 (&kr)[9], u32x4 (&vr)[8], int t) {
+    const int key0 = kbeg + t * kTile;
+    const f16* kp = row_of(key0 + r);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) kr[s] = ld16(kp + 128 * w + 64 * g + 8 * s);
+    kr[8] = ld16(kp + kDC + 16 * w + 8 * g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = key0 + kg * 8 + j;
+      vr[j] = sel16(key < kend, ld16(row_of(key) + 128 * w + 8 * dc));
+    }
+  };
+  f16* vt = vts + w * kVTileHalfs;
+  RowState st;
+  row_state_init(st);
+  auto compute = [&](const u32x4 (&kr)[9], const u32x4 (&vr)[8], int t, int buf) {
+    store_vt(vt, vr, dc, kg);
+    floatx16 sp = floatx16{};
+#pragma unroll
+    for (int s = 0; s < 9; ++s) sp = mfma32(as_h8(kr[s]), qb[s], sp);
+    float* slot = sx[buf];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) slot[w * kSSlot + i * 64 + lane] = sp[i];
+    __syncthreads();
+    floatx16 s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      s[i] = ((slot[i * 64 + lane] + slot[kSSlot + i * 64 + lane]) + slot[2 * kSSlot + i * 64 + lane]) +
+             slot[3 * kSSlot + i * 64 + lane];
+    const int key0 = kbeg + t * kTile;
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int key = key0 + 8 * blk + 4 * g + c;
+        s[4 * blk + c] = key < kend ? s[4 * blk + c] * a.sl2 : kNegInf;
+      }
+    half8 pb[2];
+    softmax_update(st, s, pb);
+    pv_tile(st, vt, pb, lane);
+  };
+  {
+    u32x4 kA[9], vA[8], kB[9], vB[8];
+    issue(kA, vA, 0);
+    int t = 0;
+    while (true) {
+      if (t + 1 < ntiles) issue(kB, vB, t + 1);
+      compute(kA, vA, t, t & 1);
+      if (++t >= ntiles) break;
+      if (t + 1 < ntiles) issue(kA, vA, t + 1);
+      compute(kB, vB, t, t & 1);
+      if (++t >= ntiles) break;
+    }
+  }
+  // Partial: O[head][128w + d'] for this wave's value dims; m and l are identical in all waves.
+  float* po = a.po + (size_t)item * 32 * kDC;
+  const float ltot = st.l + xor32(st.l);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      floatx4 v = floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]};
+      *reinterpret_cast<floatx4*>(po + r * kDC + 128 * w + dt * 32 + 8 * blk + 4 * g) = v;
+    }
+  if (w == 0 && g == 0) {
+    a.pml[((size_t)item * 32 + r) * 2] = st.m;
+    a.pml[((size_t)item * 32 + r) * 2 + 1] = ltot;
+  }
+}
+
+// One workgroup (256 threads, 2 value dims each) per (b, head): LSE merge over the chunks.
+__global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
+  const int bh = blockIdx.x;
+  const int b = bh / kH, head = bh % kH, hb = head / 32, hr = head % 32;
+  const int cnt = min(a.cnt[b], kTopK);
+  const int nch = (cnt + kChunk - 1) / kChunk;
+  const size_t item0 = ((size_t)b * 4 + hb) * kNChunk;
+  float M = kNegInf;
+  for (int c = 0; c < nch; ++c) M = fmaxf(M, a.pml[((item0 + c) * 32 + hr) * 2]);
+  const float Muse = (M == kNegInf) ? 0.f : M;
+  float n0 = 0.f, n1 = 0.f, den = 0.f;
+  const int d = threadIdx.x;
+  for (int c = 0; c < nch; ++c) {
+    const size_t base = (item0 + c) * 32 + hr;
+    const float wgt = fast_exp2(a.pml[base * 2] - Muse);
+    den += wgt * a.pml[base * 2 + 1];
+    n0 += wgt * a.po[base * kDC + d];
+    n1 += wgt * a.po[base * kDC + d + 256];
+  }
+  f16* o = a.out + (size_t)bh * kDC;
+  o[d] = (f16)(n0 / den);
+  o[d + 256] = (f16)(n1 / den);
+}
+
+struct DsaLayout {
+  size_t hist, scores, po, pml, total;
+};
+
+static DsaLayout dsa_layout(int64_t B, int64_t L) {
+  DsaLayout l;
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  l.hist = 0;
+  l.scores = up(l.hist + (size_t)B * kBins * 4);
+  l.po = up(l.scores + (size_t)B * L * 4);
+  l.pml = up(l.po + (size_t)B * 4 * kNChunk * 32 * kDC * 4);
+  l.total = up(l.pml + (size_t)B * 4 * kNChunk * 32 * 2 * 4) + 256;
+  return l;
+}
+
+static int dsa_fill_args(DsaArgs& a, const void* q, const void* kv, const void* iq, const void* ik, const void* w,
+                         const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L, void* ws) {
+  const DsaLayout lay = dsa_layout(B, L);
+  char* base = (char*)align_up(ws, 256);
+  a.q = (const f16*)q; a.kv = (const f16*)kv; a.iq = (const f16*)iq; a.ik = (const f16*)ik; a.w = (const float*)w;
+  a.lens = (const int*)lens; a.out = (f16*)out; a.idx = (int*)idx; a.cnt = (int*)cnt;
+  a.hist = (uint32_t*)(base + lay.hist);
+  a.scores = (float*)(base + lay.scores);
+  a.po = (float*)(base + lay.po);
+  a.pml = (float*)(base + lay.pml);
+  a.B = (int)B; a.L = (int)L;
+  a.sl2 = (float)(1.0 / sqrt(192.0)) * kLog2e;
+  return 0;
+}
+
+static int launch_index_select(const DsaArgs& a, hipStream_t s) {
+  if (a.L > kTopK) {
+    hipLaunchKernelGGL(dsa_hist_zero_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
+    VMK_CHECK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(dsa_indexer_kernel, dim3((unsigned)((a.L + kIdxWG - 1) / kIdxWG), (unsigned)a.B), dim3(512),
+                       0, s, a);
+    VMK_CHECK_HIP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(dsa_select_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
+  VMK_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
+static int launch_attention(const DsaArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(dsa_attn_kernel, dim3((unsigned)(a.B * 4 * kNChunk)), dim3(256), 0, s, a);
+  VMK_CHECK_HIP(hipGetLastError());
+  hipLaunchKernelGGL(dsa_combine_kernel, dim3((unsigned)(a.B * kH)), dim3(256), 0, s, a);
+  VMK_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // namespace vmk
+
+using namespace vmk;
+
+extern "C" size_t vmk_dsa_workspace_size(int64_t B, int64_t L) {
+  if (B <= 0 || L <= 0) return 0;
+  return dsa_layout(B, L).total;
+}
+
+#define DSA_COMMON_CHECKS()                                                                    \
+  VMK_CHECK(B > 0 && L > 0 && L < (1 << 30) && B < (1 << 20), "bad B or L");                  \
+  VMK_CHECK(workspace && ws_bytes >= vmk_dsa_workspace_size(B, L),                             \
+            "workspace too small (query vmk_dsa_workspace_size)")
+
+extern "C" int vmk_dsa_indexer_select(const void* iq, const void* ik, const void* w, const void* lens, void* idx,
+                                      void* cnt, int64_t B, int64_t L, void* workspace, size_t ws_bytes,
+                                      void* stream) {
+  VMK_CHECK(iq && ik && w && idx && cnt, "null pointer argument");
+  DSA_COMMON_CHECKS();
+  VMK_CHECK(aligned16(iq) && aligned16(ik), "iq/ik must be 16-byte aligned");
+  DsaArgs a;
+  dsa_fill_args(a, nullptr, nullptr, iq, ik, w, lens, nullptr, idx, cnt, B, L, workspace);
+  return launch_index_select(a, (hipStream_t)stream);
+}
+
+extern "C" int vmk_dsa_sparse_mla(const void* q, const void* kv, const void* idx, const void* cnt, void* out,
+                                  int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream) {
+  VMK_CHECK(q && kv && idx && cnt && out, "null pointer argument");
+  DSA_COMMON_CHECKS();
+  VMK_CHECK(aligned16(q) && aligned16(kv), "q/kv must be 16-byte aligned");
+  DsaArgs a;
+  dsa_fill_args(a, q, kv, nullptr, nullptr, nullptr, nullptr, out, (void*)idx, (void*)cnt, B, L, workspace);
+  return launch_attention(a, (hipStream_t)stream);
+}
+
+extern "C" int vmk_dsa_decode(const void* q, const void* kv, const void* iq, const void* ik, const void* w,
+                              const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L,
+                              void* workspace, size_t ws_bytes, void* stream) {
+  VMK_CHECK(q && kv && iq && ik && w && out && idx && cnt, "null pointer argument");
+  DSA_COMMON_CHECKS();
+  VMK_CHECK(aligned16(q) && aligned16(kv) && aligned16(iq) && aligned16(ik), "tensors must be 16-byte aligned");
+  DsaArgs a;
+  dsa_fill_args(a, q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace);
+  hipStream_t s = (hipStream_t)stream;
+  if (int rc = launch_index_select(a, s)) return rc;
+  return launch_attention(a, s);
+}
