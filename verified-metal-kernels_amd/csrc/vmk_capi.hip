@@ -17,6 +17,32 @@ void set_error(const char* fmt, ...) {
 
 extern "C" const char* vmk_last_error(void) { return vmk::g_err; }
 
+// Measurement hook: the next launch of kernel `kernel_id` (vmk::KernelId) on this host thread is bracketed by
+// hipEventRecord(before) / hipEventRecord(after) on the stream it is launched on; the request is then cleared.
+namespace vmk {
+static thread_local hipEvent_t g_prof_before = nullptr, g_prof_after = nullptr;
+static thread_local int g_prof_kernel = -1;
+
+void prof_before(int kernel_id, hipStream_t s) {
+  if (g_prof_kernel == kernel_id && g_prof_before) (void)hipEventRecord(g_prof_before, s);
+}
+
+void prof_after(int kernel_id, hipStream_t s) {
+  if (g_prof_kernel == kernel_id && g_prof_after) {
+    (void)hipEventRecord(g_prof_after, s);
+    g_prof_kernel = -1;
+    g_prof_before = g_prof_after = nullptr;
+  }
+}
+}  // namespace vmk
+
+extern "C" int vmk_profile_next(void* before, void* after, int kernel_id) {
+  vmk::g_prof_before = (hipEvent_t)before;
+  vmk::g_prof_after = (hipEvent_t)after;
+  vmk::g_prof_kernel = kernel_id;
+  return 0;
+}
+
 extern "C" int vmk_version(void) { return 1; }
 
 // Architecture check: 0 when the current device is gfx950, 1 otherwise (message in vmk_last_error).

@@ -431,19 +431,27 @@ static int launch_index_select(const DsaArgs& a, hipStream_t s) {
   if (a.L > kTopK) {
     hipLaunchKernelGGL(dsa_hist_zero_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
     VMK_CHECK_HIP(hipGetLastError());
+    prof_before(kKDsaIndexer, s);
     hipLaunchKernelGGL(dsa_indexer_kernel, dim3((unsigned)((a.L + kIdxWG - 1) / kIdxWG), (unsigned)a.B), dim3(512),
                        0, s, a);
+    prof_after(kKDsaIndexer, s);
     VMK_CHECK_HIP(hipGetLastError());
   }
+  prof_before(kKDsaSelect, s);
   hipLaunchKernelGGL(dsa_select_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
+  prof_after(kKDsaSelect, s);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
 }
 
 static int launch_attention(const DsaArgs& a, hipStream_t s) {
+  prof_before(kKDsaAttn, s);
   hipLaunchKernelGGL(dsa_attn_kernel, dim3((unsigned)(a.B * 4 * kNChunk)), dim3(256), 0, s, a);
+  prof_after(kKDsaAttn, s);
   VMK_CHECK_HIP(hipGetLastError());
+  prof_before(kKDsaCombine, s);
   hipLaunchKernelGGL(dsa_combine_kernel, dim3((unsigned)(a.B * kH)), dim3(256), 0, s, a);
+  prof_after(kKDsaCombine, s);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
 }

@@ -6,6 +6,14 @@
 
 namespace vmk {
 void set_error(const char* fmt, ...);
+
+// Kernel ids of the measurement hook (vmk_profile_next).
+enum KernelId {
+  kKSpecPartial = 0, kKSpecCombine = 1, kKPrefixPartial = 2, kKPrefixCombine = 3,
+  kKDsaIndexer = 4, kKDsaSelect = 5, kKDsaAttn = 6, kKDsaCombine = 7,
+};
+void prof_before(int kernel_id, hipStream_t s);
+void prof_after(int kernel_id, hipStream_t s);
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline void* align_up(void* p, size_t a) { return (void*)(((uintptr_t)p + a - 1) & ~(uintptr_t)(a - 1)); }
 }  // namespace vmk

@@ -216,10 +216,14 @@ extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, 
   a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   if (p.n_items > 0) {
+    prof_before(kKPrefixPartial, s);
     hipLaunchKernelGGL(prefix_partial_kernel, dim3((unsigned)p.n_items), dim3(256), 0, s, a);
+    prof_after(kKPrefixPartial, s);
     VMK_CHECK_HIP(hipGetLastError());
   }
+  prof_before(kKPrefixCombine, s);
   hipLaunchKernelGGL(prefix_combine_kernel, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
+  prof_after(kKPrefixCombine, s);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
 }

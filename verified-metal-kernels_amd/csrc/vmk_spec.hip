@@ -169,9 +169,13 @@ extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, cons
   a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   const unsigned items = (unsigned)(B * Hkv * p.nrb * p.nsplit);
+  prof_before(kKSpecPartial, s);
   hipLaunchKernelGGL(spec_partial_kernel, dim3(items), dim3(64 * p.WR * p.WK), 0, s, a);
+  prof_after(kKSpecPartial, s);
   VMK_CHECK_HIP(hipGetLastError());
+  prof_before(kKSpecCombine, s);
   hipLaunchKernelGGL(spec_combine_kernel, dim3((unsigned)(B * Hkv * kd * (Hq / Hkv))), dim3(128), 0, s, a);
+  prof_after(kKSpecCombine, s);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
 }

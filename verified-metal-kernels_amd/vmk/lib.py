@@ -18,6 +18,7 @@ _SIGS = {
     "vmk_last_error": [],
     "vmk_check_device": [],
     "vmk_debug_mfma32": [_c_vp, _c_vp, _c_vp, _c_vp],
+    "vmk_profile_next": [_c_vp, _c_vp, ctypes.c_int],
     "vmk_spec_workspace_size": [_c_i64] * 6,
     "vmk_spec_verify": [_c_vp] * 5 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
     "vmk_prefix_workspace_size": [_c_i64] * 7,
@@ -51,6 +52,11 @@ def load():
         fn.restype = _RET.get(name, ctypes.c_int)
     _lib = lib
     return lib
+
+
+# Kernel ids of vmk_profile_next (include/vmk.h).
+KERNEL_IDS = {"spec_partial": 0, "spec_combine": 1, "prefix_partial": 2, "prefix_combine": 3,
+              "dsa_indexer": 4, "dsa_select": 5, "dsa_attn": 6, "dsa_combine": 7}
 
 
 def exported_symbols():
