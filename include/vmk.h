@@ -1,0 +1,108 @@
+/* libvmk: MI355X (gfx950) kernels for shared-prefix decode, speculative chain/tree verification and DeepSeek Sparse
+ * Attention decode, behind a plain C ABI (raw device pointers, sizes, a caller-provided workspace and a HIP stream).
+ *
+ * Conventions shared by every entry point:
+ *   - tensors are dense row-major device buffers, 16-byte aligned; fp16 unless stated otherwise;
+ *   - inputs are never written; outputs are fully overwritten;
+ *   - `stream` is a hipStream_t (NULL = default stream); the call only enqueues work and returns;
+ *   - `workspace` is device memory of at least the size returned by the matching *_workspace_size query; its
+ *     contents need no initialisation and are garbage afterwards; two calls sharing one workspace must be ordered;
+ *   - return 0 on success; 1 = rejected arguments (nothing launched), 2 = HIP launch/runtime error; the message of
+ *     the last failure on this host thread is returned by vmk_last_error().
+ *
+ * Each entry point replaces the `kernel(**inputs)` function of one of the reference's kernel modules, called with
+ * the keyword inputs listed in verify.py:35-37; the Python modules verified-metal-kernels_amd/kernels/*_mi355x.py
+ * keep that signature and call into this ABI.
+ */
+#ifndef VMK_H
+#define VMK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version (1). */
+int vmk_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* vmk_last_error(void);
+
+/* 0 when the current HIP device is a gfx950 (the only architecture this library is built for), else 1. */
+int vmk_check_device(void);
+
+/* ---------------------------------------------------------------------------------------------- speculative verify
+ * Replaces kernel(q, k, v, bits) of kernels/spec_opus55_v7.py:467-521 (op contract ops/spec.py:1-3, 59-82).
+ *   q          (B, kd, Hq, D)        fp16    draft queries
+ *   k, v       (B, Hkv, L, D)        fp16    cache; the last kd positions are the drafts themselves
+ *   mask_words (B, kd, W)            uint32  W = ceil(kd/32); bit j%32 of word j/32 of draft i: i may attend draft j
+ *                                            (the reference's (B, kd) int32 `bits` is the W = 1 case)
+ *   out        (B, kd, Hq, D)        fp16
+ * D must be 128, Hq a multiple of Hkv, L >= kd.  Context positions (< L-kd) are visible to every draft. */
+size_t vmk_spec_workspace_size(int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L);
+int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
+                    int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, void* workspace,
+                    size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------- shared-prefix decode
+ * Replaces kernel(q, kp, vp, ks, vs) of kernels/prefix_opus55_v8.py:282-355 (op contract ops/prefix.py:1-4, 57-70).
+ *   q       (N, Hq, D)        fp16   one decode token per request
+ *   kp, vp  (Hkv, P, D)       fp16   shared prefix (may be NULL when P == 0)
+ *   ks, vs  (N, Hkv, S, D)    fp16   per-request suffixes, padded to S rows (may be NULL when S == 0)
+ *   slens   (N,)              int32  rows of each suffix in use when ragged != 0 (clamped to [0, S]); else unused
+ *   out     (N, Hq, D)        fp16
+ * D must be 128, Hq a multiple of Hkv with at most 32 query heads per KV head. */
+size_t vmk_prefix_workspace_size(int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int64_t S,
+                                 int64_t ragged);
+int vmk_prefix_decode(const void* q, const void* kp, const void* vp, const void* ks, const void* vs,
+                      const void* slens, void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t P,
+                      int64_t S, int64_t ragged, void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------- DSA decode
+ * Replaces kernel(q, kv, iq, ik, w, lens) of kernels/dsa_opus55_v7.py:946-977 (op contract ops/dsa.py:1-9, 53-83).
+ *   q     (B, 128, 576)  fp16    absorbed queries (512 latent + 64 rope)
+ *   kv    (B, L, 576)    fp16    latent cache; the value is the first 512 dims of the same row
+ *   iq    (B, 64, 128)   fp16    indexer queries
+ *   ik    (B, L, 128)    fp16    indexer keys
+ *   w     (B, 64)        fp32    indexer head weights
+ *   lens  (B,)           int32   valid positions per request, or NULL for all L
+ *   idx   (B, 2048)      int32   selected positions; entries [0, cnt[b]) are valid (out for the select entries,
+ *                                in for vmk_dsa_sparse_mla).  Order: positions above the threshold bucket in increasing
+ *                                order, then the bucket's picks in increasing order; ties at the threshold are taken in
+ *                                increasing position order.  With n <= 2048 valid positions, idx = 0..n-1.
+ *   cnt   (B,)           int32   min(n, 2048)
+ *   out   (B, 128, 512)  fp16
+ * score[l] = sum_h w[h] * max(iq[h] . ik[l], 0) in fp32; attention scale 1/sqrt(192). */
+size_t vmk_dsa_workspace_size(int64_t B, int64_t L);
+/* Indexer + exact top-2048 only (the reference's indexer_mpp/indexer_float + select, dsa_opus55_v7.py:963-973). */
+int vmk_dsa_indexer_select(const void* iq, const void* ik, const void* w, const void* lens, void* idx, void* cnt,
+                           int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream);
+/* Sparse absorbed-MLA attention over given indices (the reference's attn_mpp/attn_float, dsa_opus55_v7.py:975). */
+int vmk_dsa_sparse_mla(const void* q, const void* kv, const void* idx, const void* cnt, void* out, int64_t B,
+                       int64_t L, void* workspace, size_t ws_bytes, void* stream);
+/* The whole decode step: vmk_dsa_indexer_select followed by vmk_dsa_sparse_mla (idx/cnt are written). */
+int vmk_dsa_decode(const void* q, const void* kv, const void* iq, const void* ik, const void* w, const void* lens,
+                   void* out, void* idx, void* cnt, int64_t B, int64_t L, void* workspace, size_t ws_bytes,
+                   void* stream);
+
+/* ---------------------------------------------------------------------------------------------- measurement hook
+ * No reference counterpart (the reference times whole calls only, bench.py:61-96).  The next launch of kernel
+ * `kernel_id` on this host thread is bracketed by hipEventRecord(before) and hipEventRecord(after) on its stream.
+ * Ids: 0 spec_partial, 1 spec_combine, 2 prefix_partial, 3 prefix_combine, 4 dsa_indexer, 5 dsa_select,
+ *      6 dsa_attn, 7 dsa_combine. */
+int vmk_profile_next(void* before_event, void* after_event, int kernel_id);
+
+/* ---------------------------------------------------------------------------------------------- test hooks
+ * No reference counterpart.  Lane-layout check of the 32x32x16 fp16 MFMA (a, b: 64 lanes x 8 fp16; d: 64 x 16 fp32),
+ * and a stage dump of the attention wave pipeline for one 32-key tile (q, k, v: 32 x 128 fp16). */
+int vmk_debug_mfma32(const void* a, const void* b, void* d, void* stream);
+int vmk_debug_tile(const void* q, const void* k, const void* v, void* s, void* vt, void* o, void* ml, float sl2,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VMK_H */

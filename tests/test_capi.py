@@ -1,0 +1,90 @@
+"""The C-ABI library: builds, loads without a GPU, and exports exactly the entry points include/vmk.h declares.
+Argument checks that reject before any launch are exercised here too (they never touch the GPU)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vmk.h")
+
+
+def declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(vmk_[a-z0-9_]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from vmk import lib as L
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("libvmk.so not built")
+    return L.load()
+
+
+def test_header_declares_the_binding_table():
+    from vmk import lib as L
+    assert declared() == sorted(L.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", lib._name], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (vmk_[a-z0-9_]+)\b", out))
+    missing = [s for s in declared() if s not in exported]
+    assert not missing, missing
+
+
+def test_version_and_error_string(lib):
+    assert lib.vmk_version() == 1
+    assert isinstance(lib.vmk_last_error(), bytes)
+
+
+def test_workspace_queries_reject_bad_shapes(lib):
+    assert lib.vmk_spec_workspace_size(1, 8, 32, 8, 64, 100) == 0        # D != 128
+    assert lib.vmk_spec_workspace_size(1, 8, 30, 8, 128, 100) == 0       # Hq not a multiple of Hkv
+    assert lib.vmk_spec_workspace_size(1, 8, 32, 8, 128, 4) == 0         # L < kd
+    assert lib.vmk_spec_workspace_size(4, 8, 32, 8, 128, 32768) > 0
+    assert lib.vmk_prefix_workspace_size(8, 32, 8, 128, 0, 0, 0) == 0     # no keys at all
+    assert lib.vmk_prefix_workspace_size(8, 32, 8, 128, 2048, 256, 0) > 0
+    assert lib.vmk_dsa_workspace_size(0, 100) == 0
+    assert lib.vmk_dsa_workspace_size(4, 65536) > 4 * 65536 * 4
+
+
+def test_entry_points_reject_before_launch(lib):
+    """Host-side checks return 1 with a message and launch nothing (null pointers, bad sizes, small workspace)."""
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails its checks first
+    rc = lib.vmk_spec_verify(None, fake, fake, fake, fake, 1, 8, 32, 8, 128, 100, 1, fake, 1 << 30, None)
+    assert rc == 1 and b"null pointer" in lib.vmk_last_error()
+    rc = lib.vmk_spec_verify(fake, fake, fake, fake, fake, 1, 40, 32, 8, 128, 100, 1, fake, 1 << 30, None)
+    assert rc == 1 and b"words" in lib.vmk_last_error()
+    rc = lib.vmk_spec_verify(fake, fake, fake, fake, fake, 1, 8, 32, 8, 128, 100, 1, fake, 16, None)
+    assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
+    rc = lib.vmk_prefix_decode(fake, fake, fake, fake, fake, None, fake, 4, 32, 8, 128, 100, 10, 1, fake, 1 << 30,
+                               None)
+    assert rc == 1 and b"slens" in lib.vmk_last_error()
+    rc = lib.vmk_dsa_decode(fake, fake, fake, fake, fake, None, fake, fake, fake, 2, 5000, fake, 1024, None)
+    assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
+    rc = lib.vmk_dsa_decode(fake, fake, fake, fake, None, None, fake, fake, fake, 2, 5000, fake, 1 << 30, None)
+    assert rc == 1 and b"null pointer" in lib.vmk_last_error()
+
+
+def test_python_wrappers_validate_shapes_without_gpu():
+    import torch
+    import vmk
+    q = torch.zeros(2, 8, 32, 128, dtype=torch.float16)
+    with pytest.raises(ValueError):   # CPU tensors are rejected before any device work
+        vmk.spec_verify(q, torch.zeros(2, 8, 100, 128, dtype=torch.float16),
+                        torch.zeros(2, 8, 100, 128, dtype=torch.float16), torch.zeros(2, 8, 1, dtype=torch.int32))
+    with pytest.raises(TypeError):
+        vmk.spec_verify(q.float(), q, q, q)
+
+
+def test_kernel_modules_reject_bf16():
+    import torch
+    import spec_mi355x
+    x = torch.zeros(1, 1, 32, 128, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        spec_mi355x.kernel(x, x, x, torch.ones(1, 1, dtype=torch.int32))

@@ -16,3 +16,12 @@ def kernel(q, kv, iq, ik, w, lens=None):
     if lens is not None:
         lens = lens.to(device=q.device, dtype=torch.int32).contiguous()
     return vmk.dsa_decode(q, kv, iq, ik, w, lens)
+
+
+def select(iq, ik, w, lens=None):
+    """The indexer + exact top-2048 stage alone: returns idx (B, 2048) int32 and cnt (B,) int32."""
+    iq, ik = (x.to(torch.float16).contiguous() for x in (iq, ik))
+    w = w.to(device=iq.device, dtype=torch.float32).contiguous()
+    if lens is not None:
+        lens = lens.to(device=iq.device, dtype=torch.int32).contiguous()
+    return vmk.dsa_indexer_select(iq, ik, w, lens)
