@@ -128,45 +128,136 @@ __device__ __forceinline__ void pv_tile(RowState& st, const f16* vt, const half8
   lds_fence();
 }
 
-// ---- one wave's walk over the tiles t0, t0+tstep, ... of a key sequence, with a one-tile-ahead prefetch held in
-// two register buffers used in turn (no copies).  The key source `src` provides, for an absolute key index:
-//   krow(key) / vrow(key): an in-bounds row pointer (clamped by the source),
-//   valid(key):            whether the key belongs to the sequence,
-//   mask_scale(s, key0, g): turns the raw S^T tile into log2-domain scores, -inf where masked.
-template <class Src>
-__device__ __forceinline__ void issue_tile(u32x4 (&kr)[8], u32x4 (&vr)[8], const Src& src, int key0, int lane) {
-  const int r = lane & 31, g = lane >> 5, dc = lane & 15, kg = lane >> 4;
-  load_k(kr, src.krow(key0 + r), g);
-  load_v(vr, [&](int j) { return src.vrow(key0 + kg * 8 + j); }, [&](int j) { return src.valid(key0 + kg * 8 + j); },
-         dc);
+// ---- tile staging through LDS with direct-to-LDS loads (global_load_lds_dwordx4: each lane's 16 bytes land at
+// LDS slot `lane` of the instruction's 1 KB block, no VGPR staging).
+//
+// A stage holds one 32-key tile: K rows in bytes [0, 8192), V rows in [8192, 16384), each row 256 bytes (D = 128).
+// Within a row, the 16-byte chunk c is stored at chunk position c ^ (row & 15) (XOR swizzle), so that the K-operand
+// reads (32 lanes on 32 rows, same chunk) and the transposed V reads hit distinct LDS banks.
+constexpr int kStageBytes = 16384;
+
+#define VMK_GPTR(p) ((const void __attribute__((address_space(1)))*)(p))
+#define VMK_LPTR(p) ((void __attribute__((address_space(3)))*)(p))
+
+// Waits until at most n of this wave's vector-memory operations are outstanding (loads return in order).  An asm
+// statement with a memory clobber, so the compiler neither drops it nor moves LDS accesses across it.
+template <int n>
+__device__ __forceinline__ void wait_vmem() {
+  if constexpr (n == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (n == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else static_assert(n == 0 || n == 16, "unsupported wait count");
 }
 
+// Issues the 16 direct-to-LDS loads of one tile (8 for K, 8 for V).  Instruction j covers rows 4j..4j+3; lane l
+// loads logical chunk (l & 15) ^ (row & 15) of row 4j + (l >> 4), which lands at chunk position l & 15.
+// src.krow/src.vrow clamp the key to the sequence, so every address is in bounds.
 template <class Src>
-__device__ __forceinline__ void compute_tile(RowState& st, const half8 (&qb)[8], f16* vt, const u32x4 (&kr)[8],
-                                             const u32x4 (&vr)[8], const Src& src, int key0, int lane) {
-  store_vt(vt, vr, lane & 15, lane >> 4);
-  floatx16 s = qk_tile(kr, qb);
-  src.mask_scale(s, key0, lane >> 5);
+__device__ __forceinline__ void issue_tile_dma(char* __restrict__ stage, const Src& src, int key0, int lane) {
+  const int sub = lane >> 4, cl = lane & 15;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = 4 * j + sub;
+    const int c = cl ^ (row & 15);
+    __builtin_amdgcn_global_load_lds(VMK_GPTR(src.krow(key0 + row) + 8 * c), VMK_LPTR(stage + j * 1024), 16, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = 4 * j + sub;
+    const int c = cl ^ (row & 15);
+    __builtin_amdgcn_global_load_lds(VMK_GPTR(src.vrow(key0 + row) + 8 * c), VMK_LPTR(stage + 8192 + j * 1024), 16,
+                                     0, 0);
+  }
+}
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+// Transposed 8-byte LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes, lane 4a+c receives element c of
+// the 8-byte chunks addressed by lanes a, 4+a, 8+a, 12+a (in that order).
+__device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
+  const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (short4v __attribute__((address_space(3)))*)(VMK_LPTR(p)));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// One tile from a stage: S^T = K.Q^T from the K rows, masked online softmax, O^T += V^T.P^T with the V^T operand read
+// transposed from the V rows.  `kvalid` = number of keys of this tile that belong to the sequence (V of the others
+// is zeroed so that p = 0 never meets a non-finite value of a clamped row).
+template <class Src>
+__device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)[8], const char* __restrict__ stage,
+                                                 const Src& src, int key0, int kvalid, int lane) {
+  const int r = lane & 31, g = lane >> 5;
+  floatx16 s = floatx16{};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const u32x4 k = *reinterpret_cast<const u32x4*>(stage + r * 256 + (((8 * g + t) ^ (r & 15)) << 4));
+    s = mfma32(as_h8(k), qb[t], s);
+  }
+  src.mask_scale(s, key0, g);
   half8 pb[2];
   softmax_update(st, s, pb);
-  pv_tile(st, vt, pb, lane);
+  // V^T operand of (d-tile dt, step t): source lane l addresses row 16t + 8rr + 4g + ((l & 15) >> 2) at head-dim
+  // 32dt + 16((l >> 4) & 1) + 4(l & 3); the transposed read then gives lane l the dim 32dt + (l & 31) of the four
+  // keys 16t + 8rr + 4g + e, e = 0..3, which are exactly the keys of P^T's elements 4rr..4rr+3.
+  const char* vbase = stage + 8192;
+  const int e = (lane & 15) >> 2, hc = (lane >> 4) & 1, a4 = lane & 3;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      u32x2 part[2];
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int row = 16 * t + 8 * rr + 4 * g + e;
+        const int col = 32 * dt + 16 * hc + 4 * a4;                  // halfs
+        const int chunk = (col >> 3) ^ (row & 15);
+        part[rr] = lds_read_tr16(vbase + row * 256 + (chunk << 4) + ((col & 7) << 1));
+      }
+      half8 va = as_h8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});
+      if (kvalid < kTile) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (16 * t + 8 * (j >> 2) + 4 * g + (j & 3) >= kvalid) va[j] = (f16)0.f;
+      }
+      st.o[dt] = mfma32(va, pb[t], st.o[dt]);
+    }
+  }
 }
 
+// One wave's walk over the tiles t0, t0+tstep, ... (< ntiles) of [kbeg, ...), double-buffered in two private stages.
+// The key source `src` provides, for an absolute key index: krow(key) / vrow(key) (in-bounds row pointers, clamped
+// by the source), kend (one past the last key of the sequence part this walk covers), and
+// mask_scale(s, key0, g) (raw S^T tile -> log2-domain scores, -inf where masked).
 template <class Src>
-__device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], f16* vt, const Src& src, int kbeg,
-                                          int t0, int ntiles, int tstep, int lane) {
-  u32x4 kA[8], vA[8], kB[8], vB[8];
+__device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], char* __restrict__ s0,
+                                          char* __restrict__ s1, const Src& src, int kbeg, int t0, int ntiles,
+                                          int tstep, int lane) {
   int t = t0;
-  if (t < ntiles) issue_tile(kA, vA, src, kbeg + t * kTile, lane);
-  while (t < ntiles) {
+  if (t >= ntiles) return;
+  issue_tile_dma(s0, src, kbeg + t * kTile, lane);
+  while (true) {
     const int t1 = t + tstep;
-    if (t1 < ntiles) issue_tile(kB, vB, src, kbeg + t1 * kTile, lane);
-    compute_tile(st, qb, vt, kA, vA, src, kbeg + t * kTile, lane);
+    int key0 = kbeg + t * kTile;
+    if (t1 < ntiles) {
+      issue_tile_dma(s1, src, kbeg + t1 * kTile, lane);
+      wait_vmem<16>();
+    } else {
+      wait_vmem<0>();
+    }
+    compute_tile_lds(st, qb, s0, src, key0, min(kTile, src.kend - key0), lane);
     if (t1 >= ntiles) break;
     const int t2 = t1 + tstep;
-    if (t2 < ntiles) issue_tile(kA, vA, src, kbeg + t2 * kTile, lane);
-    compute_tile(st, qb, vt, kB, vB, src, kbeg + t1 * kTile, lane);
+    key0 = kbeg + t1 * kTile;
+    asm volatile("" ::: "memory");
+    if (t2 < ntiles) {
+      issue_tile_dma(s0, src, kbeg + t2 * kTile, lane);
+      wait_vmem<16>();
+    } else {
+      wait_vmem<0>();
+    }
+    compute_tile_lds(st, qb, s1, src, key0, min(kTile, src.kend - key0), lane);
+    if (t2 >= ntiles) break;
     t = t2;
+    asm volatile("" ::: "memory");
   }
 }
 
@@ -223,10 +314,14 @@ __device__ __forceinline__ void store_partial(float* po, float* pml, const RowSt
 
 // ---- one workgroup of WR x WK waves (WR * WK <= 4, 256 threads launched): WR row blocks of 32 rows, WK waves
 // interleaving the tiles of [kbeg, kbeg + 32*ntiles).  Writes one partial (O, m, l) for the WG's 32*WR rows to
-// po (row stride 128 floats) / pml; rows >= nrows are skipped.  smem must hold 3 * kSlotFloats floats.
+// po (row stride 128 floats) / pml; rows >= nrows are skipped.  smem must hold kAttnSmemBytes: two private stages
+// per wave during the walk, then the cross-wave merge slots.
 // qrow(row) returns an in-bounds Q row pointer for a WG-local row (clamped by the caller for rows >= nrows).
+constexpr int kAttnSmemBytes = 4 * 2 * kStageBytes;
+static_assert(3 * kSlotFloats * 4 <= kAttnSmemBytes, "merge slots must fit in the stage memory");
+
 template <class Src, class QRow>
-__device__ __forceinline__ void attend_wg(float* smem, const Src& src, QRow qrow, int nrows, int kbeg, int ntiles,
+__device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow, int nrows, int kbeg, int ntiles,
                                           int WR, int WK, float* po, float* pml) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wr = wave % WR, wk = wave / WR;
@@ -234,16 +329,17 @@ __device__ __forceinline__ void attend_wg(float* smem, const Src& src, QRow qrow
   const int row = wr * 32 + (lane & 31);
   half8 qb[8];
   load_qt(qb, qrow(row < nrows ? row : 0), lane >> 5, row < nrows);
-  f16* vt = reinterpret_cast<f16*>(smem) + wave * kVTileHalfs;
   RowState st;
   row_state_init(st);
-  if (active) wave_walk(st, qb, vt, src, kbeg, wk, ntiles, WK, lane);
+  char* mine = smem + wave * 2 * kStageBytes;
+  if (active) wave_walk(st, qb, mine, mine + kStageBytes, src, kbeg, wk, ntiles, WK, lane);
+  float* slots = reinterpret_cast<float*>(smem);
   if (WK > 1) {
     __syncthreads();
-    if (active && wk > 0) state_to_lds(smem + (wr * (WK - 1) + wk - 1) * kSlotFloats, st, lane);
+    if (active && wk > 0) state_to_lds(slots + (wr * (WK - 1) + wk - 1) * kSlotFloats, st, lane);
     __syncthreads();
     if (active && wk == 0)
-      for (int o = 1; o < WK; ++o) merge_from_lds(st, smem + (wr * (WK - 1) + o - 1) * kSlotFloats, lane);
+      for (int o = 1; o < WK; ++o) merge_from_lds(st, slots + (wr * (WK - 1) + o - 1) * kSlotFloats, lane);
   }
   if (active && wk == 0) store_partial(po + (size_t)wr * 32 * 128, pml + wr * 32 * 2, st, lane, nrows - wr * 32);
 }

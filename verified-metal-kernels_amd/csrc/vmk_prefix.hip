@@ -59,7 +59,7 @@ __device__ __forceinline__ int suffix_len(const PrefixArgs& a, int n) {
 }
 
 __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
-  __shared__ __attribute__((aligned(16))) float smem[3 * kSlotFloats];
+  __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
   const int item = blockIdx.x;
   RangeSrc src;
   src.sl2 = a.sl2;

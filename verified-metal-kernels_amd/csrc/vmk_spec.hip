@@ -21,16 +21,24 @@ struct SpecArgs {
   float sl2;               // softmax scale * log2(e)
 };
 
-// Keys of one (batch, KV head) for one split: rows of k/v, the draft mask on the last kd positions.
+// Keys of one (batch, KV head) for one split: rows of k/v, and the draft mask of this lane's row on the last kd
+// positions, preloaded as up to kMaskWords 32-bit words (kd <= 32 * kMaskWords).
+constexpr int kMaskWords = 8;
+
 struct SpecSrc {
   const f16* kbase;
   const f16* vbase;
-  const uint32_t* mrow;    // mask words of this lane's draft row
-  int kend, tail0, kd;
+  uint32_t mw[kMaskWords];
+  int kend, tail0;
   float sl2;
   __device__ const f16* krow(int key) const { return kbase + (size_t)min(key, kend - 1) * 128; }
   __device__ const f16* vrow(int key) const { return vbase + (size_t)min(key, kend - 1) * 128; }
-  __device__ bool valid(int key) const { return key < kend; }
+  __device__ uint32_t bit(int j) const {          // bit j of the row's mask, 0 <= j < 32 * kMaskWords
+    uint32_t w = mw[0];
+#pragma unroll
+    for (int i = 1; i < kMaskWords; ++i) w = (j >> 5) == i ? mw[i] : w;
+    return (w >> (j & 31)) & 1u;
+  }
   __device__ void mask_scale(floatx16& s, int key0, int g) const {
     const bool tail = key0 + kTile > tail0;           // same for the whole wave
 #pragma unroll
@@ -39,11 +47,7 @@ struct SpecSrc {
       for (int c = 0; c < 4; ++c) {
         const int key = key0 + 8 * blk + 4 * g + c;
         bool ok = key < kend;
-        if (tail) {
-          const int j = min(max(key - tail0, 0), kd - 1);
-          const uint32_t w = mrow[j >> 5];
-          ok = ok && (key < tail0 || ((w >> (j & 31)) & 1u));
-        }
+        if (tail) ok = ok && (key < tail0 || bit(key - tail0));
         s[4 * blk + c] = ok ? s[4 * blk + c] * sl2 : kNegInf;
       }
   }
@@ -51,7 +55,7 @@ struct SpecSrc {
 
 // One workgroup = WR x WK waves: WR row blocks of 32 rows, WK waves interleaving the key tiles of one split.
 __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
-  __shared__ __attribute__((aligned(16))) float smem[3 * kSlotFloats];   // >= 4 transposed V tiles
+  __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
   const int item = blockIdx.x;
   const int split = item % a.nsplit;
   const int rb = (item / a.nsplit) % a.nrb;
@@ -66,11 +70,12 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   const size_t kvoff = (size_t)grp * a.L * 128;
   src.kbase = a.k + kvoff;
   src.vbase = a.v + kvoff;
-  src.mrow = a.bits + (size_t)(b * a.kd + di) * a.W;
+  const uint32_t* mrow = a.bits + (size_t)(b * a.kd + di) * a.W;
+#pragma unroll
+  for (int i = 0; i < kMaskWords; ++i) src.mw[i] = i < a.W ? mrow[i] : 0u;
   const int kbeg = split * a.chunk;
   src.kend = min(a.L, kbeg + a.chunk);
   src.tail0 = a.L - a.kd;
-  src.kd = a.kd;
   src.sl2 = a.sl2;
   const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
   const size_t rows_wg = 32 * a.WR;
@@ -154,6 +159,7 @@ extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, cons
   VMK_CHECK(D == 128, "only head_dim 128 is supported");
   VMK_CHECK(L >= kd, "L must count the kd drafts (L >= kd)");
   VMK_CHECK(W == (kd + 31) / 32, "mask must hold ceil(kd/32) 32-bit words per draft");
+  VMK_CHECK(kd <= 32 * kMaskWords, "at most 256 drafts");
   VMK_CHECK((Hq / Hkv) * kd <= 1 << 20 && B * Hkv * L <= (int64_t)1 << 40, "sizes out of range");
   VMK_CHECK(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "tensors must be 16-byte aligned");
   const size_t need = vmk_spec_workspace_size(B, kd, Hq, Hkv, D, L);
