@@ -148,6 +148,20 @@ __device__ __forceinline__ void wait_vmem() {
   else static_assert(n == 0 || n == 16, "unsupported wait count");
 }
 
+// Same with a count known only at run time (0 <= n <= 63; larger counts wait for everything).
+__device__ __forceinline__ void wait_vmem_dyn(int n) {
+#define VMK_WAIT_CASE(k) case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+  switch (n) {
+    VMK_WAIT_CASE(1) VMK_WAIT_CASE(2) VMK_WAIT_CASE(3) VMK_WAIT_CASE(4) VMK_WAIT_CASE(5) VMK_WAIT_CASE(6)
+    VMK_WAIT_CASE(7) VMK_WAIT_CASE(8) VMK_WAIT_CASE(9) VMK_WAIT_CASE(10) VMK_WAIT_CASE(11) VMK_WAIT_CASE(12)
+    VMK_WAIT_CASE(13) VMK_WAIT_CASE(14) VMK_WAIT_CASE(15) VMK_WAIT_CASE(16) VMK_WAIT_CASE(18) VMK_WAIT_CASE(20)
+    VMK_WAIT_CASE(24) VMK_WAIT_CASE(27) VMK_WAIT_CASE(28) VMK_WAIT_CASE(32) VMK_WAIT_CASE(36) VMK_WAIT_CASE(40)
+    VMK_WAIT_CASE(45) VMK_WAIT_CASE(48)
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+  }
+#undef VMK_WAIT_CASE
+}
+
 // Issues the 16 direct-to-LDS loads of one tile (8 for K, 8 for V).  Instruction j covers rows 4j..4j+3; lane l
 // loads logical chunk (l & 15) ^ (row & 15) of row 4j + (l >> 4), which lands at chunk position l & 15.
 // src.krow/src.vrow clamp the key to the sequence, so every address is in bounds.
@@ -166,6 +180,35 @@ __device__ __forceinline__ void issue_tile_dma(char* __restrict__ stage, const S
     const int c = cl ^ (row & 15);
     __builtin_amdgcn_global_load_lds(VMK_GPTR(src.vrow(key0 + row) + 8 * c), VMK_LPTR(stage + 8192 + j * 1024), 16,
                                      0, 0);
+  }
+}
+
+// The share of one tile's 16 DMA instructions issued by wave `part` of `nparts` (instructions part, part+nparts, ..).
+template <class Src>
+__device__ __forceinline__ void issue_tile_dma_part(char* __restrict__ stage, const Src& src, int key0, int lane,
+                                                    int part, int nparts) {
+  const int sub = lane >> 4, cl = lane & 15;
+  for (int i = part; i < 16; i += nparts) {
+    const int j = i & 7;
+    const int row = 4 * j + sub;
+    const int c = cl ^ (row & 15);
+    const f16* g = i < 8 ? src.krow(key0 + row) : src.vrow(key0 + row);
+    __builtin_amdgcn_global_load_lds(VMK_GPTR(g + 8 * c), VMK_LPTR(stage + (i < 8 ? 0 : 8192) + j * 1024), 16, 0,
+                                     0);
+  }
+}
+
+// ---- a ring of NS stages shared by the NW waves of a workgroup; every wave consumes every tile.  Each wave issues
+// DPW of the tile's DMA instructions (issue(stage, t) must issue exactly DPW per wave) and waits for its own, and a
+// barrier per tile then makes the whole tile visible and frees the stage the next issue overwrites.
+template <int NS, int DPW, class Issue, class Compute>
+__device__ __forceinline__ void ring_walk(char* ring, int stage_bytes, int ntiles, Issue issue, Compute compute) {
+  for (int t = 0; t < NS - 1 && t < ntiles; ++t) issue(ring + t * stage_bytes, t);
+  for (int t = 0; t < ntiles; ++t) {
+    wait_vmem_dyn(DPW * min(NS - 2, ntiles - 1 - t));
+    __syncthreads();
+    if (t + NS - 1 < ntiles) issue(ring + ((t + NS - 1) % NS) * stage_bytes, t + NS - 1);
+    compute(ring + (t % NS) * stage_bytes, t);
   }
 }
 
@@ -342,6 +385,87 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
       for (int o = 1; o < WK; ++o) merge_from_lds(st, slots + (wr * (WK - 1) + o - 1) * kSlotFloats, lane);
   }
   if (active && wk == 0) store_partial(po + (size_t)wr * 32 * 128, pml + wr * 32 * 2, st, lane, nrows - wr * 32);
+}
+
+// ---- log-sum-exp merge of the partials of one output row, NT threads, PER head-dims per thread (d = tid + k*NT).
+// part(i, ml, o) sets ml -> (m, l) and o -> the partial's O row of partial i (0 <= i < nparts).  The m/l of a batch
+// of NT partials are fetched in parallel and their weights shared through LDS, so that the O loads of the
+// accumulation loop are independent of each other and can all be in flight together.
+template <int NT, int PER, class Part>
+__device__ __forceinline__ void combine_row(int nparts, Part part, f16* out) {
+  __shared__ float sw[NT], sl[NT], red[NT / 64];
+  const int tid = threadIdx.x;
+  float M = kNegInf;
+  for (int b0 = 0; b0 < nparts; b0 += NT) {
+    if (b0 + tid < nparts) {
+      const float* ml;
+      const float* o;
+      part(b0 + tid, ml, o);
+      M = fmaxf(M, ml[0]);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = M;
+  __syncthreads();
+  M = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) M = fmaxf(M, red[w]);
+  const float Muse = (M == kNegInf) ? 0.f : M;
+  float num[PER], den = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) num[k] = 0.f;
+  for (int b0 = 0; b0 < nparts; b0 += NT) {
+    const int n = min(NT, nparts - b0);
+    __syncthreads();
+    if (tid < n) {
+      const float* ml;
+      const float* o;
+      part(b0 + tid, ml, o);
+      const float w = fast_exp2(ml[0] - Muse);
+      sw[tid] = w;
+      sl[tid] = w * ml[1];
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int j = 0; j < n; ++j) {
+      const float* ml;
+      const float* o;
+      part(b0 + j, ml, o);
+      const float w = sw[j];
+      den += sl[j];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) num[k] += w * o[tid + k * NT];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) out[tid + k * NT] = (f16)(num[k] / den);
+}
+
+// ---- one workgroup of NW waves sharing a ring of kRowsStages stages: wave w owns rows [32w, 32w+32) and every wave
+// consumes every tile of [kbeg, kbeg + 32*ntiles).  Writes the WG's partial (32*NW rows) like attend_wg.
+constexpr int kRowsStages = 4;
+constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
+
+template <int NW, class Src, class QRow>
+__device__ __forceinline__ void attend_wg_rows(char* smem, const Src& src, QRow qrow, int nrows, int kbeg,
+                                               int ntiles, float* po, float* pml) {
+  static_assert(16 % NW == 0, "the 16 DMA instructions of a tile must split evenly over the waves");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = wave * 32 + (lane & 31);
+  half8 qb[8];
+  load_qt(qb, qrow(row < nrows ? row : 0), lane >> 5, row < nrows);
+  RowState st;
+  row_state_init(st);
+  const bool has_rows = wave * 32 < nrows;
+  ring_walk<kRowsStages, 16 / NW>(
+      smem, kStageBytes, ntiles,
+      [&](char* stage, int t) { issue_tile_dma_part(stage, src, kbeg + t * kTile, lane, wave, NW); },
+      [&](const char* stage, int t) {
+        const int key0 = kbeg + t * kTile;
+        if (has_rows) compute_tile_lds(st, qb, stage, src, key0, min(kTile, src.kend - key0), lane);
+      });
+  if (has_rows) store_partial(po + (size_t)wave * 32 * 128, pml + wave * 32 * 2, st, lane, nrows - wave * 32);
 }
 
 }  // namespace vmk

@@ -380,21 +380,13 @@ __global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
   const int cnt = min(a.cnt[b], kTopK);
   const int nch = (cnt + kChunk - 1) / kChunk;
   const size_t item0 = ((size_t)b * 4 + hb) * kNChunk;
-  float M = kNegInf;
-  for (int c = 0; c < nch; ++c) M = fmaxf(M, a.pml[((item0 + c) * 32 + hr) * 2]);
-  const float Muse = (M == kNegInf) ? 0.f : M;
-  float n0 = 0.f, n1 = 0.f, den = 0.f;
-  const int d = threadIdx.x;
-  for (int c = 0; c < nch; ++c) {
-    const size_t base = (item0 + c) * 32 + hr;
-    const float wgt = fast_exp2(a.pml[base * 2] - Muse);
-    den += wgt * a.pml[base * 2 + 1];
-    n0 += wgt * a.po[base * kDC + d];
-    n1 += wgt * a.po[base * kDC + d + 256];
-  }
-  f16* o = a.out + (size_t)bh * kDC;
-  o[d] = (f16)(n0 / den);
-  o[d + 256] = (f16)(n1 / den);
+  combine_row<256, 2>(nch,
+                      [&](int c, const float*& ml, const float*& o) {
+                        const size_t base = (item0 + c) * 32 + hr;
+                        ml = a.pml + base * 2;
+                        o = a.po + base * kDC;
+                      },
+                      a.out + (size_t)bh * kDC);
 }
 
 struct DsaLayout {

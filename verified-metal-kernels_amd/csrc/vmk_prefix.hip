@@ -31,6 +31,7 @@ struct PrefixArgs {
   int WRp, WKp, nrb_p, nsplit_p, chunk_p;   // prefix plan
   int nsplit_s, chunk_s;                    // suffix plan (WR = 1, WK = 4)
   int n_prefix_items;
+  int item0;               // first item handled by the key-split kernel (n_prefix_items when prefix rows run apart)
   float sl2;
 };
 
@@ -60,7 +61,7 @@ __device__ __forceinline__ int suffix_len(const PrefixArgs& a, int n) {
 
 __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
-  const int item = blockIdx.x;
+  const int item = a.item0 + blockIdx.x;
   RangeSrc src;
   src.sl2 = a.sl2;
   if (item < a.n_prefix_items) {
@@ -100,13 +101,40 @@ __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
   }
 }
 
+// Prefix items when N*G > 64: NW waves own 32 of the N*G rows each and share one LDS ring, so the prefix chunk is
+// streamed from HBM once per 32*NW rows.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kRowsSmemBytes];
+  const int item = blockIdx.x;
+  const int split = item % a.nsplit_p;
+  const int rb = (item / a.nsplit_p) % a.nrb_p;
+  const int h = item / (a.nsplit_p * a.nrb_p);
+  RangeSrc src;
+  src.sl2 = a.sl2;
+  const size_t off = (size_t)h * a.P * 128;
+  src.kbase = a.kp + off;
+  src.vbase = a.vp + off;
+  const int kbeg = split * a.chunk_p;
+  src.kend = min(a.P, kbeg + a.chunk_p);
+  const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
+  const int row0 = rb * NW * 32;
+  const size_t rows_wg = 32 * NW;
+  attend_wg_rows<NW>(smem, src,
+                     [&](int r) {
+                       const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
+                       return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
+                     },
+                     a.N * a.G - row0, kbeg, ntiles, a.po_p + (size_t)item * rows_wg * 128,
+                     a.pml_p + (size_t)item * rows_wg * 2);
+}
+
 // One workgroup (128 threads = head-dims) per output row (n, hq): merge the prefix splits of KV head h and the
 // suffix chunks of request n.
 __global__ __launch_bounds__(128) void prefix_combine_kernel(PrefixArgs a) {
   const int rowg = blockIdx.x;                 // n * Hq + hq
   const int n = rowg / a.Hq, hq = rowg % a.Hq;
   const int h = hq / a.G, gg = hq % a.G;
-  const int d = threadIdx.x;
   const int prow = n * a.G + gg;               // row of this output among the N*G rows of KV head h
   const int rows_p = 32 * a.WRp;
   const int rb = prow / rows_p, rl = prow % rows_p;
@@ -115,27 +143,23 @@ __global__ __launch_bounds__(128) void prefix_combine_kernel(PrefixArgs a) {
   const int sn = suffix_len(a, n);
   const int ns = (sn + a.chunk_s - 1) / a.chunk_s;
   const size_t sitem0 = ((size_t)n * a.Hkv + h) * a.nsplit_s;
-  float M = kNegInf;
-  for (int s = 0; s < np; ++s) M = fmaxf(M, a.pml_p[((pitem0 + s) * rows_p + rl) * 2]);
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.pml_s[((sitem0 + s) * 32 + gg) * 2]);
-  const float Muse = (M == kNegInf) ? 0.f : M;
-  float num = 0.f, den = 0.f;
-  for (int s = 0; s < np; ++s) {
-    const size_t base = (pitem0 + s) * rows_p + rl;
-    const float w = fast_exp2(a.pml_p[base * 2] - Muse);
-    den += w * a.pml_p[base * 2 + 1];
-    num += w * a.po_p[base * 128 + d];
-  }
-  for (int s = 0; s < ns; ++s) {
-    const size_t base = (sitem0 + s) * 32 + gg;
-    const float w = fast_exp2(a.pml_s[base * 2] - Muse);
-    den += w * a.pml_s[base * 2 + 1];
-    num += w * a.po_s[base * 128 + d];
-  }
-  a.out[(size_t)rowg * 128 + d] = (f16)(num / den);
+  combine_row<128, 1>(np + ns,
+                      [&](int s, const float*& ml, const float*& o) {
+                        if (s < np) {
+                          const size_t base = (pitem0 + s) * rows_p + rl;
+                          ml = a.pml_p + base * 2;
+                          o = a.po_p + base * 128;
+                        } else {
+                          const size_t base = (sitem0 + (s - np)) * 32 + gg;
+                          ml = a.pml_s + base * 2;
+                          o = a.po_s + base * 128;
+                        }
+                      },
+                      a.out + (size_t)rowg * 128);
 }
 
 struct PrefixPlan {
+  bool rows_mode;
   int WRp, WKp, nrb_p, nsplit_p, chunk_p, nsplit_s, chunk_s;
   size_t po_p, pml_p, po_s, pml_s;
   int n_prefix_items, n_items;
@@ -144,12 +168,13 @@ struct PrefixPlan {
 static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int64_t S) {
   PrefixPlan p;
   const int64_t G = Hq / Hkv, R = N * G;
-  if (R <= 32) { p.WRp = 1; p.WKp = 4; }
-  else if (R <= 64) { p.WRp = 2; p.WKp = 2; }
-  else { p.WRp = 4; p.WKp = 1; }
+  p.rows_mode = R > 64;
+  if (p.rows_mode) { p.WRp = R <= 128 ? 4 : 8; p.WKp = 1; }   // row-split: WRp = waves sharing one ring
+  else if (R <= 32) { p.WRp = 1; p.WKp = 4; }
+  else { p.WRp = 2; p.WKp = 2; }
   const int64_t rows_wg = 32 * p.WRp;
   p.nrb_p = (int)((R + rows_wg - 1) / rows_wg);
-  // Prefix chunks of ~1024 keys (fewer for small P so that short prefixes still spread over the GPU).
+  // Prefix chunks of at most 1024 keys, fewer when that spreads the prefix over ~256 workgroups.
   int64_t chunk = 1024;
   if (P > 0) {
     const int64_t want = std::max<int64_t>(1, 256 / std::max<int64_t>(1, Hkv * p.nrb_p));
@@ -213,14 +238,22 @@ extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, 
   a.N = (int)N; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.P = (int)P; a.S = (int)S;
   a.WRp = p.WRp; a.WKp = p.WKp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;
   a.nsplit_s = p.nsplit_s; a.chunk_s = p.chunk_s; a.n_prefix_items = p.n_prefix_items;
+  a.item0 = p.rows_mode ? p.n_prefix_items : 0;
   a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  if (p.n_items > 0) {
-    prof_before(kKPrefixPartial, s);
-    hipLaunchKernelGGL(prefix_partial_kernel, dim3((unsigned)p.n_items), dim3(256), 0, s, a);
-    prof_after(kKPrefixPartial, s);
+  prof_before(kKPrefixPartial, s);
+  if (p.rows_mode && p.n_prefix_items > 0) {
+    if (p.WRp == 4)
+      hipLaunchKernelGGL(prefix_rows_kernel<4>, dim3((unsigned)p.n_prefix_items), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(prefix_rows_kernel<8>, dim3((unsigned)p.n_prefix_items), dim3(512), 0, s, a);
     VMK_CHECK_HIP(hipGetLastError());
   }
+  if (p.n_items - a.item0 > 0) {
+    hipLaunchKernelGGL(prefix_partial_kernel, dim3((unsigned)(p.n_items - a.item0)), dim3(256), 0, s, a);
+    VMK_CHECK_HIP(hipGetLastError());
+  }
+  prof_after(kKPrefixPartial, s);
   prof_before(kKPrefixCombine, s);
   hipLaunchKernelGGL(prefix_combine_kernel, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
   prof_after(kKPrefixCombine, s);

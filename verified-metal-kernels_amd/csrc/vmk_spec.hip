@@ -88,31 +88,63 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
             a.part_ml + (size_t)item * rows_wg * 2);
 }
 
+// Row-split variant for kd*G > 64 rows: NW waves own 32 rows each and share one LDS ring, so every K/V tile of the
+// split is streamed from HBM once per workgroup of 32*NW rows.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void spec_partial_rows_kernel(SpecArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kRowsSmemBytes];
+  const int item = blockIdx.x;
+  const int split = item % a.nsplit;
+  const int rb = (item / a.nsplit) % a.nrb;
+  const int grp = item / (a.nsplit * a.nrb);
+  const int b = grp / a.Hkv, h = grp % a.Hkv;
+  const int R = a.kd * a.G;
+  const int row0 = rb * NW * 32;
+  const int lrow = row0 + (threadIdx.x & 31) + 32 * (threadIdx.x >> 6);
+  const int di = (lrow < R ? lrow : 0) / a.G;
+  SpecSrc src;
+  const size_t kvoff = (size_t)grp * a.L * 128;
+  src.kbase = a.k + kvoff;
+  src.vbase = a.v + kvoff;
+  const uint32_t* mrow = a.bits + (size_t)(b * a.kd + di) * a.W;
+#pragma unroll
+  for (int i = 0; i < kMaskWords; ++i) src.mw[i] = i < a.W ? mrow[i] : 0u;
+  const int kbeg = split * a.chunk;
+  src.kend = min(a.L, kbeg + a.chunk);
+  src.tail0 = a.L - a.kd;
+  src.sl2 = a.sl2;
+  const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
+  const size_t rows_wg = 32 * NW;
+  attend_wg_rows<NW>(smem, src,
+                     [&](int r) {
+                       const int qr = row0 + r, i = qr / a.G, gg = qr % a.G;
+                       return a.q + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128;
+                     },
+                     R - row0, kbeg, ntiles, a.part_o + (size_t)item * rows_wg * 128,
+                     a.part_ml + (size_t)item * rows_wg * 2);
+}
+
 // LSE merge of the nsplit partials of every query row; one workgroup (128 threads = head-dims) per row.
 __global__ __launch_bounds__(128) void spec_combine_kernel(SpecArgs a) {
   const int R = a.kd * a.G;
   const int rowg = blockIdx.x;                 // grp * R + row
   const int grp = rowg / R, row = rowg % R;
   const int rb = row / (32 * a.WR), rl = row % (32 * a.WR);
-  const int d = threadIdx.x;
   const size_t rows_wg = 32 * a.WR;
   const size_t item0 = (size_t)(grp * a.nrb + rb) * a.nsplit;
-  float M = kNegInf;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[((item0 + s) * rows_wg + rl) * 2]);
-  const float Muse = (M == kNegInf) ? 0.f : M;
-  float num = 0.f, den = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
-    const size_t base = (item0 + s) * rows_wg + rl;
-    const float w = fast_exp2(a.part_ml[base * 2] - Muse);
-    den += w * a.part_ml[base * 2 + 1];
-    num += w * a.part_o[base * 128 + d];
-  }
   const int b = grp / a.Hkv, h = grp % a.Hkv;
   const int i = row / a.G, gg = row % a.G;
-  a.out[((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128 + d] = (f16)(num / den);
+  combine_row<128, 1>(a.nsplit,
+                      [&](int s, const float*& ml, const float*& o) {
+                        const size_t base = (item0 + s) * rows_wg + rl;
+                        ml = a.part_ml + base * 2;
+                        o = a.part_o + base * 128;
+                      },
+                      a.out + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128);
 }
 
 struct SpecPlan {
+  bool rows_mode;
   int WR, WK, nrb, nsplit, chunk;
   size_t po_floats, pml_floats;
 };
@@ -120,15 +152,17 @@ struct SpecPlan {
 static SpecPlan spec_plan(int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t L) {
   SpecPlan p;
   const int64_t G = Hq / Hkv, R = kd * G;
-  if (R <= 32) { p.WR = 1; p.WK = 4; }
-  else if (R <= 64) { p.WR = 2; p.WK = 2; }
-  else { p.WR = 4; p.WK = 1; }
+  p.rows_mode = R > 64;
+  if (p.rows_mode) { p.WR = R <= 128 ? 4 : 8; p.WK = 1; }   // row-split: WR = waves sharing one ring
+  else if (R <= 32) { p.WR = 1; p.WK = 4; }
+  else { p.WR = 2; p.WK = 2; }
   const int64_t rows_wg = 32 * p.WR;
   p.nrb = (int)((R + rows_wg - 1) / rows_wg);
   const int64_t base = B * Hkv * p.nrb;
   const int64_t max_split = (L + kTile * p.WK - 1) / (kTile * p.WK);
-  int64_t ns = (1024 + base - 1) / base;
-  // Keep the fp32 partials (rows * 130 floats per split) under ~8 % of the K/V stream.
+  // Key-split workgroups are small (4 waves, 1 per CU by LDS): aim at ~1024; row-split ones carry 32*WR rows and
+  // their fp32 partials grow with the rows, so aim at ~256 and keep partials under ~8 % of the K/V stream.
+  int64_t ns = ((p.rows_mode ? 256 : 1024) + base - 1) / base;
   const int64_t cap = std::max<int64_t>(1, (int64_t)(0.08 * (double)L / (double)(p.nrb * rows_wg)));
   ns = std::max<int64_t>(1, std::min(ns, std::min(max_split, cap)));
   int64_t chunk = (L + ns - 1) / ns;
@@ -176,7 +210,12 @@ extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, cons
   hipStream_t s = (hipStream_t)stream;
   const unsigned items = (unsigned)(B * Hkv * p.nrb * p.nsplit);
   prof_before(kKSpecPartial, s);
-  hipLaunchKernelGGL(spec_partial_kernel, dim3(items), dim3(64 * p.WR * p.WK), 0, s, a);
+  if (!p.rows_mode)
+    hipLaunchKernelGGL(spec_partial_kernel, dim3(items), dim3(256), 0, s, a);
+  else if (p.WR == 4)
+    hipLaunchKernelGGL(spec_partial_rows_kernel<4>, dim3(items), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(spec_partial_rows_kernel<8>, dim3(items), dim3(512), 0, s, a);
   prof_after(kKSpecPartial, s);
   VMK_CHECK_HIP(hipGetLastError());
   prof_before(kKSpecCombine, s);
