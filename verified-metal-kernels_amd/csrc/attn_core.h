@@ -87,25 +87,32 @@ __device__ __forceinline__ floatx16 qk_tile(const u32x4 (&kr)[8], const half8 (&
 }
 
 // Online-softmax update with scores already scaled to the log2 domain (masked keys = -inf).  Returns P^T operands.
-// Guard: while the row has seen only -inf, the subtrahend is 0 so exp2(-inf) = 0 and a NaN score still yields NaN.
+// The reference point m only moves when a tile's max exceeds it by more than 8 (a factor 256): p = exp2(s - m) then
+// stays <= 256, which fp16 P and the fp32 sums hold exactly as well as p <= 1, and the O rescale is skipped for the
+// whole wave unless some row moved.  Guard: while a row has seen only -inf, the subtrahend is 0 so exp2(-inf) = 0
+// and a NaN score still yields NaN.
 __device__ __forceinline__ void softmax_update(RowState& st, floatx16& s, half8 (&pb)[2]) {
   float tmax = s[0];
 #pragma unroll
   for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
   tmax = fmaxf(tmax, xor32(tmax));
-  const float mnew = fmaxf(st.m, tmax);
+  const bool move = tmax > st.m + 8.f;          // false for NaN / -inf tiles
+  const float mnew = move ? tmax : st.m;
   const float muse = (mnew == kNegInf) ? 0.f : mnew;
-  const float alpha = fast_exp2(st.m - muse);
   float lsum = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     s[i] = fast_exp2(s[i] - muse);
     lsum += s[i];
   }
-  st.l = st.l * alpha + lsum;
-  st.m = mnew;
+  if (__builtin_amdgcn_ballot_w64(move)) {       // rare after the first tiles
+    const float alpha = fast_exp2(st.m - muse);
+    st.l *= alpha;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) st.o[dt] *= alpha;
+    for (int dt = 0; dt < 4; ++dt) st.o[dt] *= alpha;
+  }
+  st.l += lsum;
+  st.m = mnew;
   pb[0] = pack8(s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7]);
   pb[1] = pack8(s[8], s[9], s[10], s[11], s[12], s[13], s[14], s[15]);
 }
@@ -161,6 +168,10 @@ __device__ __forceinline__ void wait_vmem_dyn(int n) {
   }
 #undef VMK_WAIT_CASE
 }
+
+// One all-zero fp16 row (256 bytes, zero-initialised at load time and never written): the K/V source of every key
+// outside the sequence, so a tile's spare rows are zeros and p = 0 never meets a non-finite value of a foreign row.
+__device__ const f16 g_zero_row[128] = {};
 
 // Issues the 16 direct-to-LDS loads of one tile (8 for K, 8 for V).  Instruction j covers rows 4j..4j+3; lane l
 // loads logical chunk (l & 15) ^ (row & 15) of row 4j + (l >> 4), which lands at chunk position l & 15.
@@ -223,11 +234,10 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
 }
 
 // One tile from a stage: S^T = K.Q^T from the K rows, masked online softmax, O^T += V^T.P^T with the V^T operand read
-// transposed from the V rows.  `kvalid` = number of keys of this tile that belong to the sequence (V of the others
-// is zeroed so that p = 0 never meets a non-finite value of a clamped row).
+// transposed from the V rows (rows of keys outside the sequence were loaded from g_zero_row).
 template <class Src>
 __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)[8], const char* __restrict__ stage,
-                                                 const Src& src, int key0, int kvalid, int lane) {
+                                                 const Src& src, int key0, int lane) {
   const int r = lane & 31, g = lane >> 5;
   floatx16 s = floatx16{};
 #pragma unroll
@@ -255,20 +265,15 @@ __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)
         const int chunk = (col >> 3) ^ (row & 15);
         part[rr] = lds_read_tr16(vbase + row * 256 + (chunk << 4) + ((col & 7) << 1));
       }
-      half8 va = as_h8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});
-      if (kvalid < kTile) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (16 * t + 8 * (j >> 2) + 4 * g + (j & 3) >= kvalid) va[j] = (f16)0.f;
-      }
+      const half8 va = as_h8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});
       st.o[dt] = mfma32(va, pb[t], st.o[dt]);
     }
   }
 }
 
 // One wave's walk over the tiles t0, t0+tstep, ... (< ntiles) of [kbeg, ...), double-buffered in two private stages.
-// The key source `src` provides, for an absolute key index: krow(key) / vrow(key) (in-bounds row pointers, clamped
-// by the source), kend (one past the last key of the sequence part this walk covers), and
+// The key source `src` provides, for an absolute key index: krow(key) / vrow(key) (in-bounds row pointers; keys at
+// or past kend give g_zero_row), kend (one past the last key of the sequence part this walk covers), and
 // mask_scale(s, key0, g) (raw S^T tile -> log2-domain scores, -inf where masked).
 template <class Src>
 __device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], char* __restrict__ s0,
@@ -286,7 +291,7 @@ __device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], ch
     } else {
       wait_vmem<0>();
     }
-    compute_tile_lds(st, qb, s0, src, key0, min(kTile, src.kend - key0), lane);
+    compute_tile_lds(st, qb, s0, src, key0, lane);
     if (t1 >= ntiles) break;
     const int t2 = t1 + tstep;
     key0 = kbeg + t1 * kTile;
@@ -297,7 +302,7 @@ __device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], ch
     } else {
       wait_vmem<0>();
     }
-    compute_tile_lds(st, qb, s1, src, key0, min(kTile, src.kend - key0), lane);
+    compute_tile_lds(st, qb, s1, src, key0, lane);
     if (t2 >= ntiles) break;
     t = t2;
     asm volatile("" ::: "memory");
@@ -463,7 +468,7 @@ __device__ __forceinline__ void attend_wg_rows(char* smem, const Src& src, QRow 
       [&](char* stage, int t) { issue_tile_dma_part(stage, src, kbeg + t * kTile, lane, wave, NW); },
       [&](const char* stage, int t) {
         const int key0 = kbeg + t * kTile;
-        if (has_rows) compute_tile_lds(st, qb, stage, src, key0, min(kTile, src.kend - key0), lane);
+        if (has_rows) compute_tile_lds(st, qb, stage, src, key0, lane);
       });
   if (has_rows) store_partial(po + (size_t)wave * 32 * 128, pml + wave * 32 * 2, st, lane, nrows - wave * 32);
 }

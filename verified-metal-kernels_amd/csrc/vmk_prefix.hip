@@ -40,10 +40,15 @@ struct RangeSrc {
   const f16* vbase;
   int kend;
   float sl2;
-  __device__ const f16* krow(int key) const { return kbase + (size_t)min(key, kend - 1) * 128; }
-  __device__ const f16* vrow(int key) const { return vbase + (size_t)min(key, kend - 1) * 128; }
+  __device__ const f16* krow(int key) const { return key < kend ? kbase + (size_t)key * 128 : g_zero_row; }
+  __device__ const f16* vrow(int key) const { return key < kend ? vbase + (size_t)key * 128 : g_zero_row; }
   __device__ bool valid(int key) const { return key < kend; }
   __device__ void mask_scale(floatx16& s, int key0, int g) const {
+    if (key0 + kTile <= kend) {                            // whole tile inside (same for the whole wave)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] *= sl2;
+      return;
+    }
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
 #pragma unroll

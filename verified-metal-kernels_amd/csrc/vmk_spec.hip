@@ -31,8 +31,8 @@ struct SpecSrc {
   uint32_t mw[kMaskWords];
   int kend, tail0;
   float sl2;
-  __device__ const f16* krow(int key) const { return kbase + (size_t)min(key, kend - 1) * 128; }
-  __device__ const f16* vrow(int key) const { return vbase + (size_t)min(key, kend - 1) * 128; }
+  __device__ const f16* krow(int key) const { return key < kend ? kbase + (size_t)key * 128 : g_zero_row; }
+  __device__ const f16* vrow(int key) const { return key < kend ? vbase + (size_t)key * 128 : g_zero_row; }
   __device__ uint32_t bit(int j) const {          // bit j of the row's mask, 0 <= j < 32 * kMaskWords
     uint32_t w = mw[0];
 #pragma unroll
@@ -40,14 +40,18 @@ struct SpecSrc {
     return (w >> (j & 31)) & 1u;
   }
   __device__ void mask_scale(floatx16& s, int key0, int g) const {
-    const bool tail = key0 + kTile > tail0;           // same for the whole wave
+    if (key0 + kTile <= tail0 && key0 + kTile <= kend) {   // whole tile visible (same for the whole wave)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] *= sl2;
+      return;
+    }
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int key = key0 + 8 * blk + 4 * g + c;
-        bool ok = key < kend;
-        if (tail) ok = ok && (key < tail0 || bit(key - tail0));
+        const uint32_t vis = (key < tail0) | bit(max(key - tail0, 0));
+        const bool ok = (key < kend) & (vis != 0u);
         s[4 * blk + c] = ok ? s[4 * blk + c] * sl2 : kNegInf;
       }
   }
