@@ -139,9 +139,14 @@ __device__ __forceinline__ void pv_tile(RowState& st, const f16* vt, const half8
 // LDS slot `lane` of the instruction's 1 KB block, no VGPR staging).
 //
 // A stage holds one 32-key tile: K rows in bytes [0, 8192), V rows in [8192, 16384), each row 256 bytes (D = 128).
-// Within a row, the 16-byte chunk c is stored at chunk position c ^ (row & 15) (XOR swizzle), so that the K-operand
-// reads (32 lanes on 32 rows, same chunk) and the transposed V reads hit distinct LDS banks.
+// Within a row, the 16-byte chunk c is stored at chunk position c ^ swz(row), where swz swaps the two 2-bit fields of
+// row & 15.  A row is exactly one pass over the 64 LDS banks, so the bank of a chunk is its position.  swz is a
+// bijection on 16 consecutive rows, so the K-operand reads (16 rows, one logical chunk, per pass) are conflict-free.
+// For the transposed V reads (8 rows x 4 logical chunks x 2 half-chunks per instruction) the 32 (row, chunk) pairs
+// fall on all 16 positions exactly twice, i.e. the minimum two passes.
 constexpr int kStageBytes = 16384;
+
+__device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
 
 #define VMK_GPTR(p) ((const void __attribute__((address_space(1)))*)(p))
 #define VMK_LPTR(p) ((void __attribute__((address_space(3)))*)(p))
@@ -182,13 +187,13 @@ __device__ __forceinline__ void issue_tile_dma(char* __restrict__ stage, const S
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int row = 4 * j + sub;
-    const int c = cl ^ (row & 15);
+    const int c = cl ^ swz(row);
     __builtin_amdgcn_global_load_lds(VMK_GPTR(src.krow(key0 + row) + 8 * c), VMK_LPTR(stage + j * 1024), 16, 0, 0);
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int row = 4 * j + sub;
-    const int c = cl ^ (row & 15);
+    const int c = cl ^ swz(row);
     __builtin_amdgcn_global_load_lds(VMK_GPTR(src.vrow(key0 + row) + 8 * c), VMK_LPTR(stage + 8192 + j * 1024), 16,
                                      0, 0);
   }
@@ -202,7 +207,7 @@ __device__ __forceinline__ void issue_tile_dma_part(char* __restrict__ stage, co
   for (int i = part; i < 16; i += nparts) {
     const int j = i & 7;
     const int row = 4 * j + sub;
-    const int c = cl ^ (row & 15);
+    const int c = cl ^ swz(row);
     const f16* g = i < 8 ? src.krow(key0 + row) : src.vrow(key0 + row);
     __builtin_amdgcn_global_load_lds(VMK_GPTR(g + 8 * c), VMK_LPTR(stage + (i < 8 ? 0 : 8192) + j * 1024), 16, 0,
                                      0);
@@ -242,7 +247,7 @@ __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)
   floatx16 s = floatx16{};
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const u32x4 k = *reinterpret_cast<const u32x4*>(stage + r * 256 + (((8 * g + t) ^ (r & 15)) << 4));
+    const u32x4 k = *reinterpret_cast<const u32x4*>(stage + r * 256 + (((8 * g + t) ^ swz(r)) << 4));
     s = mfma32(as_h8(k), qb[t], s);
   }
   src.mask_scale(s, key0, g);
@@ -262,7 +267,7 @@ __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)
       for (int rr = 0; rr < 2; ++rr) {
         const int row = 16 * t + 8 * rr + 4 * g + e;
         const int col = 32 * dt + 16 * hc + 4 * a4;                  // halfs
-        const int chunk = (col >> 3) ^ (row & 15);
+        const int chunk = (col >> 3) ^ swz(row);
         part[rr] = lds_read_tr16(vbase + row * 256 + (chunk << 4) + ((col & 7) << 1));
       }
       const half8 va = as_h8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});

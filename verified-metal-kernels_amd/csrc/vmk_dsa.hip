@@ -173,6 +173,29 @@ __device__ void find_threshold(SelectShared& sh, int nbins, uint32_t need) {
   __syncthreads();
 }
 
+// Scores are read in rounds of 32768 positions: thread t owns the 32 consecutive positions base + 32t .. +31 of a
+// round, loaded as 8 float4 at once and kept in registers for the count and emit passes of that round.
+constexpr int kRound = 32768;
+constexpr int kPerThread = kRound / 1024;
+
+__device__ __forceinline__ void load_round(const float* sc, int base, int n, uint32_t (&key)[kPerThread]) {
+  const int p0 = base + threadIdx.x * kPerThread;
+  floatx4 v[kPerThread / 4];
+#pragma unroll
+  for (int i = 0; i < kPerThread / 4; ++i) {
+    const int p = p0 + 4 * i;
+    v[i] = p + 3 < n ? *reinterpret_cast<const floatx4*>(sc + p) : floatx4{0.f, 0.f, 0.f, 0.f};
+    if (p + 3 >= n) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[i][e] = p + e < n ? sc[p + e] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPerThread / 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[4 * i + e] = p0 + 4 * i + e < n ? fkey(v[i][e]) : 0u;   // 0: below every key
+}
+
 __global__ __launch_bounds__(1024) void dsa_select_kernel(DsaArgs a) {
   __shared__ SelectShared sh;
   const int b = blockIdx.x;
@@ -190,40 +213,50 @@ __global__ __launch_bounds__(1024) void dsa_select_kernel(DsaArgs a) {
   find_threshold(sh, kBins, kTopK);
   const uint32_t b1 = sh.thr_bin;
   uint32_t need = sh.thr_need;
+  const uint32_t n_gt = kTopK - need;                // positions above the bucket, all selected
   const float* sc = a.scores + (size_t)b * a.L;
-  const int per = (n + 1023) / 1024;                 // thread-contiguous position ranges
-  const int p_lo = min(n, tid * per), p_hi = min(n, p_lo + per);
-  uint32_t c_gt = 0, c_eq = 0, tot;
-  for (int p = p_lo; p < p_hi; ++p) {
-    const uint32_t bin = fkey(sc[p]) >> 19;
-    c_gt += bin > b1;
-    c_eq += bin == b1;
-  }
-  uint32_t o_gt = block_excl_scan(c_gt, sh.red, &tot);
-  uint32_t o_eq = block_excl_scan(c_eq, sh.red, &tot);
-  const uint32_t n_gt = kTopK - need;                // elements above the bucket, all selected
-  const uint32_t ncand = tot;
-  const bool in_lds = ncand <= (uint32_t)kCand;
-  for (int p = p_lo; p < p_hi; ++p) {
-    const uint32_t key = fkey(sc[p]);
-    const uint32_t bin = key >> 19;
-    if (bin > b1) {
-      if (o_gt < n_gt) idx[o_gt] = p;
-      ++o_gt;
+  // Pass over the scores: positions above bucket b1 go straight to idx, bucket b1 to the LDS candidates.
+  uint32_t gt_base = 0, eq_base = 0;
+  for (int base = 0; base < n; base += kRound) {
+    uint32_t key[kPerThread];
+    load_round(sc, base, n, key);
+    uint32_t c_gt = 0, c_eq = 0, t_gt, t_eq;
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      c_gt += (key[i] >> 19) > b1;
+      c_eq += (key[i] >> 19) == b1;
     }
-    else if (bin == b1 && in_lds) { sh.cand_key[o_eq] = key; sh.cand_pos[o_eq] = p; ++o_eq; }
+    uint32_t o_gt = gt_base + block_excl_scan(c_gt, sh.red, &t_gt);
+    uint32_t o_eq = eq_base + block_excl_scan(c_eq, sh.red, &t_eq);
+    const int p0 = base + tid * kPerThread;
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      const uint32_t bin = key[i] >> 19;
+      if (bin > b1) {
+        if (o_gt < n_gt) idx[o_gt] = p0 + i;
+        ++o_gt;
+      } else if (bin == b1) {
+        if (o_eq < (uint32_t)kCand) { sh.cand_key[o_eq] = key[i]; sh.cand_pos[o_eq] = p0 + i; }
+        ++o_eq;
+      }
+    }
+    gt_base += t_gt;
+    eq_base += t_eq;
   }
-  // Candidate ranges: in LDS, or (too many ties for LDS) the scores again, filtered to the bucket.
-  const int cper = in_lds ? (int)((ncand + 1023) / 1024) : per;
-  const int c_lo = in_lds ? min((int)ncand, tid * cper) : p_lo;
-  const int c_hi = in_lds ? min((int)ncand, c_lo + cper) : p_hi;
+  const uint32_t ncand = eq_base;
+  const bool in_lds = ncand <= (uint32_t)kCand;
+  // Candidate walk: LDS list (thread-contiguous ranges), or (too many ties for LDS) the scores again.
+  const int cper = (int)((ncand + 1023) / 1024);
+  const int c_lo = min((int)ncand, tid * cper), c_hi = min((int)ncand, c_lo + cper);
+  const int sper = (n + 1023) / 1024;
+  const int s_lo = min(n, tid * sper), s_hi = min(n, s_lo + sper);
   auto for_each = [&](auto&& f) {
-    for (int i = c_lo; i < c_hi; ++i) {
-      if (in_lds) {
-        f(sh.cand_key[i], sh.cand_pos[i]);
-      } else {
-        const uint32_t key = fkey(sc[i]);
-        if ((key >> 19) == b1) f(key, i);
+    if (in_lds) {
+      for (int i = c_lo; i < c_hi; ++i) f(sh.cand_key[i], sh.cand_pos[i]);
+    } else {
+      for (int p = s_lo; p < s_hi; ++p) {
+        const uint32_t key = fkey(sc[p]);
+        if ((key >> 19) == b1) f(key, p);
       }
     }
   };

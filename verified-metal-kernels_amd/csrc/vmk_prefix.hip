@@ -190,8 +190,9 @@ static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int
   p.chunk_p = (int)chunk;
   p.nsplit_p = P > 0 ? (int)((P + chunk - 1) / chunk) : 0;
   p.n_prefix_items = (int)(Hkv * p.nrb_p * p.nsplit_p);
-  // Suffix chunks of 512 keys (4 waves x 4 tiles); rows are only the G heads of one request.
-  int64_t cs = 512;
+  // Suffix chunks of up to 2048 keys (a whole suffix at the BASELINE shapes): one long-lived workgroup per
+  // (request, KV head); the hardware dispatcher balances the ragged lengths.  Rows are only the G heads of a request.
+  int64_t cs = 2048;
   if (S < cs) cs = std::max<int64_t>(kTile, (S + kTile - 1) / kTile * kTile);
   p.chunk_s = (int)cs;
   p.nsplit_s = (int)((S + cs - 1) / cs);

@@ -164,9 +164,9 @@ static SpecPlan spec_plan(int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_
   p.nrb = (int)((R + rows_wg - 1) / rows_wg);
   const int64_t base = B * Hkv * p.nrb;
   const int64_t max_split = (L + kTile * p.WK - 1) / (kTile * p.WK);
-  // Key-split workgroups are small (4 waves, 1 per CU by LDS): aim at ~1024; row-split ones carry 32*WR rows and
-  // their fp32 partials grow with the rows, so aim at ~256 and keep partials under ~8 % of the K/V stream.
-  int64_t ns = ((p.rows_mode ? 256 : 1024) + base - 1) / base;
+  // Both kinds hold one CU's LDS: aim at ~256 long-lived workgroups, and keep the fp32 partials (which grow with the
+  // rows) under ~8 % of the K/V stream.
+  int64_t ns = (256 + base - 1) / base;     // about one long-lived workgroup per CU
   const int64_t cap = std::max<int64_t>(1, (int64_t)(0.08 * (double)L / (double)(p.nrb * rows_wg)));
   ns = std::max<int64_t>(1, std::min(ns, std::min(max_split, cap)));
   int64_t chunk = (L + ns - 1) / ns;
