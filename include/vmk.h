@@ -5,8 +5,10 @@
  *   - tensors are dense row-major device buffers, 16-byte aligned; fp16 unless stated otherwise;
  *   - inputs are never written; outputs are fully overwritten;
  *   - `stream` is a hipStream_t (NULL = default stream); the call only enqueues work and returns;
- *   - `workspace` is device memory of at least the size returned by the matching *_workspace_size query; its
- *     contents need no initialisation and are garbage afterwards; two calls sharing one workspace must be ordered;
+ *   - `workspace` is device memory of at least the size returned by the matching *_workspace_size query.  Its first
+ *     VMK_WORKSPACE_HEAD bytes (the head) must be zero before the first call that uses it, and every call leaves the
+ *     head zero again (kernels accumulate histograms and counters into it), so zero it once at allocation; the rest
+ *     needs no initialisation.  Calls sharing one workspace must be ordered (one stream, or synchronised);
  *   - return 0 on success; 1 = rejected arguments (nothing launched), 2 = HIP launch/runtime error; the message of
  *     the last failure on this host thread is returned by vmk_last_error().
  *
@@ -23,6 +25,9 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* Bytes at the start of every workspace that must be zero before first use (see above). */
+#define VMK_WORKSPACE_HEAD ((size_t)2 << 20)
 
 /* Library version (1). */
 int vmk_version(void);
@@ -90,8 +95,8 @@ int vmk_dsa_decode(const void* q, const void* kv, const void* iq, const void* ik
 /* ---------------------------------------------------------------------------------------------- measurement hook
  * No reference counterpart (the reference times whole calls only, bench.py:61-96).  The next launch of kernel
  * `kernel_id` on this host thread is bracketed by hipEventRecord(before) and hipEventRecord(after) on its stream.
- * Ids: 0 spec_partial, 1 spec_combine, 2 prefix_partial, 3 prefix_combine, 4 dsa_indexer, 5 dsa_select,
- *      6 dsa_attn, 7 dsa_combine. */
+ * Ids: 0 spec_partial, 1 spec_combine, 2 prefix_partial, 3 prefix_combine, 4 dsa_indexer, 5 dsa_select (final),
+ *      6 dsa_attn, 7 dsa_combine, 8 dsa_select_scan. */
 int vmk_profile_next(void* before_event, void* after_event, int kernel_id);
 
 /* ---------------------------------------------------------------------------------------------- test hooks

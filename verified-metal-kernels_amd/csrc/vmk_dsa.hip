@@ -4,9 +4,10 @@
 // (kernels/dsa_opus55_v7.py:27-98, 100-307, 309-535, 553-605, 629-727) behind the
 // kernel(q, kv, iq, ik, w, lens) contract of ops/dsa.py:1-9.
 //
-// Workspace layout:
+// Workspace layout (after the zero-invariant head, which holds the histograms when B <= 64):
 //   hist   : B x 8192 uint32   per-request histogram of the top 13 bits of the score key
-//   scores : B x L    float    indexer scores
+//   scores : B x Ls   float    indexer scores (Ls = L rounded up to whole 4096-position scan slices)
+//   glist, ekey, epos : B x Ls select_scan's per-slice compacted lists; gcnt, ecnt: their lengths
 //   po/pml : attention partials [b][head block][chunk][32][512] and [..][32][2]
 #include "attn_core.h"
 #include "vmk_internal.h"
@@ -19,6 +20,8 @@ constexpr int kIdxWG = 1024;       // positions per indexer workgroup (8 waves x
 constexpr int kChunk = 128;        // selected keys per attention workgroup
 constexpr int kNChunk = kTopK / kChunk;
 constexpr int kCand = 4096;        // LDS candidate capacity of the select kernel
+constexpr int kScanWG = 4096;      // positions per select_scan workgroup (256 threads x 16)
+constexpr int kMaxSlices = 1024;   // select_final handles up to 1024 scan slices (L <= 4M)
 
 struct DsaArgs {
   const f16* q;         // (B, 128, 576)
@@ -31,10 +34,17 @@ struct DsaArgs {
   int* cnt;             // (B,)
   f16* out;             // (B, 128, 512)
   uint32_t* hist;       // (B, 8192)
-  float* scores;        // (B, L)
+  float* scores;        // (B, Ls)
   float* po;            // (B, 4, kNChunk, 32, 512)
   float* pml;           // (B, 4, kNChunk, 32, 2)
-  int B, L;
+  int* glist;           // (B, L) per scan slice: positions above the threshold bucket, in position order
+  uint32_t* ekey;       // (B, L) per scan slice: keys of the threshold bucket's positions, in position order
+  int* epos;            // (B, L) ... and their positions
+  int* gcnt;            // (B, nb) list lengths per slice
+  int* ecnt;            // (B, nb)
+  int B, L, nb;         // nb = scan slices per request
+  int Ls;               // row stride of scores and the scan lists: nb * kScanWG
+  int hist_in_head;     // 1: hist lives in the zero-invariant workspace head (no zero-fill launch needed)
   float sl2;            // attention scale * log2(e)
 };
 
@@ -87,7 +97,7 @@ __global__ __launch_bounds__(512) void dsa_indexer_kernel(DsaArgs a) {
     const float tot = part + xor32(part);
     const int pos = t * kTile + r;
     if (g == 0 && pos < n) {
-      a.scores[(size_t)b * a.L + pos] = tot;
+      a.scores[(size_t)b * a.Ls + pos] = tot;
       atomicAdd(&hist[fkey(tot) >> 19], 1u);
     }
   };
@@ -113,13 +123,18 @@ __global__ __launch_bounds__(512) void dsa_indexer_kernel(DsaArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ select
-// Exact top-2048 per request, one 1024-thread workgroup per request.  Radix digits of the score key: bits 31..19
-// (histogram from the indexer), 18..8 and 7..0 (LDS histograms over the candidates of the threshold bucket).
-// Compaction uses block scans over thread-contiguous position ranges, so the output order (selected positions
-// above the threshold bucket in increasing order, then the bucket's picks in increasing order, ties broken by
-// position) does not depend on scheduling, and neither do the attention sums that follow.
+// Exact top-2048 per request in two launches.  Radix digits of the score key: bits 31..19 (the indexer's histogram),
+// 18..8 and 7..0 (LDS histograms over the threshold bucket's candidates).
+//   select_scan  (4096 positions per workgroup): every workgroup finds the threshold bucket b1 from the histogram,
+//                then compacts its slice: positions above b1 to glist, bucket-b1 (key, position) pairs to ekey/epos;
+//   select_final (one workgroup per request): concatenates the slices' lists in slice order, refines the bucket to
+//                the exact threshold key T and emits the remaining picks.
+// All compaction uses block scans over thread-contiguous position ranges, so the output order (positions above the
+// bucket in increasing order, then the bucket's picks in increasing order, ties at T broken by position) does not
+// depend on scheduling, and neither do the attention sums that follow.
 
-// Block-wide (1024 threads) exclusive prefix sum of v over thread ids; *total receives the sum of all v.
+// Block-wide exclusive prefix sum of v over thread ids (NT threads); *total receives the sum of all v.
+template <int NT>
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint32_t x = v;  // inclusive prefix within the wave
@@ -131,7 +146,8 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
   if (lane == 63) red[wave] = x;
   __syncthreads();
   uint32_t before = 0, all = 0;
-  for (int w2 = 0; w2 < 16; ++w2) {
+#pragma unroll
+  for (int w2 = 0; w2 < NT / 64; ++w2) {
     const uint32_t t = red[w2];
     all += t;
     if (w2 < wave) before += t;
@@ -141,30 +157,23 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
   return before + x - v;
 }
 
-struct SelectShared {
-  uint32_t hist[kBins];
-  uint32_t cand_key[kCand];
-  int cand_pos[kCand];
-  uint32_t red[16];
-  uint32_t thr_bin, thr_need;
-};
-
-// Finds, in hist[0..nbins) (nbins a multiple of 1024), the bin holding the need-th largest element: thr_bin, and
-// thr_need = need minus the count strictly above that bin.  Every thread of the block must call it.
-__device__ void find_threshold(SelectShared& sh, int nbins, uint32_t need) {
-  const int per = nbins / 1024;
-  const int lo = (1023 - threadIdx.x) * per;        // thread 0 owns the highest bins: a prefix scan runs top-down
+// Finds, in hist[0..nbins) (nbins a multiple of NT), the bin holding the need-th largest element: out[0] = bin,
+// out[1] = need minus the count strictly above that bin.  Every thread of the block must call it.
+template <int NT>
+__device__ void find_threshold(const uint32_t* hist, int nbins, uint32_t need, uint32_t* red, uint32_t* out) {
+  const int per = nbins / NT;
+  const int lo = (NT - 1 - threadIdx.x) * per;      // thread 0 owns the highest bins: a prefix scan runs top-down
   uint32_t local = 0;
-  for (int i = 0; i < per; ++i) local += sh.hist[lo + i];
+  for (int i = 0; i < per; ++i) local += hist[lo + i];
   uint32_t total;
-  const uint32_t above = block_excl_scan(local, sh.red, &total);
+  const uint32_t above = block_excl_scan<NT>(local, red, &total);
   if (above < need && above + local >= need) {
     uint32_t acc = above;
     for (int i = per - 1; i >= 0; --i) {
-      const uint32_t c = sh.hist[lo + i];
+      const uint32_t c = hist[lo + i];
       if (acc + c >= need) {
-        sh.thr_bin = lo + i;
-        sh.thr_need = need - acc;
+        out[0] = lo + i;
+        out[1] = need - acc;
         break;
       }
       acc += c;
@@ -173,117 +182,148 @@ __device__ void find_threshold(SelectShared& sh, int nbins, uint32_t need) {
   __syncthreads();
 }
 
-// Scores are read in rounds of 32768 positions: thread t owns the 32 consecutive positions base + 32t .. +31 of a
-// round, loaded as 8 float4 at once and kept in registers for the count and emit passes of that round.
-constexpr int kRound = 32768;
-constexpr int kPerThread = kRound / 1024;
-
-__device__ __forceinline__ void load_round(const float* sc, int base, int n, uint32_t (&key)[kPerThread]) {
-  const int p0 = base + threadIdx.x * kPerThread;
-  floatx4 v[kPerThread / 4];
-#pragma unroll
-  for (int i = 0; i < kPerThread / 4; ++i) {
-    const int p = p0 + 4 * i;
-    v[i] = p + 3 < n ? *reinterpret_cast<const floatx4*>(sc + p) : floatx4{0.f, 0.f, 0.f, 0.f};
-    if (p + 3 >= n) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[i][e] = p + e < n ? sc[p + e] : 0.f;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < kPerThread / 4; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) key[4 * i + e] = p0 + 4 * i + e < n ? fkey(v[i][e]) : 0u;   // 0: below every key
-}
-
-__global__ __launch_bounds__(1024) void dsa_select_kernel(DsaArgs a) {
-  __shared__ SelectShared sh;
-  const int b = blockIdx.x;
+__global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ uint32_t red[4], thr[2];
+  const int b = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
   const int n = valid_len(a, b);
-  const int tid = threadIdx.x;
-  int* idx = a.idx + (size_t)b * kTopK;
-  if (n <= kTopK) {
-    for (int i = tid; i < kTopK; i += 1024) idx[i] = i < n ? i : 0;
-    if (tid == 0) a.cnt[b] = n;
+  const int base = wg * kScanWG;
+  if (n <= kTopK || base >= n) {                   // whole workgroup: nothing of this slice is selected
+    if (tid == 0) { a.gcnt[b * a.nb + wg] = 0; a.ecnt[b * a.nb + wg] = 0; }
     return;
   }
   const uint32_t* gh = a.hist + (size_t)b * kBins;
-  for (int i = tid; i < kBins; i += 1024) sh.hist[i] = gh[i];
-  __syncthreads();
-  find_threshold(sh, kBins, kTopK);
-  const uint32_t b1 = sh.thr_bin;
-  uint32_t need = sh.thr_need;
-  const uint32_t n_gt = kTopK - need;                // positions above the bucket, all selected
-  const float* sc = a.scores + (size_t)b * a.L;
-  // Pass over the scores: positions above bucket b1 go straight to idx, bucket b1 to the LDS candidates.
-  uint32_t gt_base = 0, eq_base = 0;
-  for (int base = 0; base < n; base += kRound) {
-    uint32_t key[kPerThread];
-    load_round(sc, base, n, key);
-    uint32_t c_gt = 0, c_eq = 0, t_gt, t_eq;
+  for (int i = tid; i < kBins; i += 256) hist[i] = gh[i];
+  // This thread's 16 positions (4 float4), loaded while the threshold is found.
+  const float* sc = a.scores + (size_t)b * a.Ls;
+  const int p0 = base + tid * 16;
+  uint32_t key[16];
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      c_gt += (key[i] >> 19) > b1;
-      c_eq += (key[i] >> 19) == b1;
-    }
-    uint32_t o_gt = gt_base + block_excl_scan(c_gt, sh.red, &t_gt);
-    uint32_t o_eq = eq_base + block_excl_scan(c_eq, sh.red, &t_eq);
-    const int p0 = base + tid * kPerThread;
+  for (int i = 0; i < 4; ++i) {
+    const int p = p0 + 4 * i;
+    const floatx4 v = *reinterpret_cast<const floatx4*>(sc + p);   // rows are padded to whole slices
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      const uint32_t bin = key[i] >> 19;
-      if (bin > b1) {
-        if (o_gt < n_gt) idx[o_gt] = p0 + i;
-        ++o_gt;
-      } else if (bin == b1) {
-        if (o_eq < (uint32_t)kCand) { sh.cand_key[o_eq] = key[i]; sh.cand_pos[o_eq] = p0 + i; }
-        ++o_eq;
-      }
-    }
-    gt_base += t_gt;
-    eq_base += t_eq;
+    for (int e = 0; e < 4; ++e) key[4 * i + e] = fkey(v[e]);
   }
-  const uint32_t ncand = eq_base;
+  const int nv = n - p0;                           // positions p0 + i with i < nv are valid
+  __syncthreads();
+  find_threshold<256>(hist, kBins, kTopK, red, thr);
+  const uint32_t b1 = thr[0];
+  uint32_t c_gt = 0, c_eq = 0, t_gt, t_eq;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    c_gt += i < nv && (key[i] >> 19) > b1;
+    c_eq += i < nv && (key[i] >> 19) == b1;
+  }
+  uint32_t o_gt = block_excl_scan<256>(c_gt, red, &t_gt);
+  uint32_t o_eq = block_excl_scan<256>(c_eq, red, &t_eq);
+  int* gl = a.glist + (size_t)b * a.Ls + base;
+  uint32_t* ek = a.ekey + (size_t)b * a.Ls + base;
+  int* ep = a.epos + (size_t)b * a.Ls + base;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t bin = key[i] >> 19;
+    if (i >= nv) break;
+    if (bin > b1) gl[o_gt++] = p0 + i;
+    else if (bin == b1) { ek[o_eq] = key[i]; ep[o_eq] = p0 + i; ++o_eq; }
+  }
+  if (tid == 0) { a.gcnt[b * a.nb + wg] = (int)t_gt; a.ecnt[b * a.nb + wg] = (int)t_eq; }
+}
+
+struct SelectShared {
+  uint32_t hist[2048];
+  uint32_t cand_key[kCand];
+  int cand_pos[kCand];
+  uint32_t goff[kMaxSlices + 1], eoff[kMaxSlices + 1];
+  uint32_t red[16], thr[2];
+};
+
+// Slice holding list element e, given exclusive offsets off[0..ns] (off[ns] = total).
+__device__ __forceinline__ int slice_of(const uint32_t* off, int ns, uint32_t e) {
+  int lo = 0, hi = ns - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (off[mid] <= e) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
+  __shared__ SelectShared sh;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int n = valid_len(a, b);
+  int* idx = a.idx + (size_t)b * kTopK;
+  uint32_t* gh = a.hist + (size_t)b * kBins;
+  if (n <= kTopK) {
+    for (int i = tid; i < kTopK; i += 1024) idx[i] = i < n ? i : 0;
+    if (a.L > kTopK)
+      for (int i = tid; i < kBins; i += 1024) gh[i] = 0;       // the indexer ran: leave the histogram zero
+    if (tid == 0) a.cnt[b] = n;
+    return;
+  }
+  const int ns = (n + kScanWG - 1) / kScanWG;
+  // Slice offsets of both lists (one slice per thread).
+  const uint32_t g = tid < ns ? (uint32_t)a.gcnt[b * a.nb + tid] : 0u;
+  const uint32_t e = tid < ns ? (uint32_t)a.ecnt[b * a.nb + tid] : 0u;
+  uint32_t n_gt, ncand;
+  const uint32_t go = block_excl_scan<1024>(g, sh.red, &n_gt);
+  const uint32_t eo = block_excl_scan<1024>(e, sh.red, &ncand);
+  if (tid < ns) { sh.goff[tid] = go; sh.eoff[tid] = eo; }
+  if (tid == 0) { sh.goff[ns] = n_gt; sh.eoff[ns] = ncand; }
+  __syncthreads();
+  // Positions above the bucket: the slices' lists back to back.
+  const int* glb = a.glist + (size_t)b * a.Ls;
+  for (uint32_t s = tid; s < n_gt && s < (uint32_t)kTopK; s += 1024) {
+    const int sl = slice_of(sh.goff, ns, s);
+    idx[s] = glb[sl * kScanWG + (s - sh.goff[sl])];
+  }
+  uint32_t need = kTopK - n_gt;                      // picks still to make from the bucket (>= 1)
+  const uint32_t* ekb = a.ekey + (size_t)b * a.Ls;
+  const int* epb = a.epos + (size_t)b * a.Ls;
   const bool in_lds = ncand <= (uint32_t)kCand;
-  // Candidate walk: LDS list (thread-contiguous ranges), or (too many ties for LDS) the scores again.
+  if (in_lds)
+    for (uint32_t c = tid; c < ncand; c += 1024) {
+      const int sl = slice_of(sh.eoff, ns, c);
+      sh.cand_key[c] = ekb[sl * kScanWG + (c - sh.eoff[sl])];
+      sh.cand_pos[c] = epb[sl * kScanWG + (c - sh.eoff[sl])];
+    }
+  // Candidate walk over thread-contiguous ranges of the ordered candidate list (LDS, or global when too many ties).
   const int cper = (int)((ncand + 1023) / 1024);
   const int c_lo = min((int)ncand, tid * cper), c_hi = min((int)ncand, c_lo + cper);
-  const int sper = (n + 1023) / 1024;
-  const int s_lo = min(n, tid * sper), s_hi = min(n, s_lo + sper);
   auto for_each = [&](auto&& f) {
-    if (in_lds) {
-      for (int i = c_lo; i < c_hi; ++i) f(sh.cand_key[i], sh.cand_pos[i]);
-    } else {
-      for (int p = s_lo; p < s_hi; ++p) {
-        const uint32_t key = fkey(sc[p]);
-        if ((key >> 19) == b1) f(key, p);
+    for (int c = c_lo; c < c_hi; ++c) {
+      if (in_lds) {
+        f(sh.cand_key[c], sh.cand_pos[c]);
+      } else {
+        const int sl = slice_of(sh.eoff, ns, (uint32_t)c);
+        const size_t o = (size_t)sl * kScanWG + (c - sh.eoff[sl]);
+        f(ekb[o], epb[o]);
       }
     }
   };
-  __syncthreads();
   for (int i = tid; i < 2048; i += 1024) sh.hist[i] = 0;
   __syncthreads();
   for_each([&](uint32_t key, int) { atomicAdd(&sh.hist[(key >> 8) & 0x7FF], 1u); });
   __syncthreads();
-  find_threshold(sh, 2048, need);
-  const uint32_t b2 = sh.thr_bin;
-  need = sh.thr_need;
+  find_threshold<1024>(sh.hist, 2048, need, sh.red, sh.thr);
+  const uint32_t b2 = sh.thr[0];
+  need = sh.thr[1];
   sh.hist[tid] = 0;
   __syncthreads();
   for_each([&](uint32_t key, int) {
     if (((key >> 8) & 0x7FF) == b2) atomicAdd(&sh.hist[key & 0xFF], 1u);
   });
   __syncthreads();
-  find_threshold(sh, 1024, need);
-  const uint32_t T = (b1 << 19) | (b2 << 8) | sh.thr_bin;
-  const uint32_t need_eq = sh.thr_need;
+  find_threshold<1024>(sh.hist, 1024, need, sh.red, sh.thr);
+  const int sl0 = slice_of(sh.eoff, ns, 0);                        // the bucket is non-empty: need >= 1 of it
+  const uint32_t b1 = ekb[(size_t)sl0 * kScanWG] >> 19;
+  const uint32_t T = (b1 << 19) | (b2 << 8) | sh.thr[0];
+  const uint32_t need_eq = sh.thr[1];
   // Bucket picks: keys above T, then the first need_eq keys equal to T in position order.
   uint32_t c_above = 0, c_tie = 0, above_total, tie_total;
   for_each([&](uint32_t key, int) { c_above += key > T; c_tie += key == T; });
-  uint32_t o_above = block_excl_scan(c_above, sh.red, &above_total);
-  uint32_t o_tie = block_excl_scan(c_tie, sh.red, &tie_total);
-  // Slots: [0, n_gt) above the bucket, then the bucket's keys > T, then need_eq ties.  The guards only matter if
-  // the histogram disagreed with the scores; they keep every write inside this request's 2048 slots.
+  uint32_t o_above = block_excl_scan<1024>(c_above, sh.red, &above_total);
+  uint32_t o_tie = block_excl_scan<1024>(c_tie, sh.red, &tie_total);
   for_each([&](uint32_t key, int p) {
     if (key > T) {
       const uint32_t slot = n_gt + o_above++;
@@ -294,6 +334,7 @@ __global__ __launch_bounds__(1024) void dsa_select_kernel(DsaArgs a) {
       ++o_tie;
     }
   });
+  for (int i = tid; i < kBins; i += 1024) gh[i] = 0;               // leave the histogram zero for the next call
   if (tid == 0) a.cnt[b] = kTopK;
 }
 
@@ -423,17 +464,31 @@ __global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
 }
 
 struct DsaLayout {
-  size_t hist, scores, po, pml, total;
+  size_t hist, scores, glist, ekey, epos, gcnt, ecnt, po, pml, total;
+  bool hist_in_head;
 };
 
+// The per-request histograms live in the zero-invariant workspace head when they fit (B <= 64); the data regions
+// follow the head.
 static DsaLayout dsa_layout(int64_t B, int64_t L) {
   DsaLayout l;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
-  l.hist = 0;
-  l.scores = up(l.hist + (size_t)B * kBins * 4);
-  l.po = up(l.scores + (size_t)B * L * 4);
-  l.pml = up(l.po + (size_t)B * 4 * kNChunk * 32 * kDC * 4);
-  l.total = up(l.pml + (size_t)B * 4 * kNChunk * 32 * 2 * 4) + 256;
+  const size_t hist_bytes = (size_t)B * kBins * 4;
+  l.hist_in_head = hist_bytes <= kWsHead;
+  size_t o = kWsHead;
+  l.hist = l.hist_in_head ? 0 : o;
+  if (!l.hist_in_head) o = up(o + hist_bytes);
+  const int64_t nb = (L + kScanWG - 1) / kScanWG;
+  const size_t row = (size_t)B * nb * kScanWG * 4;     // rows padded to whole scan slices
+  l.scores = o;            o = up(o + row);
+  l.glist = o;             o = up(o + row);
+  l.ekey = o;              o = up(o + row);
+  l.epos = o;              o = up(o + row);
+  l.gcnt = o;              o = up(o + (size_t)B * nb * 4);
+  l.ecnt = o;              o = up(o + (size_t)B * nb * 4);
+  l.po = o;                o = up(o + (size_t)B * 4 * kNChunk * 32 * kDC * 4);
+  l.pml = o;               o = up(o + (size_t)B * 4 * kNChunk * 32 * 2 * 4);
+  l.total = o + 256;
   return l;
 }
 
@@ -445,25 +500,39 @@ static int dsa_fill_args(DsaArgs& a, const void* q, const void* kv, const void* 
   a.lens = (const int*)lens; a.out = (f16*)out; a.idx = (int*)idx; a.cnt = (int*)cnt;
   a.hist = (uint32_t*)(base + lay.hist);
   a.scores = (float*)(base + lay.scores);
+  a.glist = (int*)(base + lay.glist);
+  a.ekey = (uint32_t*)(base + lay.ekey);
+  a.epos = (int*)(base + lay.epos);
+  a.gcnt = (int*)(base + lay.gcnt);
+  a.ecnt = (int*)(base + lay.ecnt);
   a.po = (float*)(base + lay.po);
   a.pml = (float*)(base + lay.pml);
   a.B = (int)B; a.L = (int)L;
+  a.nb = (int)((L + kScanWG - 1) / kScanWG);
+  a.Ls = a.nb * kScanWG;
+  a.hist_in_head = lay.hist_in_head ? 1 : 0;
   a.sl2 = (float)(1.0 / sqrt(192.0)) * kLog2e;
   return 0;
 }
 
 static int launch_index_select(const DsaArgs& a, hipStream_t s) {
   if (a.L > kTopK) {
-    hipLaunchKernelGGL(dsa_hist_zero_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
-    VMK_CHECK_HIP(hipGetLastError());
+    if (!a.hist_in_head) {
+      hipLaunchKernelGGL(dsa_hist_zero_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
+      VMK_CHECK_HIP(hipGetLastError());
+    }
     prof_before(kKDsaIndexer, s);
     hipLaunchKernelGGL(dsa_indexer_kernel, dim3((unsigned)((a.L + kIdxWG - 1) / kIdxWG), (unsigned)a.B), dim3(512),
                        0, s, a);
     prof_after(kKDsaIndexer, s);
     VMK_CHECK_HIP(hipGetLastError());
+    prof_before(kKDsaSelectScan, s);
+    hipLaunchKernelGGL(dsa_select_scan_kernel, dim3((unsigned)a.nb, (unsigned)a.B), dim3(256), 0, s, a);
+    prof_after(kKDsaSelectScan, s);
+    VMK_CHECK_HIP(hipGetLastError());
   }
   prof_before(kKDsaSelect, s);
-  hipLaunchKernelGGL(dsa_select_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
+  hipLaunchKernelGGL(dsa_select_final_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
   prof_after(kKDsaSelect, s);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
@@ -491,7 +560,7 @@ extern "C" size_t vmk_dsa_workspace_size(int64_t B, int64_t L) {
 }
 
 #define DSA_COMMON_CHECKS()                                                                    \
-  VMK_CHECK(B > 0 && L > 0 && L < (1 << 30) && B < (1 << 20), "bad B or L");                  \
+  VMK_CHECK(B > 0 && L > 0 && L <= (int64_t)kMaxSlices * kScanWG && B < (1 << 20), "bad B or L (L <= 4M)"); \
   VMK_CHECK(workspace && ws_bytes >= vmk_dsa_workspace_size(B, L),                             \
             "workspace too small (query vmk_dsa_workspace_size)")
 

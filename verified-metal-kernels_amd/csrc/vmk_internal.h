@@ -10,10 +10,14 @@ void set_error(const char* fmt, ...);
 // Kernel ids of the measurement hook (vmk_profile_next).
 enum KernelId {
   kKSpecPartial = 0, kKSpecCombine = 1, kKPrefixPartial = 2, kKPrefixCombine = 3,
-  kKDsaIndexer = 4, kKDsaSelect = 5, kKDsaAttn = 6, kKDsaCombine = 7,
+  kKDsaIndexer = 4, kKDsaSelect = 5, kKDsaAttn = 6, kKDsaCombine = 7, kKDsaSelectScan = 8,
 };
 void prof_before(int kernel_id, hipStream_t s);
 void prof_after(int kernel_id, hipStream_t s);
+
+// Every workspace starts with a head of kWsHead bytes that must be zero before the first call and that every call
+// leaves zero again (used for histograms and counters that kernels accumulate into); data regions follow it.
+constexpr size_t kWsHead = (size_t)2 << 20;
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline void* align_up(void* p, size_t a) { return (void*)(((uintptr_t)p + a - 1) & ~(uintptr_t)(a - 1)); }
 }  // namespace vmk

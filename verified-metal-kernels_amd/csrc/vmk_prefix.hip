@@ -213,7 +213,7 @@ extern "C" size_t vmk_prefix_workspace_size(int64_t N, int64_t Hq, int64_t Hkv, 
   (void)ragged;
   if (N <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || D != 128 || P < 0 || S < 0 || P + S <= 0) return 0;
   PrefixPlan p = prefix_plan(N, Hq, Hkv, P, S);
-  return (p.po_p + p.pml_p + p.po_s + p.pml_s) * sizeof(float) + 4 * 256;
+  return kWsHead + (p.po_p + p.pml_p + p.po_s + p.pml_s) * sizeof(float) + 4 * 256;
 }
 
 extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, const void* ks, const void* vs,
@@ -237,7 +237,7 @@ extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, 
   a.q = (const f16*)q; a.kp = (const f16*)kp; a.vp = (const f16*)vp; a.ks = (const f16*)ks; a.vs = (const f16*)vs;
   a.slens = ragged ? (const int*)slens : nullptr;
   a.out = (f16*)out;
-  a.po_p = (float*)align_up(workspace, 256);
+  a.po_p = (float*)align_up((char*)workspace + kWsHead, 256);
   a.pml_p = (float*)align_up(a.po_p + p.po_p, 256);
   a.po_s = (float*)align_up(a.pml_p + p.pml_p, 256);
   a.pml_s = (float*)align_up(a.po_s + p.po_s, 256);

@@ -186,7 +186,7 @@ using namespace vmk;
 extern "C" size_t vmk_spec_workspace_size(int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L) {
   if (B <= 0 || kd <= 0 || Hkv <= 0 || Hq % Hkv || D != 128 || L < kd) return 0;
   SpecPlan p = spec_plan(B, kd, Hq, Hkv, L);
-  return (p.po_floats + p.pml_floats) * sizeof(float) + 256;
+  return kWsHead + (p.po_floats + p.pml_floats) * sizeof(float) + 256;
 }
 
 extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out,
@@ -206,7 +206,7 @@ extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, cons
   SpecArgs a;
   a.q = (const f16*)q; a.k = (const f16*)k; a.v = (const f16*)v; a.bits = (const uint32_t*)mask_words;
   a.out = (f16*)out;
-  a.part_o = (float*)align_up(workspace, 256);
+  a.part_o = (float*)align_up((char*)workspace + kWsHead, 256);
   a.part_ml = a.part_o + p.po_floats;
   a.B = (int)B; a.kd = (int)kd; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = (int)W;
   a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;

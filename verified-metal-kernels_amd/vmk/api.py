@@ -26,12 +26,15 @@ def device_ok(device):
 
 
 def workspace(nbytes, device):
-    """A cached uint8 buffer of at least `nbytes` on `device` (grown, never shrunk)."""
+    """A cached uint8 buffer of at least `nbytes` on `device` (grown, never shrunk).
+
+    Allocated zeroed: libvmk requires the workspace head (its first 2 MiB) to be zero before the first call, and
+    every call leaves it zero again."""
     dev = torch.device(device)
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=dev)
+        buf = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=dev)
         _ws[key] = buf
     return buf
 

@@ -57,7 +57,8 @@ def load():
 
 # Kernel ids of vmk_profile_next (include/vmk.h).
 KERNEL_IDS = {"spec_partial": 0, "spec_combine": 1, "prefix_partial": 2, "prefix_combine": 3,
-              "dsa_indexer": 4, "dsa_select": 5, "dsa_attn": 6, "dsa_combine": 7}
+              "dsa_indexer": 4, "dsa_select": 5, "dsa_attn": 6, "dsa_combine": 7,
+              "dsa_select_scan": 8}
 
 
 def exported_symbols():
