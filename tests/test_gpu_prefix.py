@@ -11,7 +11,10 @@ pytestmark = pytest.mark.gpu
 
 CASES = [(s, d, 7 + i) for i, (s, d) in enumerate(prefix.FUZZ)] + [(s, d, 40 + i) for i, (s, d) in
                                                                    enumerate(prefix.EXTRA)]
-CASES += [(dict(N=8, P=2048, S=256), "randn", 100), (dict(N=64, P=1000, S=300, S_min=1), "outlier", 101)]
+CASES += [(dict(N=8, P=2048, S=256), "randn", 100), (dict(N=64, P=1000, S=300, S_min=1), "outlier", 101),
+          # many rows per KV head with suffixes longer than one suffix item (separate merge launch), and with
+          # empty suffixes (rows made of the prefix alone)
+          (dict(N=20, P=3000, S=2500, S_min=1), "randn", 102), (dict(N=40, P=500, S=8, S_min=0), "randn", 103)]
 
 
 @pytest.mark.parametrize("shape,dist,seed", CASES)

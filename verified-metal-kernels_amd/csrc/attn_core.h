@@ -240,77 +240,76 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
 
 // One tile from a stage: S^T = K.Q^T from the K rows, masked online softmax, O^T += V^T.P^T with the V^T operand read
 // transposed from the V rows (rows of keys outside the sequence were loaded from g_zero_row).
+// Read schedule: the 8 K operands and the first 4 transposed V halves are issued up front (12 <= 15 outstanding
+// LDS reads, the counter's limit), the other 12 V halves two after each of the first six QK MFMAs, so their latency
+// hides behind the QK chain and the softmax instead of being paid read by read.
 template <class Src>
 __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)[8], const char* __restrict__ stage,
                                                  const Src& src, int key0, int lane) {
   const int r = lane & 31, g = lane >> 5;
-  floatx16 s = floatx16{};
+  u32x4 kk[8];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const u32x4 k = *reinterpret_cast<const u32x4*>(stage + r * 256 + (((8 * g + t) ^ swz(r)) << 4));
-    s = mfma32(as_h8(k), qb[t], s);
-  }
-  src.mask_scale(s, key0, g);
-  half8 pb[2];
-  softmax_update(st, s, pb);
+  for (int t = 0; t < 8; ++t) kk[t] = *reinterpret_cast<const u32x4*>(stage + r * 256 + (((8 * g + t) ^ swz(r)) << 4));
   // V^T operand of (d-tile dt, step t): source lane l addresses row 16t + 8rr + 4g + ((l & 15) >> 2) at head-dim
   // 32dt + 16((l >> 4) & 1) + 4(l & 3); the transposed read then gives lane l the dim 32dt + (l & 31) of the four
   // keys 16t + 8rr + 4g + e, e = 0..3, which are exactly the keys of P^T's elements 4rr..4rr+3.
   const char* vbase = stage + 8192;
   const int e = (lane & 15) >> 2, hc = (lane >> 4) & 1, a4 = lane & 3;
+  u32x2 vv[4][2][2];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
+  for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      u32x2 part[2];
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
         const int row = 16 * t + 8 * rr + 4 * g + e;
         const int col = 32 * dt + 16 * hc + 4 * a4;                  // halfs
         const int chunk = (col >> 3) ^ swz(row);
-        part[rr] = lds_read_tr16(vbase + row * 256 + (chunk << 4) + ((col & 7) << 1));
+        vv[dt][t][rr] = lds_read_tr16(vbase + row * 256 + (chunk << 4) + ((col & 7) << 1));
       }
-      const half8 va = as_h8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});
+  floatx16 s = floatx16{};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) s = mfma32(as_h8(kk[t]), qb[t], s);
+  __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);     // DS reads: K operands, V halves of d-tile 0
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one QK MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);    // two more V halves
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  src.mask_scale(s, key0, g);
+  half8 pb[2];
+  softmax_update(st, s, pb);
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const half8 va = as_h8(u32x4{vv[dt][t][0][0], vv[dt][t][0][1], vv[dt][t][1][0], vv[dt][t][1][1]});
       st.o[dt] = mfma32(va, pb[t], st.o[dt]);
     }
-  }
 }
 
-// One wave's walk over the tiles t0, t0+tstep, ... (< ntiles) of [kbeg, ...), double-buffered in two private stages.
+// One wave's walk over the tiles t0, t0+tstep, ... (< ntiles) of [kbeg, ...) through a private ring of NS stages
+// (NS - 1 tiles in flight while one is computed; NS <= 4 keeps the wait counts within vmcnt's range).
 // The key source `src` provides, for an absolute key index: krow(key) / vrow(key) (in-bounds row pointers; keys at
 // or past kend give g_zero_row), kend (one past the last key of the sequence part this walk covers), and
 // mask_scale(s, key0, g) (raw S^T tile -> log2-domain scores, -inf where masked).
-template <class Src>
-__device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], char* __restrict__ s0,
-                                          char* __restrict__ s1, const Src& src, int kbeg, int t0, int ntiles,
-                                          int tstep, int lane) {
-  int t = t0;
-  if (t >= ntiles) return;
-  issue_tile_dma(s0, src, kbeg + t * kTile, lane);
-  while (true) {
-    const int t1 = t + tstep;
-    int key0 = kbeg + t * kTile;
-    if (t1 < ntiles) {
-      issue_tile_dma(s1, src, kbeg + t1 * kTile, lane);
-      wait_vmem<16>();
-    } else {
-      wait_vmem<0>();
-    }
-    compute_tile_lds(st, qb, s0, src, key0, lane);
-    if (t1 >= ntiles) break;
-    const int t2 = t1 + tstep;
-    key0 = kbeg + t1 * kTile;
+template <int NS, class Src>
+__device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], char* __restrict__ ring,
+                                          const Src& src, int kbeg, int t0, int ntiles, int tstep, int lane) {
+  static_assert(NS >= 2 && NS <= 4, "1 to 3 tiles in flight");
+  if (t0 >= ntiles) return;
+  const int n = (ntiles - t0 + tstep - 1) / tstep;          // tiles of this wave
+  for (int j = 0; j < NS - 1 && j < n; ++j)
+    issue_tile_dma(ring + j * kStageBytes, src, kbeg + (t0 + j * tstep) * kTile, lane);
+  for (int j = 0; j < n; ++j) {
+    const int jn = j + NS - 1;
     asm volatile("" ::: "memory");
-    if (t2 < ntiles) {
-      issue_tile_dma(s0, src, kbeg + t2 * kTile, lane);
-      wait_vmem<16>();
-    } else {
-      wait_vmem<0>();
-    }
-    compute_tile_lds(st, qb, s1, src, key0, lane);
-    if (t2 >= ntiles) break;
-    t = t2;
-    asm volatile("" ::: "memory");
+    // Stage jn % NS last held tile j - 1, whose LDS reads all returned before its MFMAs could use them.
+    if (jn < n) issue_tile_dma(ring + (jn % NS) * kStageBytes, src, kbeg + (t0 + jn * tstep) * kTile, lane);
+    wait_vmem_dyn(16 * min(NS - 1, n - 1 - j));
+    compute_tile_lds(st, qb, ring + (j % NS) * kStageBytes, src, kbeg + (t0 + j * tstep) * kTile, lane);
   }
 }
 
@@ -365,15 +364,15 @@ __device__ __forceinline__ void store_partial(float* po, float* pml, const RowSt
   }
 }
 
-// ---- one workgroup of WR x WK waves (WR * WK <= 4, 256 threads launched): WR row blocks of 32 rows, WK waves
+// ---- one workgroup of WR x WK waves (WR * WK * NSW <= 8, 256 threads launched): WR row blocks of 32 rows, WK waves
 // interleaving the tiles of [kbeg, kbeg + 32*ntiles).  Writes one partial (O, m, l) for the WG's 32*WR rows to
-// po (row stride 128 floats) / pml; rows >= nrows are skipped.  smem must hold kAttnSmemBytes: two private stages
-// per wave during the walk, then the cross-wave merge slots.
+// po (row stride 128 floats) / pml; rows >= nrows are skipped.  smem must hold kAttnSmemBytes: NSW private stages
+// per active wave during the walk, then the cross-wave merge slots.
 // qrow(row) returns an in-bounds Q row pointer for a WG-local row (clamped by the caller for rows >= nrows).
-constexpr int kAttnSmemBytes = 4 * 2 * kStageBytes;
+constexpr int kAttnSmemBytes = 8 * kStageBytes;
 static_assert(3 * kSlotFloats * 4 <= kAttnSmemBytes, "merge slots must fit in the stage memory");
 
-template <class Src, class QRow>
+template <int NSW = 2, class Src, class QRow>
 __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow, int nrows, int kbeg, int ntiles,
                                           int WR, int WK, float* po, float* pml) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -384,8 +383,7 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
   load_qt(qb, qrow(row < nrows ? row : 0), lane >> 5, row < nrows);
   RowState st;
   row_state_init(st);
-  char* mine = smem + wave * 2 * kStageBytes;
-  if (active) wave_walk(st, qb, mine, mine + kStageBytes, src, kbeg, wk, ntiles, WK, lane);
+  if (active) wave_walk<NSW>(st, qb, smem + wave * NSW * kStageBytes, src, kbeg, wk, ntiles, WK, lane);
   float* slots = reinterpret_cast<float*>(smem);
   if (WK > 1) {
     __syncthreads();
@@ -454,7 +452,7 @@ __device__ __forceinline__ void combine_row(int nparts, Part part, f16* out) {
 
 // ---- one workgroup of NW waves sharing a ring of kRowsStages stages: wave w owns rows [32w, 32w+32) and every wave
 // consumes every tile of [kbeg, kbeg + 32*ntiles).  Writes the WG's partial (32*NW rows) like attend_wg.
-constexpr int kRowsStages = 4;
+constexpr int kRowsStages = 8;
 constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
 
 template <int NW, class Src, class QRow>

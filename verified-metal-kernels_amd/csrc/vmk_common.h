@@ -29,7 +29,13 @@ __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
+// Value of lane l ^ 32.  v_permlane32_swap exchanges the upper half of its first operand with the lower half of
+// its second: with both operands x, lanes 0-31 find x[l + 32] in the second result and lanes 32-63 find x[l - 32]
+// in the first.  A VALU op, so it neither waits for nor queues behind outstanding LDS reads (ds_bpermute would).
+__device__ __forceinline__ float xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
 
 __device__ __forceinline__ half8 zero_h8() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
 

@@ -32,6 +32,8 @@ struct PrefixArgs {
   int nsplit_s, chunk_s;                    // suffix plan (WR = 1, WK = 4)
   int n_prefix_items;
   int item0;               // first item handled by the key-split kernel (n_prefix_items when prefix rows run apart)
+  int* order;              // (N,) requests by decreasing suffix length (written by the prefix launch), or null
+  int fuse;                // 1: suffix items are whole suffixes and merge the (finished) prefix partials themselves
   float sl2;
 };
 
@@ -64,6 +66,65 @@ __device__ __forceinline__ int suffix_len(const PrefixArgs& a, int n) {
   return a.slens ? min(max(a.slens[n], 0), a.S) : a.S;
 }
 
+// LDS offset of a fused suffix item's partial: past attend_wg's three cross-wave merge slots.
+constexpr int kFuseOff = 3 * kSlotFloats * 4;
+static_assert(kFuseOff + (32 * 128 + 64) * 4 <= kAttnSmemBytes, "fused partial must fit in the stage memory");
+
+// Final output of request n's G rows of KV head h: log-sum-exp merge of the suffix partial (LDS: lpo rows of 128
+// floats, lpml (m, l) pairs) with the prefix partials of those rows.  One wave per row, two head-dims per lane.
+// Lane s holds the (m, l) of prefix partial b0 + s; the O rows are fetched 16 partials at a time with independent
+// loads (one memory round trip per 16), weighted with the lane-broadcast weights.
+__device__ void merge_prefix_rows(const PrefixArgs& a, const float* lpo, const float* lpml, int n, int h) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int np = a.P > 0 ? a.nsplit_p : 0;
+  const int rows_p = 32 * a.WRp;
+  for (int gg = wave; gg < a.G; gg += 4) {
+    const int prow = n * a.G + gg, rb = prow / rows_p, rl = prow % rows_p;
+    const size_t pbase = ((size_t)h * a.nrb_p + rb) * a.nsplit_p * rows_p + rl;   // partial s at pbase + s*rows_p
+    const float ms = lpml[2 * gg], ls = lpml[2 * gg + 1];
+    float M = ms;
+    for (int s0 = lane; s0 < np; s0 += 64) M = fmaxf(M, a.pml_p[(pbase + (size_t)s0 * rows_p) * 2]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    const float Mu = (M == kNegInf) ? 0.f : M;
+    const float ws = fast_exp2(ms - Mu);
+    float den = 0.f;                                       // this lane's share of the prefix denominators
+    float2 num = *reinterpret_cast<const float2*>(lpo + gg * 128 + 2 * lane);
+    num.x *= ws;
+    num.y *= ws;
+    for (int b0 = 0; b0 < np; b0 += 64) {
+      float w = 0.f;
+      if (b0 + lane < np) {
+        const float2 ml = *reinterpret_cast<const float2*>(a.pml_p + (pbase + (size_t)(b0 + lane) * rows_p) * 2);
+        w = fast_exp2(ml.x - Mu);
+        den += w * ml.y;
+      }
+      const int nb = min(64, np - b0);
+      for (int j0 = 0; j0 < nb; j0 += 16) {
+        float2 v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int j = b0 + min(j0 + k, nb - 1);          // clamped: in bounds; weight 0 past nb
+          v[k] = *reinterpret_cast<const float2*>(a.po_p + (pbase + (size_t)j * rows_p) * 128 + 2 * lane);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const float wb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (j0 + k) & 63));
+          const float wj = j0 + k < nb ? wb : 0.f;
+          num.x += wj * v[k].x;
+          num.y += wj * v[k].y;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+    den += ws * ls;
+    f16* out = a.out + ((size_t)n * a.Hq + h * a.G + gg) * 128 + 2 * lane;
+    out[0] = (f16)(num.x / den);
+    out[1] = (f16)(num.y / den);
+  }
+}
+
 __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
   const int item = a.item0 + blockIdx.x;
@@ -91,27 +152,69 @@ __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
   } else {
     const int sitem = item - a.n_prefix_items;
     const int split = sitem % a.nsplit_s;
-    const int nh = sitem / a.nsplit_s;
+    int nh = sitem / a.nsplit_s;
+    if (a.order) nh = a.order[nh / a.Hkv] * a.Hkv + nh % a.Hkv;   // long suffixes are dispatched first
     const int n = nh / a.Hkv, h = nh % a.Hkv;
     const int kbeg = split * a.chunk_s;
     const int sn = suffix_len(a, n);
-    if (kbeg >= sn) return;                               // whole workgroup: nothing of this suffix is here
+    if (kbeg >= sn && !a.fuse) return;                    // whole workgroup: nothing of this suffix is here
     const size_t off = ((size_t)n * a.Hkv + h) * a.S * 128;
     src.kbase = a.ks + off;
     src.vbase = a.vs + off;
     src.kend = min(sn, kbeg + a.chunk_s);
-    const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
-    attend_wg(smem, src, [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; }, a.G, kbeg, ntiles,
-              1, 4, a.po_s + (size_t)sitem * 32 * 128, a.pml_s + (size_t)sitem * 32 * 2);
+    const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
+    auto qrow = [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; };
+    if (!a.fuse) {
+      const size_t pi = (size_t)nh * a.nsplit_s + split;
+      attend_wg(smem, src, qrow, a.G, kbeg, ntiles, 1, 4, a.po_s + pi * 32 * 128, a.pml_s + pi * 32 * 2);
+      return;
+    }
+    // Whole suffix: keep the partial in LDS (past the merge slots) and merge it with the prefix partials here.
+    float* lpo = reinterpret_cast<float*>(smem + kFuseOff);
+    float* lpml = lpo + 32 * 128;
+    attend_wg(smem, src, qrow, a.G, kbeg, ntiles, 1, 4, lpo, lpml);
+    __syncthreads();
+    merge_prefix_rows(a, lpo, lpml, n, h);
   }
 }
 
 // Prefix items when N*G > 64: NW waves own 32 of the N*G rows each and share one LDS ring, so the prefix chunk is
 // streamed from HBM once per 32*NW rows.
+// Counting sort of the requests by decreasing suffix length (256 buckets), run by one workgroup of the prefix
+// launch so the suffix launch can dispatch its longest items first.  Only the schedule depends on it: every item
+// computes the same values whatever order it runs in.
+template <int NT>
+__device__ void build_suffix_order(const PrefixArgs& a, uint32_t* cnt /* LDS, 256 */) {
+  const int tid = threadIdx.x;
+  const int bw = a.S / 256 + 1;
+  for (int i = tid; i < 256; i += NT) cnt[i] = 0;
+  __syncthreads();
+  for (int n = tid; n < a.N; n += NT) atomicAdd(&cnt[255 - suffix_len(a, n) / bw], 1u);
+  __syncthreads();
+  if (tid < 64) {                                          // exclusive scan, 4 buckets per lane
+    uint32_t c[4], t = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { c[k] = cnt[4 * tid + k]; t += c[k]; }
+    uint32_t x = t;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(x, o, 64);
+      if (tid >= o) x += y;
+    }
+    uint32_t run = x - t;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { cnt[4 * tid + k] = run; run += c[k]; }
+  }
+  __syncthreads();
+  for (int n = tid; n < a.N; n += NT) a.order[atomicAdd(&cnt[255 - suffix_len(a, n) / bw], 1u)] = n;
+  __syncthreads();
+}
+
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kRowsSmemBytes];
   const int item = blockIdx.x;
+  if (item == 0 && a.order) build_suffix_order<64 * NW>(a, reinterpret_cast<uint32_t*>(smem));
   const int split = item % a.nsplit_p;
   const int rb = (item / a.nsplit_p) % a.nrb_p;
   const int h = item / (a.nsplit_p * a.nrb_p);
@@ -166,8 +269,9 @@ __global__ __launch_bounds__(128) void prefix_combine_kernel(PrefixArgs a) {
 struct PrefixPlan {
   bool rows_mode;
   int WRp, WKp, nrb_p, nsplit_p, chunk_p, nsplit_s, chunk_s;
-  size_t po_p, pml_p, po_s, pml_s;
+  size_t po_p, pml_p, po_s, pml_s, order;
   int n_prefix_items, n_items;
+  bool fuse;
 };
 
 static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int64_t S) {
@@ -201,6 +305,9 @@ static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int
   p.pml_p = (size_t)p.n_prefix_items * rows_wg * 2;
   p.po_s = (size_t)N * Hkv * p.nsplit_s * 32 * 128;
   p.pml_s = (size_t)N * Hkv * p.nsplit_s * 32 * 2;
+  p.order = (size_t)N;
+  // With the prefix partials finished by an earlier launch, whole-suffix items finish their rows themselves.
+  p.fuse = p.rows_mode && p.n_prefix_items > 0 && p.nsplit_s == 1;
   return p;
 }
 
@@ -213,7 +320,7 @@ extern "C" size_t vmk_prefix_workspace_size(int64_t N, int64_t Hq, int64_t Hkv, 
   (void)ragged;
   if (N <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || D != 128 || P < 0 || S < 0 || P + S <= 0) return 0;
   PrefixPlan p = prefix_plan(N, Hq, Hkv, P, S);
-  return kWsHead + (p.po_p + p.pml_p + p.po_s + p.pml_s) * sizeof(float) + 4 * 256;
+  return kWsHead + (p.po_p + p.pml_p + p.po_s + p.pml_s + p.order) * sizeof(float) + 5 * 256;
 }
 
 extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, const void* ks, const void* vs,
@@ -241,6 +348,9 @@ extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, 
   a.pml_p = (float*)align_up(a.po_p + p.po_p, 256);
   a.po_s = (float*)align_up(a.pml_p + p.pml_p, 256);
   a.pml_s = (float*)align_up(a.po_s + p.po_s, 256);
+  // The schedule order is built by the prefix launch, so only when that runs before the suffix items.
+  a.order = (ragged && p.rows_mode && p.n_prefix_items > 0) ? (int*)align_up(a.pml_s + p.pml_s, 256) : nullptr;
+  a.fuse = p.fuse ? 1 : 0;
   a.N = (int)N; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.P = (int)P; a.S = (int)S;
   a.WRp = p.WRp; a.WKp = p.WKp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;
   a.nsplit_s = p.nsplit_s; a.chunk_s = p.chunk_s; a.n_prefix_items = p.n_prefix_items;
@@ -260,9 +370,11 @@ extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, 
     VMK_CHECK_HIP(hipGetLastError());
   }
   prof_after(kKPrefixPartial, s);
-  prof_before(kKPrefixCombine, s);
-  hipLaunchKernelGGL(prefix_combine_kernel, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
-  prof_after(kKPrefixCombine, s);
-  VMK_CHECK_HIP(hipGetLastError());
+  if (!p.fuse) {
+    prof_before(kKPrefixCombine, s);
+    hipLaunchKernelGGL(prefix_combine_kernel, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
+    prof_after(kKPrefixCombine, s);
+    VMK_CHECK_HIP(hipGetLastError());
+  }
   return 0;
 }
