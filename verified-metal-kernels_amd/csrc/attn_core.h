@@ -86,23 +86,24 @@ __device__ __forceinline__ floatx16 qk_tile(const u32x4 (&kr)[8], const half8 (&
   return acc;
 }
 
-// Online-softmax update with scores already scaled to the log2 domain (masked keys = -inf).  Returns P^T operands.
-// The reference point m only moves when a tile's max exceeds it by more than 8 (a factor 256): p = exp2(s - m) then
+// Online-softmax update of raw scores s (masked keys = -inf); p = exp2(scale * s - m) with m in the scaled (log2)
+// domain, so the scale costs one FMA per score.  Returns P^T operands.
+// The reference point m only moves when a tile's max exceeds it by more than 8 (a factor 256): p = exp2(.) then
 // stays <= 256, which fp16 P and the fp32 sums hold exactly as well as p <= 1, and the O rescale is skipped for the
 // whole wave unless some row moved.  Guard: while a row has seen only -inf, the subtrahend is 0 so exp2(-inf) = 0
-// and a NaN score still yields NaN.
-__device__ __forceinline__ void softmax_update(RowState& st, floatx16& s, half8 (&pb)[2]) {
+// and a NaN score still yields NaN.  scale must be positive (max commutes with it).
+__device__ __forceinline__ void softmax_update(RowState& st, floatx16& s, float scale, half8 (&pb)[2]) {
   float tmax = s[0];
 #pragma unroll
   for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-  tmax = fmaxf(tmax, xor32(tmax));
+  tmax = fmaxf(tmax, xor32(tmax)) * scale;
   const bool move = tmax > st.m + 8.f;          // false for NaN / -inf tiles
   const float mnew = move ? tmax : st.m;
   const float muse = (mnew == kNegInf) ? 0.f : mnew;
   float lsum = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    s[i] = fast_exp2(s[i] - muse);
+    s[i] = fast_exp2(__builtin_fmaf(s[i], scale, -muse));
     lsum += s[i];
   }
   if (__builtin_amdgcn_ballot_w64(move)) {       // rare after the first tiles
@@ -153,14 +154,9 @@ __device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >>
 
 // Waits until at most n of this wave's vector-memory operations are outstanding (loads return in order).  An asm
 // statement with a memory clobber, so the compiler neither drops it nor moves LDS accesses across it.
-template <int n>
-__device__ __forceinline__ void wait_vmem() {
-  if constexpr (n == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if constexpr (n == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else static_assert(n == 0 || n == 16, "unsupported wait count");
-}
-
-// Same with a count known only at run time (0 <= n <= 63; larger counts wait for everything).
+// Waits until at most n (0 <= n <= 63; larger counts wait for everything) of this wave's vector-memory operations
+// are outstanding (loads return in order).  An asm statement with a memory clobber, so the compiler neither drops it
+// nor moves LDS accesses across it.
 __device__ __forceinline__ void wait_vmem_dyn(int n) {
 #define VMK_WAIT_CASE(k) case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
   switch (n) {
@@ -178,54 +174,80 @@ __device__ __forceinline__ void wait_vmem_dyn(int n) {
 // outside the sequence, so a tile's spare rows are zeros and p = 0 never meets a non-finite value of a foreign row.
 __device__ const f16 g_zero_row[128] = {};
 
-// Issues the 16 direct-to-LDS loads of one tile (8 for K, 8 for V).  Instruction j covers rows 4j..4j+3; lane l
-// loads logical chunk (l & 15) ^ (row & 15) of row 4j + (l >> 4), which lands at chunk position l & 15.
-// src.krow/src.vrow clamp the key to the sequence, so every address is in bounds.
-template <class Src>
-__device__ __forceinline__ void issue_tile_dma(char* __restrict__ stage, const Src& src, int key0, int lane) {
-  const int sub = lane >> 4, cl = lane & 15;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = 4 * j + sub;
-    const int c = cl ^ swz(row);
-    __builtin_amdgcn_global_load_lds(VMK_GPTR(src.krow(key0 + row) + 8 * c), VMK_LPTR(stage + j * 1024), 16, 0, 0);
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = 4 * j + sub;
-    const int c = cl ^ swz(row);
-    __builtin_amdgcn_global_load_lds(VMK_GPTR(src.vrow(key0 + row) + 8 * c), VMK_LPTR(stage + 8192 + j * 1024), 16,
-                                     0, 0);
+// Runs f(integral_constant<int, I>) for I = 0 .. N-1 in order while it returns true; false if one returned false.
+template <int I, int N, class F>
+__device__ __forceinline__ bool unroll_while(F& f) {
+  if constexpr (I == N) {
+    return true;
+  } else {
+    if (!f(std::integral_constant<int, I>())) return false;
+    return unroll_while<I + 1, N>(f);
   }
 }
 
-// The share of one tile's 16 DMA instructions issued by wave `part` of `nparts` (instructions part, part+nparts, ..).
-template <class Src>
-__device__ __forceinline__ void issue_tile_dma_part(char* __restrict__ stage, const Src& src, int key0, int lane,
-                                                    int part, int nparts) {
-  const int sub = lane >> 4, cl = lane & 15;
-  for (int i = part; i < 16; i += nparts) {
-    const int j = i & 7;
+// Per-lane byte offsets that are the same for every tile, computed once per walk, so that a tile costs no address
+// arithmetic: the stage is a compile-time index in the unrolled walks and lands in the instructions' immediate
+// offset fields.
+//   dma[j]: this lane's 16 B of DMA instruction j (rows 4j..4j+3) within a tile's 32 rows of 256 B: logical chunk
+//           (l & 15) ^ swz(row) of row 4j + (l >> 4), which lands at chunk position l & 15 of LDS block j;
+//   k[t]:   K operand of step t: row l % 32, logical chunk 8g + t (g = l / 32), from the ring base;
+//   v[2dt + rr]: V^T half rr of d-tile dt at step 0 (step 1 is 16 rows = 4096 bytes further): source row
+//           8rr + 4g + ((l & 15) >> 2), head-dim 32dt + 16((l >> 4) & 1) + 4(l & 3), from the ring base.  swz of
+//           row + 16 equals swz of row, so step 1 really is a constant 4096 further.
+struct TileLanes {
+  uint32_t dma[8];
+  uint32_t k[8];
+  uint32_t v[8];
+};
+
+__device__ __forceinline__ TileLanes tile_lanes(int lane, uint32_t ring_off) {
+  TileLanes tl;
+  const int sub = lane >> 4, cl = lane & 15, r = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
     const int row = 4 * j + sub;
-    const int c = cl ^ swz(row);
-    const f16* g = i < 8 ? src.krow(key0 + row) : src.vrow(key0 + row);
-    __builtin_amdgcn_global_load_lds(VMK_GPTR(g + 8 * c), VMK_LPTR(stage + (i < 8 ? 0 : 8192) + j * 1024), 16, 0,
-                                     0);
+    tl.dma[j] = row * 256 + ((cl ^ swz(row)) << 4);
   }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) tl.k[t] = ring_off + r * 256 + (((8 * g + t) ^ swz(r)) << 4);
+  const int e = (lane & 15) >> 2, hc = (lane >> 4) & 1, a4 = lane & 3;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int row = 8 * rr + 4 * g + e;
+      const int col = 32 * dt + 16 * hc + 4 * a4;                  // halfs
+      const int chunk = (col >> 3) ^ swz(row);
+      tl.v[2 * dt + rr] = ring_off + 8192 + row * 256 + (chunk << 4) + ((col & 7) << 1);
+    }
+  return tl;
 }
 
-// ---- a ring of NS stages shared by the NW waves of a workgroup; every wave consumes every tile.  Each wave issues
-// DPW of the tile's DMA instructions (issue(stage, t) must issue exactly DPW per wave) and waits for its own, and a
-// barrier per tile then makes the whole tile visible and frees the stage the next issue overwrites.
-template <int NS, int DPW, class Issue, class Compute>
-__device__ __forceinline__ void ring_walk(char* ring, int stage_bytes, int ntiles, Issue issue, Compute compute) {
-  for (int t = 0; t < NS - 1 && t < ntiles; ++t) issue(ring + t * stage_bytes, t);
-  for (int t = 0; t < ntiles; ++t) {
-    wait_vmem_dyn(DPW * min(NS - 2, ntiles - 1 - t));
-    __syncthreads();
-    if (t + NS - 1 < ntiles) issue(ring + ((t + NS - 1) % NS) * stage_bytes, t + NS - 1);
-    compute(ring + (t % NS) * stage_bytes, t);
+// DMA instruction i (0..15) of a tile: i < 8 loads K rows 4i..4i+3 into LDS block i, i >= 8 the V rows of block
+// i - 8 into the V half.  A whole tile inside the sequence takes the rows at uniform base + per-lane offset; the last,
+// partial tile of a walk takes keys past src.kend from g_zero_row.
+template <class Src>
+__device__ __forceinline__ void issue_dma(char* __restrict__ stage, const Src& src, int key0, bool full, int i,
+                                          uint32_t off, int lane) {
+  const int j = i & 7;
+  char* dst = stage + (i < 8 ? 0 : 8192) + j * 1024;
+  const char* gp;
+  if (full) {
+    gp = reinterpret_cast<const char*>((i < 8 ? src.kbase : src.vbase) + (size_t)key0 * 128) + off;
+  } else {
+    const int row = 4 * j + (lane >> 4);
+    gp = reinterpret_cast<const char*>(i < 8 ? src.krow(key0 + row) : src.vrow(key0 + row)) + (off & 255);
   }
+  __builtin_amdgcn_global_load_lds(VMK_GPTR(gp), VMK_LPTR(dst), 16, 0, 0);
+}
+
+// All 16 DMA instructions of one tile from one wave.
+template <class Src>
+__device__ __forceinline__ void issue_tile_dma(char* __restrict__ stage, const Src& src, int key0,
+                                               const TileLanes& tl, int lane) {
+  const bool full = key0 + kTile <= src.kend;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) issue_dma(stage, src, key0, full, i, tl.dma[i & 7], lane);
 }
 
 typedef short short4v __attribute__((ext_vector_type(4)));
@@ -238,35 +260,28 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
   return __builtin_bit_cast(u32x2, v);
 }
 
-// One tile from a stage: S^T = K.Q^T from the K rows, masked online softmax, O^T += V^T.P^T with the V^T operand read
-// transposed from the V rows (rows of keys outside the sequence were loaded from g_zero_row).
+// One tile from a stage (stage = LDS base + compile-time stage offset; tl's offsets include the ring base):
+// S^T = K.Q^T from the K rows, masked online softmax, O^T += V^T.P^T with the V^T operand read transposed from the V
+// rows (rows of keys outside the sequence were loaded from g_zero_row).  The transposed read gives lane l the dim
+// 32dt + (l & 31) of the four keys 16t + 8rr + 4g + e, e = 0..3, which are exactly the keys of P^T's elements
+// 4rr..4rr+3.
 // Read schedule: the 8 K operands and the first 4 transposed V halves are issued up front (12 <= 15 outstanding
 // LDS reads, the counter's limit), the other 12 V halves two after each of the first six QK MFMAs, so their latency
 // hides behind the QK chain and the softmax instead of being paid read by read.
 template <class Src>
 __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)[8], const char* __restrict__ stage,
-                                                 const Src& src, int key0, int lane) {
-  const int r = lane & 31, g = lane >> 5;
+                                                 const TileLanes& tl, const Src& src, int key0, int lane) {
+  const int g = lane >> 5;
   u32x4 kk[8];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) kk[t] = *reinterpret_cast<const u32x4*>(stage + r * 256 + (((8 * g + t) ^ swz(r)) << 4));
-  // V^T operand of (d-tile dt, step t): source lane l addresses row 16t + 8rr + 4g + ((l & 15) >> 2) at head-dim
-  // 32dt + 16((l >> 4) & 1) + 4(l & 3); the transposed read then gives lane l the dim 32dt + (l & 31) of the four
-  // keys 16t + 8rr + 4g + e, e = 0..3, which are exactly the keys of P^T's elements 4rr..4rr+3.
-  const char* vbase = stage + 8192;
-  const int e = (lane & 15) >> 2, hc = (lane >> 4) & 1, a4 = lane & 3;
+  for (int t = 0; t < 8; ++t) kk[t] = *reinterpret_cast<const u32x4*>(stage + tl.k[t]);
   u32x2 vv[4][2][2];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-        const int row = 16 * t + 8 * rr + 4 * g + e;
-        const int col = 32 * dt + 16 * hc + 4 * a4;                  // halfs
-        const int chunk = (col >> 3) ^ swz(row);
-        vv[dt][t][rr] = lds_read_tr16(vbase + row * 256 + (chunk << 4) + ((col & 7) << 1));
-      }
+      for (int rr = 0; rr < 2; ++rr) vv[dt][t][rr] = lds_read_tr16(stage + tl.v[2 * dt + rr] + 4096 * t);
   floatx16 s = floatx16{};
 #pragma unroll
   for (int t = 0; t < 8; ++t) s = mfma32(as_h8(kk[t]), qb[t], s);
@@ -278,9 +293,9 @@ __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)
   }
   __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   __builtin_amdgcn_sched_barrier(0);
-  src.mask_scale(s, key0, g);
+  src.mask(s, key0, g);
   half8 pb[2];
-  softmax_update(st, s, pb);
+  softmax_update(st, s, src.scale, pb);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -290,26 +305,79 @@ __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)
     }
 }
 
+// ---- a ring of NS stages shared by the NW waves of a workgroup; every wave consumes every tile.  Wave w issues
+// the tile's DMA instructions w, w + NW, ... (16 / NW of them) and waits for its own, and a barrier per tile then
+// makes the whole tile visible and frees the stage the next issue overwrites.  The walk is unrolled by NS so every
+// stage index is a compile-time constant: compute(S, t) gets it as an integral_constant.
+template <int NS, int NW, class Src, class Compute>
+__device__ __forceinline__ void ring_walk(char* ring, const Src& src, int kbeg, int ntiles, int wave, int lane,
+                                          Compute compute) {
+  constexpr int DPW = 16 / NW;
+  uint32_t dmaw[DPW];                                       // this wave's instructions' lane offsets
+#pragma unroll
+  for (int q = 0; q < DPW; ++q) {
+    const int row = 4 * ((wave + q * NW) & 7) + (lane >> 4);
+    dmaw[q] = row * 256 + (((lane & 15) ^ swz(row)) << 4);
+  }
+  auto issue = [&](char* stage, int t) {
+    const int key0 = kbeg + t * kTile;
+    const bool full = key0 + kTile <= src.kend;
+#pragma unroll
+    for (int q = 0; q < DPW; ++q) issue_dma(stage, src, key0, full, wave + q * NW, dmaw[q], lane);
+  };
+  auto pre = [&](auto S) {
+    if (S >= ntiles) return false;
+    issue(ring + S * kStageBytes, S);
+    return true;
+  };
+  unroll_while<0, NS - 1>(pre);
+  for (int t0 = 0; t0 < ntiles; t0 += NS) {
+    auto step = [&](auto S) {
+      const int t = t0 + S;
+      if (t >= ntiles) return false;
+      wait_vmem_dyn(DPW * min(NS - 2, ntiles - 1 - t));
+      __syncthreads();
+      if (t + NS - 1 < ntiles) issue(ring + ((S + NS - 1) % NS) * kStageBytes, t + NS - 1);
+      compute(S, t);
+      return true;
+    };
+    if (!unroll_while<0, NS>(step)) break;
+  }
+}
+
 // One wave's walk over the tiles t0, t0+tstep, ... (< ntiles) of [kbeg, ...) through a private ring of NS stages
-// (NS - 1 tiles in flight while one is computed; NS <= 4 keeps the wait counts within vmcnt's range).
-// The key source `src` provides, for an absolute key index: krow(key) / vrow(key) (in-bounds row pointers; keys at
-// or past kend give g_zero_row), kend (one past the last key of the sequence part this walk covers), and
-// mask_scale(s, key0, g) (raw S^T tile -> log2-domain scores, -inf where masked).
+// (NS - 1 tiles in flight while one is computed; NS <= 4 keeps the wait counts within vmcnt's range), unrolled by NS
+// so every stage offset is a compile-time constant.  ring is this wave's ring (DMA destinations); base is the LDS
+// address the read offsets of tl are relative to (they include the ring's offset from it).
+// The key source `src` provides: kbase / vbase (row 0 of the sequence part), krow(key) / vrow(key) (in-bounds row
+// pointers; keys at or past kend give g_zero_row), kend, scale (log2-domain softmax scale) and mask(s, key0, g)
+// (masked scores of the raw S^T tile -> -inf).
 template <int NS, class Src>
 __device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], char* __restrict__ ring,
-                                          const Src& src, int kbeg, int t0, int ntiles, int tstep, int lane) {
+                                          const char* __restrict__ base, const TileLanes& tl, const Src& src,
+                                          int kbeg, int t0, int ntiles, int tstep, int lane) {
   static_assert(NS >= 2 && NS <= 4, "1 to 3 tiles in flight");
   if (t0 >= ntiles) return;
   const int n = (ntiles - t0 + tstep - 1) / tstep;          // tiles of this wave
-  for (int j = 0; j < NS - 1 && j < n; ++j)
-    issue_tile_dma(ring + j * kStageBytes, src, kbeg + (t0 + j * tstep) * kTile, lane);
-  for (int j = 0; j < n; ++j) {
-    const int jn = j + NS - 1;
-    asm volatile("" ::: "memory");
-    // Stage jn % NS last held tile j - 1, whose LDS reads all returned before its MFMAs could use them.
-    if (jn < n) issue_tile_dma(ring + (jn % NS) * kStageBytes, src, kbeg + (t0 + jn * tstep) * kTile, lane);
-    wait_vmem_dyn(16 * min(NS - 1, n - 1 - j));
-    compute_tile_lds(st, qb, ring + (j % NS) * kStageBytes, src, kbeg + (t0 + j * tstep) * kTile, lane);
+  auto key_of = [&](int j) { return kbeg + (t0 + j * tstep) * kTile; };
+  auto pre = [&](auto S) {
+    if (S >= n) return false;
+    issue_tile_dma(ring + S * kStageBytes, src, key_of(S), tl, lane);
+    return true;
+  };
+  unroll_while<0, NS - 1>(pre);
+  for (int j0 = 0; j0 < n; j0 += NS) {
+    auto step = [&](auto S) {
+      const int j = j0 + S, jn = j + NS - 1;
+      if (j >= n) return false;
+      asm volatile("" ::: "memory");
+      // Stage (S + NS - 1) % NS last held tile j - 1, whose LDS reads all returned before its MFMAs used them.
+      if (jn < n) issue_tile_dma(ring + ((S + NS - 1) % NS) * kStageBytes, src, key_of(jn), tl, lane);
+      wait_vmem_dyn(16 * min(NS - 1, n - 1 - j));
+      compute_tile_lds(st, qb, base + S * kStageBytes, tl, src, key_of(j), lane);
+      return true;
+    };
+    if (!unroll_while<0, NS>(step)) break;
   }
 }
 
@@ -383,7 +451,9 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
   load_qt(qb, qrow(row < nrows ? row : 0), lane >> 5, row < nrows);
   RowState st;
   row_state_init(st);
-  if (active) wave_walk<NSW>(st, qb, smem + wave * NSW * kStageBytes, src, kbeg, wk, ntiles, WK, lane);
+  const uint32_t ring_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * NSW * kStageBytes;
+  const TileLanes tl = tile_lanes(lane, ring_off);
+  if (active) wave_walk<NSW>(st, qb, smem + ring_off, smem, tl, src, kbeg, wk, ntiles, WK, lane);
   float* slots = reinterpret_cast<float*>(smem);
   if (WK > 1) {
     __syncthreads();
@@ -452,6 +522,9 @@ __device__ __forceinline__ void combine_row(int nparts, Part part, f16* out) {
 
 // ---- one workgroup of NW waves sharing a ring of kRowsStages stages: wave w owns rows [32w, 32w+32) and every wave
 // consumes every tile of [kbeg, kbeg + 32*ntiles).  Writes the WG's partial (32*NW rows) like attend_wg.
+// Eight stages (128 KB): seven tiles in flight, and one workgroup per CU (two would not fit).  LDS reads address
+// stages 0-3 from the per-lane offsets of tl and stages 4-7 from those of tl_hi (64 KB further), so every stage offset
+// fits the 16-bit immediate field.
 constexpr int kRowsStages = 8;
 constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
 
@@ -459,20 +532,18 @@ template <int NW, class Src, class QRow>
 __device__ __forceinline__ void attend_wg_rows(char* smem, const Src& src, QRow qrow, int nrows, int kbeg,
                                                int ntiles, float* po, float* pml) {
   static_assert(16 % NW == 0, "the 16 DMA instructions of a tile must split evenly over the waves");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row = wave * 32 + (lane & 31);
   half8 qb[8];
   load_qt(qb, qrow(row < nrows ? row : 0), lane >> 5, row < nrows);
   RowState st;
   row_state_init(st);
   const bool has_rows = wave * 32 < nrows;
-  ring_walk<kRowsStages, 16 / NW>(
-      smem, kStageBytes, ntiles,
-      [&](char* stage, int t) { issue_tile_dma_part(stage, src, kbeg + t * kTile, lane, wave, NW); },
-      [&](const char* stage, int t) {
-        const int key0 = kbeg + t * kTile;
-        if (has_rows) compute_tile_lds(st, qb, stage, src, key0, lane);
-      });
+  const TileLanes tl = tile_lanes(lane, 0), tl_hi = tile_lanes(lane, 4 * kStageBytes);
+  ring_walk<kRowsStages, NW>(smem, src, kbeg, ntiles, wave, lane, [&](auto S, int t) {
+    if (has_rows)
+      compute_tile_lds(st, qb, smem + (S & 3) * kStageBytes, S < 4 ? tl : tl_hi, src, kbeg + t * kTile, lane);
+  });
   if (has_rows) store_partial(po + (size_t)wave * 32 * 128, pml + wave * 32 * 2, st, lane, nrows - wave * 32);
 }
 

@@ -98,7 +98,7 @@ __global__ __launch_bounds__(64) void debug_tile_kernel(const vmk::f16* q, const
   RowState st;
   row_state_init(st);
   half8 pb[2];
-  softmax_update(st, s, pb);
+  softmax_update(st, s, 1.f, pb);
   pv_tile(st, vt, pb, lane);
   for (int dt = 0; dt < 4; ++dt)
     for (int i = 0; i < 16; ++i) o_out[lane * 64 + dt * 16 + i] = st.o[dt][i];

@@ -415,7 +415,7 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
         s[4 * blk + c] = key < kend ? s[4 * blk + c] * a.sl2 : kNegInf;
       }
     half8 pb[2];
-    softmax_update(st, s, pb);
+    softmax_update(st, s, 1.f, pb);
     pv_tile(st, vt, pb, lane);
   };
   {

@@ -41,22 +41,17 @@ struct RangeSrc {
   const f16* kbase;
   const f16* vbase;
   int kend;
-  float sl2;
+  float scale;
   __device__ const f16* krow(int key) const { return key < kend ? kbase + (size_t)key * 128 : g_zero_row; }
   __device__ const f16* vrow(int key) const { return key < kend ? vbase + (size_t)key * 128 : g_zero_row; }
-  __device__ bool valid(int key) const { return key < kend; }
-  __device__ void mask_scale(floatx16& s, int key0, int g) const {
-    if (key0 + kTile <= kend) {                            // whole tile inside (same for the whole wave)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] *= sl2;
-      return;
-    }
+  __device__ void mask(floatx16& s, int key0, int g) const {
+    if (key0 + kTile <= kend) return;                      // whole tile inside (same for the whole wave)
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int key = key0 + 8 * blk + 4 * g + c;
-        s[4 * blk + c] = key < kend ? s[4 * blk + c] * sl2 : kNegInf;
+        s[4 * blk + c] = key < kend ? s[4 * blk + c] : kNegInf;
       }
   }
 };
@@ -129,7 +124,7 @@ __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
   const int item = a.item0 + blockIdx.x;
   RangeSrc src;
-  src.sl2 = a.sl2;
+  src.scale = a.sl2;
   if (item < a.n_prefix_items) {
     const int split = item % a.nsplit_p;
     const int rb = (item / a.nsplit_p) % a.nrb_p;
@@ -219,7 +214,7 @@ __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
   const int rb = (item / a.nsplit_p) % a.nrb_p;
   const int h = item / (a.nsplit_p * a.nrb_p);
   RangeSrc src;
-  src.sl2 = a.sl2;
+  src.scale = a.sl2;
   const size_t off = (size_t)h * a.P * 128;
   src.kbase = a.kp + off;
   src.vbase = a.vp + off;

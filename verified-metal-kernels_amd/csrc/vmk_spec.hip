@@ -30,7 +30,7 @@ struct SpecSrc {
   const f16* vbase;
   uint32_t mw[kMaskWords];
   int kend, tail0;
-  float sl2;
+  float scale;
   __device__ const f16* krow(int key) const { return key < kend ? kbase + (size_t)key * 128 : g_zero_row; }
   __device__ const f16* vrow(int key) const { return key < kend ? vbase + (size_t)key * 128 : g_zero_row; }
   __device__ uint32_t bit(int j) const {          // bit j of the row's mask, 0 <= j < 32 * kMaskWords
@@ -39,12 +39,8 @@ struct SpecSrc {
     for (int i = 1; i < kMaskWords; ++i) w = (j >> 5) == i ? mw[i] : w;
     return (w >> (j & 31)) & 1u;
   }
-  __device__ void mask_scale(floatx16& s, int key0, int g) const {
-    if (key0 + kTile <= tail0 && key0 + kTile <= kend) {   // whole tile visible (same for the whole wave)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] *= sl2;
-      return;
-    }
+  __device__ void mask(floatx16& s, int key0, int g) const {
+    if (key0 + kTile <= tail0 && key0 + kTile <= kend) return;   // whole tile visible (same for the whole wave)
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
@@ -52,7 +48,7 @@ struct SpecSrc {
         const int key = key0 + 8 * blk + 4 * g + c;
         const uint32_t vis = (key < tail0) | bit(max(key - tail0, 0));
         const bool ok = (key < kend) & (vis != 0u);
-        s[4 * blk + c] = ok ? s[4 * blk + c] * sl2 : kNegInf;
+        s[4 * blk + c] = ok ? s[4 * blk + c] : kNegInf;
       }
   }
 };
@@ -80,7 +76,7 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   const int kbeg = split * a.chunk;
   src.kend = min(a.L, kbeg + a.chunk);
   src.tail0 = a.L - a.kd;
-  src.sl2 = a.sl2;
+  src.scale = a.sl2;
   const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
   const size_t rows_wg = 32 * a.WR;
   attend_wg(smem, src,
@@ -116,7 +112,7 @@ __global__ __launch_bounds__(64 * NW) void spec_partial_rows_kernel(SpecArgs a) 
   const int kbeg = split * a.chunk;
   src.kend = min(a.L, kbeg + a.chunk);
   src.tail0 = a.L - a.kd;
-  src.sl2 = a.sl2;
+  src.scale = a.sl2;
   const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
   const size_t rows_wg = 32 * NW;
   attend_wg_rows<NW>(smem, src,
