@@ -381,36 +381,19 @@ __device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], ch
   }
 }
 
-// Merge another partial state (same lane layout) into st.
-__device__ __forceinline__ void merge_state(RowState& st, const floatx16 (&o2)[4], float m2, float l2) {
-  const float mnew = fmaxf(st.m, m2);
-  const float muse = (mnew == kNegInf) ? 0.f : mnew;
-  const float a1 = fast_exp2(st.m - muse), a2 = fast_exp2(m2 - muse);
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) st.o[dt] = st.o[dt] * a1 + o2[dt] * a2;
-  st.l = st.l * a1 + l2 * a2;
-  st.m = mnew;
-}
+// LDS slot of one wave's state for the cross-wave merge: O as 16 floatx4 per lane, register-major (each b128 access
+// of a wave covers 1 KB contiguously), then (m, l) per lane.
+constexpr int kSlotBytes = 64 * 64 * 4 + 64 * 8;
 
-// LDS slot of one wave's state for the cross-wave merge: register-major so every access is conflict-free.
-constexpr int kSlotFloats = 66 * 64;
-
-__device__ __forceinline__ void state_to_lds(float* slot, const RowState& st, int lane) {
+__device__ __forceinline__ void state_to_slot(char* slot, const RowState& st, int lane) {
+  floatx4* o = reinterpret_cast<floatx4*>(slot);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) slot[(dt * 16 + i) * 64 + lane] = st.o[dt][i];
-  slot[64 * 64 + lane] = st.m;
-  slot[65 * 64 + lane] = st.l;
-}
-
-__device__ __forceinline__ void merge_from_lds(RowState& st, const float* slot, int lane) {
-  floatx16 o2[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o2[dt][i] = slot[(dt * 16 + i) * 64 + lane];
-  merge_state(st, o2, slot[64 * 64 + lane], slot[65 * 64 + lane]);
+    for (int blk = 0; blk < 4; ++blk)
+      o[(dt * 4 + blk) * 64 + lane] =
+          floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]};
+  reinterpret_cast<float2*>(slot + 64 * 64 * 4)[lane] = float2{st.m, st.l};
 }
 
 // Writes one wave's partial (unnormalised O, running max m, row sum l) for its 32 rows:
@@ -432,37 +415,77 @@ __device__ __forceinline__ void store_partial(float* po, float* pml, const RowSt
   }
 }
 
-// ---- one workgroup of WR x WK waves (WR * WK * NSW <= 8, 256 threads launched): WR row blocks of 32 rows, WK waves
-// interleaving the tiles of [kbeg, kbeg + 32*ntiles).  Writes one partial (O, m, l) for the WG's 32*WR rows to
-// po (row stride 128 floats) / pml; rows >= nrows are skipped.  smem must hold kAttnSmemBytes: NSW private stages
-// per active wave during the walk, then the cross-wave merge slots.
+// ---- one workgroup of WR x WK waves (WR * WK = 4, 256 threads): WR row blocks of 32 rows, WK waves interleaving the
+// tiles of [kbeg, kbeg + 32*ntiles) through private rings of NSW stages.  Writes one partial (O, m, l) for the WG's
+// 32*WR rows to po (row stride 128 floats) / pml; rows >= nrows are skipped.  po/pml may point into smem past
+// kAttnSlotsEnd.  Cross-wave merge: every wave parks its state in a slot, then wave wk of row block wr merges
+// d-tiles wk, wk + WK, ... of all WK slots and stores them, so the merge work is spread over all waves.
 // qrow(row) returns an in-bounds Q row pointer for a WG-local row (clamped by the caller for rows >= nrows).
 constexpr int kAttnSmemBytes = 8 * kStageBytes;
-static_assert(3 * kSlotFloats * 4 <= kAttnSmemBytes, "merge slots must fit in the stage memory");
+constexpr int kAttnSlotsEnd = 4 * kSlotBytes;
+static_assert(kAttnSlotsEnd <= kAttnSmemBytes, "merge slots must fit in the stage memory");
 
-template <int NSW = 2, class Src, class QRow>
+template <int WR, int WK, int NSW = 2, class Src, class QRow>
 __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow, int nrows, int kbeg, int ntiles,
-                                          int WR, int WK, float* po, float* pml) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+                                          float* po, float* pml) {
+  static_assert(WR * WK == 4 && WR * WK * NSW <= 8, "four waves, rings within the stage memory");
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wr = wave % WR, wk = wave / WR;
-  const bool active = wave < WR * WK;
-  const int row = wr * 32 + (lane & 31);
+  const int r = lane & 31, g = lane >> 5;
+  const int row = wr * 32 + r;
   half8 qb[8];
-  load_qt(qb, qrow(row < nrows ? row : 0), lane >> 5, row < nrows);
+  load_qt(qb, qrow(row < nrows ? row : 0), g, row < nrows);
   RowState st;
   row_state_init(st);
-  const uint32_t ring_off = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * NSW * kStageBytes;
+  const uint32_t ring_off = (uint32_t)wave * NSW * kStageBytes;
   const TileLanes tl = tile_lanes(lane, ring_off);
-  if (active) wave_walk<NSW>(st, qb, smem + ring_off, smem, tl, src, kbeg, wk, ntiles, WK, lane);
-  float* slots = reinterpret_cast<float*>(smem);
-  if (WK > 1) {
+  wave_walk<NSW>(st, qb, smem + ring_off, smem, tl, src, kbeg, wk, ntiles, WK, lane);
+  const int nvalid = nrows - wr * 32;
+  float* pob = po + (size_t)wr * 32 * 128;
+  float* pmlb = pml + wr * 32 * 2;
+  if constexpr (WK == 1) {
+    store_partial(pob, pmlb, st, lane, nvalid);
+  } else {
+    __syncthreads();                                        // every walk is done: the rings become slots
+    state_to_slot(smem + wave * kSlotBytes, st, lane);
     __syncthreads();
-    if (active && wk > 0) state_to_lds(slots + (wr * (WK - 1) + wk - 1) * kSlotFloats, st, lane);
-    __syncthreads();
-    if (active && wk == 0)
-      for (int o = 1; o < WK; ++o) merge_from_lds(st, slots + (wr * (WK - 1) + o - 1) * kSlotFloats, lane);
+    float mk[WK], M = kNegInf;
+#pragma unroll
+    for (int k = 0; k < WK; ++k) {
+      const float2 ml = reinterpret_cast<const float2*>(smem + (k * WR + wr) * kSlotBytes + 64 * 64 * 4)[lane];
+      mk[k] = ml.x;
+      M = fmaxf(M, ml.x);
+    }
+    const float muse = (M == kNegInf) ? 0.f : M;
+    float ak[WK], l = 0.f;
+#pragma unroll
+    for (int k = 0; k < WK; ++k) {
+      ak[k] = fast_exp2(mk[k] - muse);
+      l += ak[k] * reinterpret_cast<const float2*>(smem + (k * WR + wr) * kSlotBytes + 64 * 64 * 4)[lane].y;
+    }
+#pragma unroll
+    for (int j = 0; j < 4 / WK; ++j) {
+      const int dt = wk + j * WK;
+      floatx4 acc[4];
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) acc[blk] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < WK; ++k) {
+        const floatx4* o = reinterpret_cast<const floatx4*>(smem + (k * WR + wr) * kSlotBytes);
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) acc[blk] += ak[k] * o[(dt * 4 + blk) * 64 + lane];
+      }
+      if (r < nvalid)
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk)
+          *reinterpret_cast<floatx4*>(pob + r * 128 + dt * 32 + 8 * blk + 4 * g) = acc[blk];
+    }
+    const float ltot = l + xor32(l);
+    if (wk == 0 && g == 0 && r < nvalid) {
+      pmlb[2 * r] = M;
+      pmlb[2 * r + 1] = ltot;
+    }
   }
-  if (active && wk == 0) store_partial(po + (size_t)wr * 32 * 128, pml + wr * 32 * 2, st, lane, nrows - wr * 32);
 }
 
 // ---- log-sum-exp merge of the partials of one output row, NT threads, PER head-dims per thread (d = tid + k*NT).

@@ -37,6 +37,35 @@ __device__ __forceinline__ float xor32(float x) {
   return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
+// Wave-wide reduction with DPP moves (VALU only, no LDS): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and
+// row_mirror reduce each row of 16 lanes; row_bcast:15 (into rows 1, 3) and row_bcast:31 (into rows 2, 3) carry the
+// row results up, so lane 63 holds the total, which is returned to every lane.  Lanes a DPP move does not write
+// keep `identity`.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_move(float identity, float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
+}
+
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float x, float identity, Op op) {
+  x = op(x, dpp_move<0xB1, 0xF>(identity, x));
+  x = op(x, dpp_move<0x4E, 0xF>(identity, x));
+  x = op(x, dpp_move<0x141, 0xF>(identity, x));
+  x = op(x, dpp_move<0x140, 0xF>(identity, x));
+  x = op(x, dpp_move<0x142, 0xA>(identity, x));
+  x = op(x, dpp_move<0x143, 0xC>(identity, x));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  return wave_reduce(x, -__builtin_huge_valf(), [](float a, float b) { return fmaxf(a, b); });
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  return wave_reduce(x, 0.f, [](float a, float b) { return a + b; });
+}
+
 __device__ __forceinline__ half8 zero_h8() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
 
 __device__ __forceinline__ half8 as_h8(u32x4 u) { return __builtin_bit_cast(half8, u); }

@@ -32,7 +32,7 @@ struct PrefixArgs {
   int nsplit_s, chunk_s;                    // suffix plan (WR = 1, WK = 4)
   int n_prefix_items;
   int item0;               // first item handled by the key-split kernel (n_prefix_items when prefix rows run apart)
-  int* order;              // (N,) requests by decreasing suffix length (written by the prefix launch), or null
+  int2* order;             // (N,) (request, suffix length) by decreasing length (written by the prefix launch), or null
   int fuse;                // 1: suffix items are whole suffixes and merge the (finished) prefix partials themselves
   float sl2;
 };
@@ -61,8 +61,8 @@ __device__ __forceinline__ int suffix_len(const PrefixArgs& a, int n) {
   return a.slens ? min(max(a.slens[n], 0), a.S) : a.S;
 }
 
-// LDS offset of a fused suffix item's partial: past attend_wg's three cross-wave merge slots.
-constexpr int kFuseOff = 3 * kSlotFloats * 4;
+// LDS offset of a fused suffix item's partial: past attend_wg's cross-wave merge slots.
+constexpr int kFuseOff = kAttnSlotsEnd;
 static_assert(kFuseOff + (32 * 128 + 64) * 4 <= kAttnSmemBytes, "fused partial must fit in the stage memory");
 
 // Final output of request n's G rows of KV head h: log-sum-exp merge of the suffix partial (LDS: lpo rows of 128
@@ -120,6 +120,51 @@ __device__ void merge_prefix_rows(const PrefixArgs& a, const float* lpo, const f
   }
 }
 
+// Prefix partials of one output row held in registers: lane s has (m, l) of split s, and v[j] the lane's two
+// head-dims of split j's O row.  Fetched before a fused suffix item's walk (the prefix launch has finished), so the
+// final merge needs no memory round trip.
+constexpr int kPrefetchSplits = 32;
+struct PrefixRow {
+  float2 ml;
+  float2 v[kPrefetchSplits];
+};
+
+__device__ __forceinline__ void prefetch_prefix_row(const PrefixArgs& a, PrefixRow& pr, int n, int h, int gg,
+                                                    int lane) {
+  const int np = a.nsplit_p, rows_p = 32 * a.WRp;
+  const int prow = n * a.G + gg, rb = prow / rows_p, rl = prow % rows_p;
+  const size_t pbase = ((size_t)h * a.nrb_p + rb) * a.nsplit_p * rows_p + rl;
+  pr.ml = *reinterpret_cast<const float2*>(a.pml_p + (pbase + (size_t)min(lane, np - 1) * rows_p) * 2);
+#pragma unroll
+  for (int j = 0; j < kPrefetchSplits; ++j)
+    pr.v[j] = *reinterpret_cast<const float2*>(a.po_p + (pbase + (size_t)min(j, np - 1) * rows_p) * 128 + 2 * lane);
+}
+
+// Final output of row gg of request n, KV head h, from the suffix partial in LDS and the prefetched prefix row.
+__device__ __forceinline__ void merge_prefetched_row(const PrefixArgs& a, const PrefixRow& pr, const float* lpo,
+                                                     const float* lpml, int n, int h, int gg, int lane) {
+  const int np = a.nsplit_p;
+  const float ms = lpml[2 * gg], ls = lpml[2 * gg + 1];
+  const float M = wave_max(lane < np ? fmaxf(ms, pr.ml.x) : ms);
+  const float Mu = (M == kNegInf) ? 0.f : M;
+  const float ws = fast_exp2(ms - Mu);
+  const float w = lane < np ? fast_exp2(pr.ml.x - Mu) : 0.f;
+  float den = w * pr.ml.y;
+  float2 num = *reinterpret_cast<const float2*>(lpo + gg * 128 + 2 * lane);
+  num.x *= ws;
+  num.y *= ws;
+#pragma unroll
+  for (int j = 0; j < kPrefetchSplits; ++j) {
+    const float wj = j < np ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j)) : 0.f;
+    num.x += wj * pr.v[j].x;
+    num.y += wj * pr.v[j].y;
+  }
+  den = wave_sum(den) + ws * ls;
+  f16* out = a.out + ((size_t)n * a.Hq + h * a.G + gg) * 128 + 2 * lane;
+  out[0] = (f16)(num.x / den);
+  out[1] = (f16)(num.y / den);
+}
+
 __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
   const int item = a.item0 + blockIdx.x;
@@ -137,21 +182,28 @@ __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
     const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
     const int row0 = rb * a.WRp * 32;
     const size_t rows_wg = 32 * a.WRp;
-    attend_wg(smem, src,
-              [&](int r) {
-                const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
-                return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
-              },
-              a.N * a.G - row0, kbeg, ntiles, a.WRp, a.WKp, a.po_p + (size_t)item * rows_wg * 128,
-              a.pml_p + (size_t)item * rows_wg * 2);
+    auto qrow = [&](int r) {
+      const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
+      return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
+    };
+    float* po = a.po_p + (size_t)item * rows_wg * 128;
+    float* pml = a.pml_p + (size_t)item * rows_wg * 2;
+    if (a.WKp == 4)
+      attend_wg<1, 4>(smem, src, qrow, a.N * a.G - row0, kbeg, ntiles, po, pml);
+    else
+      attend_wg<2, 2>(smem, src, qrow, a.N * a.G - row0, kbeg, ntiles, po, pml);
   } else {
     const int sitem = item - a.n_prefix_items;
     const int split = sitem % a.nsplit_s;
-    int nh = sitem / a.nsplit_s;
-    if (a.order) nh = a.order[nh / a.Hkv] * a.Hkv + nh % a.Hkv;   // long suffixes are dispatched first
+    int nh = sitem / a.nsplit_s, sn = 0;
+    if (a.order) {                                        // long suffixes are dispatched first
+      const int2 o = a.order[nh / a.Hkv];
+      nh = o.x * a.Hkv + nh % a.Hkv;
+      sn = o.y;
+    }
     const int n = nh / a.Hkv, h = nh % a.Hkv;
     const int kbeg = split * a.chunk_s;
-    const int sn = suffix_len(a, n);
+    if (!a.order) sn = suffix_len(a, n);
     if (kbeg >= sn && !a.fuse) return;                    // whole workgroup: nothing of this suffix is here
     const size_t off = ((size_t)n * a.Hkv + h) * a.S * 128;
     src.kbase = a.ks + off;
@@ -161,15 +213,24 @@ __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
     auto qrow = [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; };
     if (!a.fuse) {
       const size_t pi = (size_t)nh * a.nsplit_s + split;
-      attend_wg(smem, src, qrow, a.G, kbeg, ntiles, 1, 4, a.po_s + pi * 32 * 128, a.pml_s + pi * 32 * 2);
+      attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, a.po_s + pi * 32 * 128, a.pml_s + pi * 32 * 2);
       return;
     }
     // Whole suffix: keep the partial in LDS (past the merge slots) and merge it with the prefix partials here.
     float* lpo = reinterpret_cast<float*>(smem + kFuseOff);
     float* lpml = lpo + 32 * 128;
-    attend_wg(smem, src, qrow, a.G, kbeg, ntiles, 1, 4, lpo, lpml);
-    __syncthreads();
-    merge_prefix_rows(a, lpo, lpml, n, h);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (a.G <= 4 && a.nsplit_p <= kPrefetchSplits) {          // wave w finishes row w
+      PrefixRow pr;
+      if (wave < a.G) prefetch_prefix_row(a, pr, n, h, wave, lane);
+      attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
+      __syncthreads();
+      if (wave < a.G) merge_prefetched_row(a, pr, lpo, lpml, n, h, wave, lane);
+    } else {
+      attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
+      __syncthreads();
+      merge_prefix_rows(a, lpo, lpml, n, h);
+    }
   }
 }
 
@@ -201,7 +262,10 @@ __device__ void build_suffix_order(const PrefixArgs& a, uint32_t* cnt /* LDS, 25
     for (int k = 0; k < 4; ++k) { cnt[4 * tid + k] = run; run += c[k]; }
   }
   __syncthreads();
-  for (int n = tid; n < a.N; n += NT) a.order[atomicAdd(&cnt[255 - suffix_len(a, n) / bw], 1u)] = n;
+  for (int n = tid; n < a.N; n += NT) {
+    const int len = suffix_len(a, n);
+    a.order[atomicAdd(&cnt[255 - len / bw], 1u)] = int2{n, len};
+  }
   __syncthreads();
 }
 
@@ -300,7 +364,7 @@ static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int
   p.pml_p = (size_t)p.n_prefix_items * rows_wg * 2;
   p.po_s = (size_t)N * Hkv * p.nsplit_s * 32 * 128;
   p.pml_s = (size_t)N * Hkv * p.nsplit_s * 32 * 2;
-  p.order = (size_t)N;
+  p.order = (size_t)2 * N;
   // With the prefix partials finished by an earlier launch, whole-suffix items finish their rows themselves.
   p.fuse = p.rows_mode && p.n_prefix_items > 0 && p.nsplit_s == 1;
   return p;
@@ -344,7 +408,7 @@ extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, 
   a.po_s = (float*)align_up(a.pml_p + p.pml_p, 256);
   a.pml_s = (float*)align_up(a.po_s + p.po_s, 256);
   // The schedule order is built by the prefix launch, so only when that runs before the suffix items.
-  a.order = (ragged && p.rows_mode && p.n_prefix_items > 0) ? (int*)align_up(a.pml_s + p.pml_s, 256) : nullptr;
+  a.order = (ragged && p.rows_mode && p.n_prefix_items > 0) ? (int2*)align_up(a.pml_s + p.pml_s, 256) : nullptr;
   a.fuse = p.fuse ? 1 : 0;
   a.N = (int)N; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.P = (int)P; a.S = (int)S;
   a.WRp = p.WRp; a.WKp = p.WKp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;

@@ -79,13 +79,16 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   src.scale = a.sl2;
   const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
   const size_t rows_wg = 32 * a.WR;
-  attend_wg(smem, src,
-            [&](int r) {
-              const int qr = row0 + r, i = qr / a.G, gg = qr % a.G;
-              return a.q + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128;
-            },
-            R - row0, kbeg, ntiles, a.WR, a.WK, a.part_o + (size_t)item * rows_wg * 128,
-            a.part_ml + (size_t)item * rows_wg * 2);
+  auto qrow = [&](int r) {
+    const int qr = row0 + r, i = qr / a.G, gg = qr % a.G;
+    return a.q + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128;
+  };
+  float* po = a.part_o + (size_t)item * rows_wg * 128;
+  float* pml = a.part_ml + (size_t)item * rows_wg * 2;
+  if (a.WK == 4)
+    attend_wg<1, 4>(smem, src, qrow, R - row0, kbeg, ntiles, po, pml);
+  else
+    attend_wg<2, 2>(smem, src, qrow, R - row0, kbeg, ntiles, po, pml);
 }
 
 // Row-split variant for kd*G > 64 rows: NW waves own 32 rows each and share one LDS ring, so every K/V tile of the
