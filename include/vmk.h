@@ -27,7 +27,7 @@ extern "C" {
 #endif
 
 /* Bytes at the start of every workspace that must be zero before first use (see above). */
-#define VMK_WORKSPACE_HEAD ((size_t)2 << 20)
+#define VMK_WORKSPACE_HEAD ((size_t)4 << 20)
 
 /* Library version (1). */
 int vmk_version(void);

@@ -6,6 +6,7 @@
 //
 // Workspace layout (after the zero-invariant head, which holds the histograms when B <= 64):
 //   hist   : B x 8192 uint32   per-request histogram of the top 13 bits of the score key
+//   chist  : B x 256 uint32    per-request histogram of the top 8 bits
 //   scores : B x Ls   float    indexer scores (Ls = L rounded up to whole 4096-position scan slices)
 //   glist, ekey, epos : B x Ls select_scan's per-slice compacted lists; gcnt, ecnt: their lengths
 //   po/pml : attention partials [b][head block][chunk][32][512] and [..][32][2]
@@ -16,7 +17,11 @@ namespace vmk {
 
 constexpr int kH = 128, kDK = 576, kDC = 512, kHI = 64, kDI = 128, kTopK = 2048;
 constexpr int kBins = 8192;        // first radix digit: key bits 31..19
+constexpr int kCBins = 256;        // coarse bins of the first digit (key bits 31..24)
 constexpr int kIdxWG = 1024;       // positions per indexer workgroup (8 waves x 4 tiles of 32)
+constexpr int kIdxWaves = 8;       // two waves per SIMD hide each other's LDS and MFMA latencies
+constexpr int kIdxStages = 2;      // private DMA ring stages per indexer wave
+constexpr int kIdxStageBytes = 8192;   // one tile: 32 positions x 256 bytes of ik
 constexpr int kChunk = 128;        // selected keys per attention workgroup
 constexpr int kNChunk = kTopK / kChunk;
 constexpr int kCand = 4096;        // LDS candidate capacity of the select kernel
@@ -45,6 +50,7 @@ struct DsaArgs {
   int B, L, nb;         // nb = scan slices per request
   int Ls;               // row stride of scores and the scan lists: nb * kScanWG
   int hist_in_head;     // 1: hist lives in the zero-invariant workspace head (no zero-fill launch needed)
+  uint32_t* chist;      // (B, 256) coarse histogram: 32 first-digit bins per coarse bin (zero-invariant like hist)
   float sl2;            // attention scale * log2(e)
 };
 
@@ -59,80 +65,6 @@ __device__ __forceinline__ int valid_len(const DsaArgs& a, int b) {
 }
 
 // ------------------------------------------------------------------------------------------------ indexer
-// S = iq . ik^T per 32-position tile (M = 64 heads as two 32-row MFMA tiles, N = positions, K = 128 dims), then
-// score = sum_h w[h] * max(S[h], 0) in fp32, and a histogram of fkey(score) >> 19 per request.
-__global__ __launch_bounds__(512) void dsa_indexer_kernel(DsaArgs a) {
-  __shared__ uint32_t hist[kBins];
-  const int b = blockIdx.y;
-  const int n = valid_len(a, b);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 31, g = lane >> 5;
-  for (int i = threadIdx.x; i < kBins; i += 512) hist[i] = 0;
-
-  half8 qa[2][8];
-  float wv[2][16];
-  const f16* iqb = a.iq + (size_t)b * kHI * kDI;
-#pragma unroll
-  for (int ht = 0; ht < 2; ++ht) {
-    load_qt(qa[ht], iqb + (ht * 32 + r) * kDI, g, true);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) wv[ht][i] = a.w[b * kHI + ht * 32 + 8 * (i >> 2) + 4 * g + (i & 3)];
-  }
-  __syncthreads();
-
-  const f16* ikb = a.ik + (size_t)b * a.L * kDI;
-  const int t0 = blockIdx.x * (kIdxWG / kTile) + wave * 4;     // this wave's 4 tiles
-  const int tend = min(t0 + 4, (n + kTile - 1) / kTile);
-  auto tile_ptr = [&](int t) { return ikb + (size_t)min(t * kTile + r, n - 1) * kDI; };
-  auto compute = [&](const u32x4 (&kr)[8], int t) {
-    floatx16 s0 = floatx16{}, s1 = floatx16{};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      s0 = mfma32(qa[0][s], as_h8(kr[s]), s0);
-      s1 = mfma32(qa[1][s], as_h8(kr[s]), s1);
-    }
-    float part = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) part += wv[0][i] * fmaxf(s0[i], 0.f) + wv[1][i] * fmaxf(s1[i], 0.f);
-    const float tot = part + xor32(part);
-    const int pos = t * kTile + r;
-    if (g == 0 && pos < n) {
-      a.scores[(size_t)b * a.Ls + pos] = tot;
-      atomicAdd(&hist[fkey(tot) >> 19], 1u);
-    }
-  };
-  if (t0 < tend) {
-    u32x4 kA[8], kB[8];
-    load_k(kA, tile_ptr(t0), g);
-    int t = t0;
-    while (true) {
-      if (t + 1 < tend) load_k(kB, tile_ptr(t + 1), g);
-      compute(kA, t);
-      if (++t >= tend) break;
-      if (t + 1 < tend) load_k(kA, tile_ptr(t + 1), g);
-      compute(kB, t);
-      if (++t >= tend) break;
-    }
-  }
-  __syncthreads();
-  uint32_t* gh = a.hist + (size_t)b * kBins;
-  for (int i = threadIdx.x; i < kBins; i += 512) {
-    const uint32_t c = hist[i];
-    if (c) atomicAdd(&gh[i], c);
-  }
-}
-
-// ------------------------------------------------------------------------------------------------ select
-// Exact top-2048 per request in two launches.  Radix digits of the score key: bits 31..19 (the indexer's histogram),
-// 18..8 and 7..0 (LDS histograms over the threshold bucket's candidates).
-//   select_scan  (4096 positions per workgroup): every workgroup finds the threshold bucket b1 from the histogram,
-//                then compacts its slice: positions above b1 to glist, bucket-b1 (key, position) pairs to ekey/epos;
-//   select_final (one workgroup per request): concatenates the slices' lists in slice order, refines the bucket to
-//                the exact threshold key T and emits the remaining picks.
-// All compaction uses block scans over thread-contiguous position ranges, so the output order (positions above the
-// bucket in increasing order, then the bucket's picks in increasing order, ties at T broken by position) does not
-// depend on scheduling, and neither do the attention sums that follow.
-
 // Block-wide exclusive prefix sum of v over thread ids (NT threads); *total receives the sum of all v.
 template <int NT>
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
@@ -161,6 +93,12 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
 // out[1] = need minus the count strictly above that bin.  Every thread of the block must call it.
 template <int NT>
 __device__ void find_threshold(const uint32_t* hist, int nbins, uint32_t need, uint32_t* red, uint32_t* out) {
+  // Defaults (bin 0) for a histogram that holds fewer than `need` elements, so callers that index with out[0]
+  // stay in bounds; the barriers of the scan below order these writes before the finder's.
+  if (threadIdx.x == 0) {
+    out[0] = 0;
+    out[1] = 0;
+  }
   const int per = nbins / NT;
   const int lo = (NT - 1 - threadIdx.x) * per;      // thread 0 owns the highest bins: a prefix scan runs top-down
   uint32_t local = 0;
@@ -182,9 +120,127 @@ __device__ void find_threshold(const uint32_t* hist, int nbins, uint32_t need, u
   __syncthreads();
 }
 
+// ik rows of one request as a key source of the DMA tile loader (K half of a stage only).
+struct IkSrc {
+  const f16* kbase;
+  const f16* vbase;
+  int kend;
+  __device__ const f16* krow(int key) const { return key < kend ? kbase + (size_t)key * kDI : g_zero_row; }
+  __device__ const f16* vrow(int key) const { return krow(key); }
+};
+
+// S = iq . ik^T per 32-position tile (M = 64 heads as two 32-row MFMA tiles, N = positions, K = 128 dims), then
+// score = sum_h w[h] * max(S[h], 0) in fp32, and histograms of fkey(score) >> 19 (fine) and >> 24 (coarse) per
+// request.  Each of the 8 waves streams its 4 tiles through a private 2-stage ring of direct-to-LDS loads; the B
+// operand (ik^T) is read from the stage with the attention core's K-operand offsets.
+__global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) {
+  __shared__ __attribute__((aligned(16))) char ring[kIdxWaves * kIdxStages * kIdxStageBytes];
+  __shared__ uint32_t hist2[kBins / 2];                     // two 16-bit bin counts per word (<= 1024 per bin)
+  __shared__ uint32_t chist[kCBins];
+  const int b = blockIdx.y, tid = threadIdx.x;
+  const int n = valid_len(a, b);
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, g = lane >> 5;
+  // Issue order: iq and w loads, then the ring's first tiles, so that the first wait for tile 0 covers both and
+  // their latencies overlap; the histogram is cleared meanwhile behind a barrier that waits for LDS only.
+  half8 qa[2][8];
+  float wv[2][16];
+  const f16* iqb = a.iq + (size_t)b * kHI * kDI;
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht) {
+    load_qt(qa[ht], iqb + (ht * 32 + r) * kDI, g, true);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) wv[ht][i] = a.w[b * kHI + ht * 32 + 8 * (i >> 2) + 4 * g + (i & 3)];
+  }
+
+  IkSrc src;
+  src.kbase = a.ik + (size_t)b * a.L * kDI;
+  src.vbase = src.kbase;
+  src.kend = n;
+  constexpr int kTilesPerWave = kIdxWG / kTile / kIdxWaves;
+  const int t0 = blockIdx.x * (kIdxWG / kTile) + wave * kTilesPerWave;   // this wave's first tile
+  const int nt = max(0, min(kTilesPerWave, (n + kTile - 1) / kTile - t0));
+  const uint32_t ring_off = (uint32_t)wave * kIdxStages * kIdxStageBytes;
+  const TileLanes tl = tile_lanes(lane, ring_off);
+  char* wring = ring + ring_off;
+  float* sc = a.scores + (size_t)b * a.Ls;
+  auto issue = [&](char* stage, int j) {
+    const int key0 = (t0 + j) * kTile;
+    const bool full = key0 + kTile <= n;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) issue_dma(stage, src, key0, full, i, tl.dma[i], lane);
+  };
+  auto compute = [&](const char* stage, int j) {
+    u32x4 kk[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) kk[t] = *reinterpret_cast<const u32x4*>(stage + tl.k[t]);
+    floatx16 s0 = floatx16{}, s1 = floatx16{};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      s0 = mfma32(qa[0][t], as_h8(kk[t]), s0);
+      s1 = mfma32(qa[1][t], as_h8(kk[t]), s1);
+    }
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) part += wv[0][i] * fmaxf(s0[i], 0.f) + wv[1][i] * fmaxf(s1[i], 0.f);
+    const float tot = part + xor32(part);
+    const int pos = (t0 + j) * kTile + r;
+    if (g == 0 && pos < n) {
+      sc[pos] = tot;
+      const uint32_t bin = fkey(tot) >> 19;
+      atomicAdd(&hist2[bin >> 1], 1u << (16 * (bin & 1)));
+      atomicAdd(&chist[bin >> 5], 1u);
+    }
+  };
+  auto pre = [&](auto S) {
+    if (S >= nt) return false;
+    issue(wring + S * kIdxStageBytes, S);
+    return true;
+  };
+  unroll_while<0, kIdxStages - 1>(pre);
+  for (int i = tid; i < kBins / 2; i += 64 * kIdxWaves) hist2[i] = 0;
+  if (tid < kCBins) chist[tid] = 0;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  for (int j0 = 0; j0 < nt; j0 += kIdxStages) {
+    auto step = [&](auto S) {
+      const int j = j0 + S, jn = j + kIdxStages - 1;
+      if (j >= nt) return false;
+      asm volatile("" ::: "memory");
+      if (jn < nt) issue(wring + ((S + kIdxStages - 1) % kIdxStages) * kIdxStageBytes, jn);
+      wait_vmem_dyn(8 * min(kIdxStages - 1, nt - 1 - j));
+      compute(ring + S * kIdxStageBytes, j);
+      return true;
+    };
+    if (!unroll_while<0, kIdxStages>(step)) break;
+  }
+  __syncthreads();
+  uint32_t* gh = a.hist + (size_t)b * kBins;
+  for (int i = tid; i < kBins / 2; i += 64 * kIdxWaves) {
+    const uint32_t c = hist2[i];
+    if (c & 0xFFFFu) atomicAdd(&gh[2 * i], c & 0xFFFFu);
+    if (c >> 16) atomicAdd(&gh[2 * i + 1], c >> 16);
+  }
+  if (tid < kCBins) {
+    const uint32_t c = chist[tid];
+    if (c) atomicAdd(&a.chist[(size_t)b * kCBins + tid], c);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ select
+// Exact top-2048 per request in two launches.  Radix digits of the score key: bits 31..19 (the indexer's histogram),
+// 18..8 and 7..0 (LDS histograms over the threshold bucket's candidates).
+//   select_scan  (4096 positions per workgroup): with the threshold bucket b1 the indexer found, every workgroup
+//                compacts its slice: positions above b1 to glist, bucket-b1 (key, position) pairs to ekey/epos;
+//   select_final (one workgroup per request): concatenates the slices' lists in slice order, refines the bucket to
+//                the exact threshold key T and emits the remaining picks.
+// All compaction uses block scans over thread-contiguous position ranges, so the output order (positions above the
+// bucket in increasing order, then the bucket's picks in increasing order, ties at T broken by position) does not
+// depend on scheduling, and neither do the attention sums that follow.
+
 __global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
-  __shared__ uint32_t hist[kBins];
-  __shared__ uint32_t red[4], thr[2];
+  __shared__ uint32_t cnt[kCBins], red[4], thr[2], b1s;
   const int b = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
   const int n = valid_len(a, b);
   const int base = wg * kScanWG;
@@ -192,9 +248,7 @@ __global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
     if (tid == 0) { a.gcnt[b * a.nb + wg] = 0; a.ecnt[b * a.nb + wg] = 0; }
     return;
   }
-  const uint32_t* gh = a.hist + (size_t)b * kBins;
-  for (int i = tid; i < kBins; i += 256) hist[i] = gh[i];
-  // This thread's 16 positions (4 float4), loaded while the threshold is found.
+  // This thread's 16 positions (4 float4), loaded while the threshold bucket is found.
   const float* sc = a.scores + (size_t)b * a.Ls;
   const int p0 = base + tid * 16;
   uint32_t key[16];
@@ -205,10 +259,25 @@ __global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) key[4 * i + e] = fkey(v[e]);
   }
-  const int nv = n - p0;                           // positions p0 + i with i < nv are valid
+  // Threshold bucket b1: the coarse histogram gives the coarse bin and the picks left in it, its 32 fine bins b1.
+  cnt[tid] = a.chist[(size_t)b * kCBins + tid];
+  if (tid == 0) b1s = 0;
   __syncthreads();
-  find_threshold<256>(hist, kBins, kTopK, red, thr);
-  const uint32_t b1 = thr[0];
+  find_threshold<256>(cnt, kCBins, kTopK, red, thr);
+  if (tid < 64) {
+    const uint32_t* fine = a.hist + (size_t)b * kBins + min(thr[0], (uint32_t)kCBins - 1) * 32;
+    uint32_t v = tid < 32 ? fine[31 - tid] : 0u;            // lane i: fine bin 31 - i (top first)
+    uint32_t x = v;                                          // inclusive prefix from the top
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      const uint32_t y = __shfl_up(x, o, 64);
+      if ((tid & 63) >= o) x += y;
+    }
+    if (tid < 32 && x >= thr[1] && x - v < thr[1]) b1s = thr[0] * 32 + 31 - tid;
+  }
+  __syncthreads();
+  const int nv = n - p0;                           // positions p0 + i with i < nv are valid
+  const uint32_t b1 = b1s;
   uint32_t c_gt = 0, c_eq = 0, t_gt, t_eq;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -256,8 +325,10 @@ __global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
   uint32_t* gh = a.hist + (size_t)b * kBins;
   if (n <= kTopK) {
     for (int i = tid; i < kTopK; i += 1024) idx[i] = i < n ? i : 0;
-    if (a.L > kTopK)
-      for (int i = tid; i < kBins; i += 1024) gh[i] = 0;       // the indexer ran: leave the histogram zero
+    if (a.L > kTopK) {                                      // the indexer ran: leave the histograms zero
+      for (int i = tid; i < kBins; i += 1024) gh[i] = 0;
+      if (tid < kCBins) a.chist[(size_t)b * kCBins + tid] = 0;
+    }
     if (tid == 0) a.cnt[b] = n;
     return;
   }
@@ -334,14 +405,16 @@ __global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
       ++o_tie;
     }
   });
-  for (int i = tid; i < kBins; i += 1024) gh[i] = 0;               // leave the histogram zero for the next call
+  for (int i = tid; i < kBins; i += 1024) gh[i] = 0;               // leave the histograms zero for the next call
+  if (tid < kCBins) a.chist[(size_t)b * kCBins + tid] = 0;
   if (tid == 0) a.cnt[b] = kTopK;
 }
 
-// Zero-fills the per-request histograms before the indexer accumulates into them.
+// Zero-fills the per-request histograms before the indexer accumulates into them (when they are not in the head).
 __global__ __launch_bounds__(1024) void dsa_hist_zero_kernel(DsaArgs a) {
   uint32_t* gh = a.hist + (size_t)blockIdx.x * kBins;
   for (int i = threadIdx.x; i < kBins; i += 1024) gh[i] = 0;
+  if (threadIdx.x < kCBins) a.chist[(size_t)blockIdx.x * kCBins + threadIdx.x] = 0;
 }
 
 // ------------------------------------------------------------------------------------------------ sparse MLA
@@ -464,20 +537,22 @@ __global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
 }
 
 struct DsaLayout {
-  size_t hist, scores, glist, ekey, epos, gcnt, ecnt, po, pml, total;
+  size_t hist, chist, scores, glist, ekey, epos, gcnt, ecnt, po, pml, total;
   bool hist_in_head;
 };
 
-// The per-request histograms live in the zero-invariant workspace head when they fit (B <= 64); the data regions
-// follow the head.
+// The per-request histograms live in the zero-invariant workspace head when they fit (B <= 64: fine histograms in
+// its histogram part, coarse ones in its counter part); otherwise in the data region, zero-filled by a launch.
 static DsaLayout dsa_layout(int64_t B, int64_t L) {
   DsaLayout l;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t hist_bytes = (size_t)B * kBins * 4;
-  l.hist_in_head = hist_bytes <= kWsHead;
+  l.hist_in_head = hist_bytes <= kWsCounters;
   size_t o = kWsHead;
   l.hist = l.hist_in_head ? 0 : o;
   if (!l.hist_in_head) o = up(o + hist_bytes);
+  l.chist = l.hist_in_head ? kWsCounters : o;
+  if (!l.hist_in_head) o = up(o + (size_t)B * kCBins * 4);
   const int64_t nb = (L + kScanWG - 1) / kScanWG;
   const size_t row = (size_t)B * nb * kScanWG * 4;     // rows padded to whole scan slices
   l.scores = o;            o = up(o + row);
@@ -499,6 +574,7 @@ static int dsa_fill_args(DsaArgs& a, const void* q, const void* kv, const void* 
   a.q = (const f16*)q; a.kv = (const f16*)kv; a.iq = (const f16*)iq; a.ik = (const f16*)ik; a.w = (const float*)w;
   a.lens = (const int*)lens; a.out = (f16*)out; a.idx = (int*)idx; a.cnt = (int*)cnt;
   a.hist = (uint32_t*)(base + lay.hist);
+  a.chist = (uint32_t*)(base + lay.chist);
   a.scores = (float*)(base + lay.scores);
   a.glist = (int*)(base + lay.glist);
   a.ekey = (uint32_t*)(base + lay.ekey);
@@ -522,8 +598,8 @@ static int launch_index_select(const DsaArgs& a, hipStream_t s) {
       VMK_CHECK_HIP(hipGetLastError());
     }
     prof_before(kKDsaIndexer, s);
-    hipLaunchKernelGGL(dsa_indexer_kernel, dim3((unsigned)((a.L + kIdxWG - 1) / kIdxWG), (unsigned)a.B), dim3(512),
-                       0, s, a);
+    hipLaunchKernelGGL(dsa_indexer_kernel, dim3((unsigned)((a.L + kIdxWG - 1) / kIdxWG), (unsigned)a.B),
+                       dim3(64 * kIdxWaves), 0, s, a);
     prof_after(kKDsaIndexer, s);
     VMK_CHECK_HIP(hipGetLastError());
     prof_before(kKDsaSelectScan, s);

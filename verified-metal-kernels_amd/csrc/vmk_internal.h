@@ -16,8 +16,10 @@ void prof_before(int kernel_id, hipStream_t s);
 void prof_after(int kernel_id, hipStream_t s);
 
 // Every workspace starts with a head of kWsHead bytes that must be zero before the first call and that every call
-// leaves zero again (used for histograms and counters that kernels accumulate into); data regions follow it.
-constexpr size_t kWsHead = (size_t)2 << 20;
+// leaves zero again (histograms and counters that kernels accumulate into); data regions follow it.
+// Layout of the head: [0, 2 MiB) histograms, [2 MiB, 4 MiB) counters.
+constexpr size_t kWsHead = (size_t)4 << 20;
+constexpr size_t kWsCounters = (size_t)2 << 20;
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline void* align_up(void* p, size_t a) { return (void*)(((uintptr_t)p + a - 1) & ~(uintptr_t)(a - 1)); }
 }  // namespace vmk

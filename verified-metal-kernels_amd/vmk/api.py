@@ -28,7 +28,7 @@ def device_ok(device):
 def workspace(nbytes, device):
     """A cached uint8 buffer of at least `nbytes` on `device` (grown, never shrunk).
 
-    Allocated zeroed: libvmk requires the workspace head (its first 2 MiB) to be zero before the first call, and
+    Allocated zeroed: libvmk requires the workspace head (its first 4 MiB) to be zero before the first call, and
     every call leaves it zero again."""
     dev = torch.device(device)
     key = dev.index if dev.index is not None else torch.cuda.current_device()
