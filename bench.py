@@ -231,6 +231,19 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     return row
 
 
+def measured_traffic(name, dom):
+    """HBM bytes per call of the dominant kernel from the committed PMC summary of this configuration
+    (profiles/<config>_traffic.json, FETCH_SIZE + WRITE_SIZE scaled by a copy-kernel calibration), else None."""
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    if t.get("kernel") != dom["kernel"]:
+        return None
+    return int(t["read_bytes"] + t["write_bytes"])
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -238,6 +251,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="C1,C2,C3,C4,C5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle timings")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="first run a plain streaming kernel that reads BYTES and writes BYTES (torch.bitwise_not "
+                         "on int32), the calibration of the PMC traffic counters")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py measures one MI355X: the three ops run on a single GPU and this build has no multi-GPU path "
@@ -248,6 +264,14 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a ROCm GPU")
     vmk.device_ok("cuda:0")
+    if a.calibrate_copy:
+        x = torch.ones(a.calibrate_copy // 4, dtype=torch.int32, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(2):
+            torch.bitwise_not(x, out=y)
+        torch.cuda.synchronize()
+        del x, y
+        log(f"calibration kernel over {a.calibrate_copy} bytes done")
     want = [c for c in a.configs.split(",") if c]
     rows = {}
     for name, opname, shape, dist in config_table():
@@ -264,7 +288,7 @@ def main():
         config=dict(workload=f"{head_name}: {head['op']} {head['shape']} dist={head['dist']}",
                     us_per_call=head["us_per_call"], pct_peak=head["pct_peak"]),
         roofline=dict(bound="hbm", achieved=dom["gbs"], peak=PEAK_HBM_GBS, unit="GB/s", frac=dom["frac"],
-                      kernel=dom["kernel"], kernel_us=dom["us"], traffic=None),
+                      kernel=dom["kernel"], kernel_us=dom["us"], traffic=measured_traffic(head_name, dom)),
         cpu_baseline={k: v for k, v in head.get("cpu_baseline", {}).items()} or None,
         ops=rows,
         device=torch.cuda.get_device_name(0),

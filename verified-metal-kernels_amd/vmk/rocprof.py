@@ -1,0 +1,100 @@
+"""Short text summaries of rocprofv3 result databases (rocpd sqlite, `-o run` -> run_results.db).
+
+    python -m vmk.rocprof kernels <run_results.db> [name-substring]      per kernel and grid: calls, avg/min/max us
+    python -m vmk.rocprof pmc <run_results.db> [name-substring]          per kernel: average counter value per dispatch
+    python -m vmk.rocprof traffic <fetch.db> <write.db> <copy_bytes>     HBM bytes per call of the dominant kernels
+
+`traffic` reads one FETCH_SIZE run and one WRITE_SIZE run of the same command (rocprofv3 collects each in its own
+pass).  The command must include a plain streaming kernel that reads `copy_bytes` bytes and writes as many
+(bench.py --calibrate-copy runs torch.bitwise_not over int32): the counters' reading for that kernel, divided by its
+true bytes, is the calibration factor applied to every kernel.
+"""
+import sqlite3
+import sys
+from collections import defaultdict
+
+KERNEL_PREFIX = "vmk::"
+
+
+def _short(name):
+    return name.split("(")[0].replace("void ", "").replace(KERNEL_PREFIX, "")
+
+
+def kernels(path, like=KERNEL_PREFIX):
+    db = sqlite3.connect(path)
+    rows = db.execute(
+        "select name, grid_x, grid_y, workgroup_x, count(*), avg(duration), min(duration), max(duration), "
+        "vgpr_count, accum_vgpr_count, lds_size from kernels where name like ? "
+        "group by name, grid_x, grid_y order by name, grid_x", (f"%{like}%",)).fetchall()
+    out = [f"{'kernel':32s} {'grid':>14s} {'wg':>5s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s}"
+           f" {'vgpr':>5s} {'agpr':>5s} {'lds':>7s}"]
+    for name, gx, gy, wgx, n, avg, mn, mx, vg, ag, lds in rows:
+        out.append(f"{_short(name):32s} {f'{gx}x{gy}':>14s} {wgx:>5d} {n:>6d} {avg / 1e3:>10.2f} {mn / 1e3:>10.2f} "
+                   f"{mx / 1e3:>10.2f} {vg:>5d} {ag:>5d} {lds:>7d}")
+    return "\n".join(out)
+
+
+def pmc_table(path, like=""):
+    """{kernel short name: {counter: [per-dispatch values]}} (each value summed over the device's instances)."""
+    db = sqlite3.connect(path)
+    rows = db.execute("select kernel_name, dispatch_id, counter_name, sum(value) from counters_collection "
+                      "where kernel_name like ? group by kernel_name, dispatch_id, counter_name",
+                      (f"%{like}%",)).fetchall()
+    acc = defaultdict(lambda: defaultdict(list))
+    for name, _disp, cname, val in rows:
+        acc[_short(name)][cname].append(val)
+    return acc
+
+
+def pmc(path, like=KERNEL_PREFIX):
+    out = []
+    for name, cs in sorted(pmc_table(path, like).items()):
+        n = max(len(v) for v in cs.values())
+        out.append(f"{name}  ({n} dispatches)")
+        for cname, vals in sorted(cs.items()):
+            out.append(f"    {cname:32s} {sum(vals) / len(vals):16.1f}")
+    return "\n".join(out)
+
+
+def _copy_kernel(table, counter):
+    """The calibration kernel (bench.py --calibrate-copy): the bitwise_not kernel with the largest reading."""
+    cands = [k for k in table if "bitwise_not" in k and counter in table[k]]
+    if not cands:
+        raise SystemExit("no calibration kernel in the run: use bench.py --calibrate-copy")
+    return max(cands, key=lambda k: max(table[k][counter]))
+
+
+def traffic(fetch_db, write_db, copy_bytes):
+    """Per vmk kernel: average calibrated HBM read and write bytes per dispatch."""
+    f, w = pmc_table(fetch_db), pmc_table(write_db)
+    ck = _copy_kernel(f, "FETCH_SIZE")
+    fc = max(f[ck]["FETCH_SIZE"]) * 1024.0                  # the largest copy dispatch is the calibration copy
+    wc = max(w[_copy_kernel(w, "WRITE_SIZE")]["WRITE_SIZE"]) * 1024.0
+    kf, kw = fc / copy_bytes, wc / copy_bytes
+    out = [f"calibration: kernel {ck!r} over {copy_bytes} bytes reads FETCH_SIZE x {kf:.3f}, "
+           f"WRITE_SIZE x {kw:.3f} of its true bytes", f"{'kernel':32s} {'dispatches':>10s} {'read_MB':>10s} "
+           f"{'write_MB':>10s}"]
+    res = {}
+    for name in sorted(f):
+        if name not in w or "FETCH_SIZE" not in f[name] or ck == name:
+            continue
+        if not any(s in name for s in ("prefix", "spec", "dsa")):
+            continue
+        fv, wv = f[name]["FETCH_SIZE"], w[name]["WRITE_SIZE"]
+        rd = sum(fv) / len(fv) * 1024.0 / kf
+        wr = sum(wv) / len(wv) * 1024.0 / kw
+        res[name] = dict(read=rd, write=wr, dispatches=len(fv))
+        out.append(f"{name:32s} {len(fv):>10d} {rd / 1e6:>10.2f} {wr / 1e6:>10.2f}")
+    return "\n".join(out), res, (kf, kw)
+
+
+if __name__ == "__main__":
+    cmd = sys.argv[1] if len(sys.argv) > 1 else ""
+    if cmd == "kernels":
+        print(kernels(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else KERNEL_PREFIX))
+    elif cmd == "pmc":
+        print(pmc(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else KERNEL_PREFIX))
+    elif cmd == "traffic":
+        print(traffic(sys.argv[2], sys.argv[3], int(sys.argv[4]))[0])
+    else:
+        raise SystemExit(__doc__)
