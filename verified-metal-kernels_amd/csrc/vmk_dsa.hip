@@ -418,14 +418,143 @@ __global__ __launch_bounds__(1024) void dsa_hist_zero_kernel(DsaArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ sparse MLA
-// Workgroup = (request b, block of 32 heads, chunk of 128 selected keys); 4 waves.  Wave w owns the QK head-dims
-// [128w, 128w+128) u [512+16w, 512+16w+16) and the value dims [128w, 128w+128): partial S^T tiles are summed
-// through LDS in a fixed order so every wave holds bit-identical scores, softmax state and P.
-constexpr int kSSlot = 16 * 64;    // floats of one wave's partial S^T tile
+// Workgroup = (request b, block of 32 heads, chunk of 128 selected keys); 4 waves.  Every wave computes the full
+// S^T tile (all 576 QK dims, in the same order, so all four hold bit-identical scores, softmax state and P) and owns
+// the value dims [128w, 128w+128) of O.
+// The selected latent rows of a 32-key tile are gathered by direct-to-LDS loads into a 3-stage ring (two tiles in
+// flight while one is computed).  In a stage, row r starts at byte r * kLatStride: 1152 bytes of the row plus 16 of
+// padding, so the 73-chunk stride is odd and 16 consecutive rows at one chunk fall on 16 distinct bank groups
+// (conflict-free K-operand reads).  DMA instruction j fills stage bytes [1024j, 1024j + 1024): lane i's 16 bytes go
+// to slot 64j + i, which is chunk (slot % 73) of row (slot / 73); padding slots and slots past the 32 rows take
+// copies of real chunks.  V^T is read from the same rows with the transposing LDS read.
+constexpr int kSSlot = 16 * 64;          // floats of one wave's partial S^T tile
+constexpr int kLatChunks = kDK / 8;      // 72 chunks of 16 bytes per latent row
+constexpr int kLatStride = (kLatChunks + 1) * 16;           // 1168 bytes
+constexpr int kLatInstr = 40;            // DMA instructions per tile: 10 per wave, >= 32 * 73 / 64 slots
+constexpr int kLatStageBytes = kLatInstr * 1024;
+constexpr int kLatStages = 3;
+static_assert(kLatInstr * 64 >= kTile * (kLatChunks + 1), "a stage holds 32 padded rows");
+
+// Zero latent row: the source of every key past the selected count.
+__device__ const f16 g_zero_latent[kDK] = {};
+
+// The 10 DMA instructions of wave w for the tile at key0.
+__device__ __forceinline__ void dsa_issue_rows(char* __restrict__ stage, const f16* kvb, const int* sidx, int kbeg,
+                                               int kend, int key0, const int (&drow)[10], const int (&dchk)[10],
+                                               int w) {
+#pragma unroll
+  for (int q = 0; q < 10; ++q) {
+    const int key = key0 + drow[q];
+    const f16* row = key < kend ? kvb + (size_t)sidx[key - kbeg] * kDK : g_zero_latent;
+    __builtin_amdgcn_global_load_lds(VMK_GPTR(row + 8 * dchk[q]), VMK_LPTR(stage + (w + 4 * q) * 1024), 16, 0, 0);
+  }
+}
+
+// S^T of the tile in stage over all 576 QK dims (36 MFMAs; the same order in every wave).
+__device__ __forceinline__ floatx16 dsa_qk(const char* __restrict__ stage, const half8 (&qb)[36], int r, int g) {
+  floatx16 s = floatx16{};
+#pragma unroll
+  for (int c = 0; c < 36; ++c) {
+    const u32x4 k = *reinterpret_cast<const u32x4*>(stage + r * kLatStride + (2 * c + g) * 16);
+    s = mfma32(as_h8(k), qb[c], s);
+  }
+  return s;
+}
+
+// O^T += V^T . P^T over this wave's 128 value dims.  V^T operand of (d-tile dt, step tt): source lane l addresses
+// key 16tt + 8rr + 4g + ((l & 15) >> 2) at value dim 128w + 32dt + 16((l >> 4) & 1) + 4(l & 3); the transposed read
+// gives lane l the dim 128w + 32dt + (l & 31) of the four keys 16tt + 8rr + 4g + e, e = 0..3, the keys of P^T's
+// elements 4rr..4rr+3.
+__device__ __forceinline__ void dsa_pv(RowState& st, const char* __restrict__ stage, const half8 (&pb)[2], int lane,
+                                       int w) {
+  const int g = lane >> 5, e = (lane & 15) >> 2, hc = (lane >> 4) & 1, a4 = lane & 3;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      u32x2 part[2];
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int row = 16 * tt + 8 * rr + 4 * g + e;
+        const int col = 128 * w + 32 * dt + 16 * hc + 4 * a4;         // halfs
+        part[rr] = lds_read_tr16(stage + row * kLatStride + (col >> 3) * 16 + (col & 7) * 2);
+      }
+      const half8 va = as_h8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});
+      st.o[dt] = mfma32(va, pb[tt], st.o[dt]);
+    }
+}
+
+// s_waitcnt vmcnt(n) as the compiler's own builtin (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
+// left at their maxima), so that the compiler's wait insertion knows which loads are complete after it.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that waits for this wave's LDS operations only (s_waitcnt lgkmcnt(0), then s_barrier).  The
+// compiler's __syncthreads would also wait for every direct-to-LDS load in flight, i.e. drain the ring; the walks
+// wait for their own tiles explicitly before barriers that publish them.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One tile: S^T over all QK dims, masked online softmax, PV over this wave's value dims.
+__device__ __forceinline__ void dsa_tile(RowState& st, const half8 (&qb)[36], const char* __restrict__ stage,
+                                         int key0, int kend, float sl2, int lane, int w) {
+  const int r = lane & 31, g = lane >> 5;
+  floatx16 s = dsa_qk(stage, qb, r, g);
+  if (key0 + kTile > kend)
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (key0 + 8 * blk + 4 * g + c >= kend) s[4 * blk + c] = kNegInf;
+  half8 pb[2];
+  softmax_update(st, s, sl2, pb);
+  dsa_pv(st, stage, pb, lane, w);
+}
+
+// Ring walk over the chunk's tiles: tile t lives in stage t % 3, two tiles are in flight while one is computed, and
+// the stage refilled at step t held tile t - 1, which every wave finished before the step's barrier.  The three
+// stages are separate LDS arrays, so the compiler can tell the stage being filled from the stage being read (it
+// would otherwise wait for every load in flight before each read); the explicit vmcnt wait and the barrier order
+// them.  Every LDS array the walk touches is a restrict-qualified parameter, so every LDS access in it carries
+// alias information (the compiler waits for all direct-to-LDS loads before any LDS access that lacks it).
+__device__ __forceinline__ void dsa_ring_walk(char* __restrict__ st0, char* __restrict__ st1, char* __restrict__ st2,
+                                              RowState& st, const half8 (&qb)[36], const f16* kvb,
+                                              const int* __restrict__ sidx, int kbeg, int kend, int ntiles,
+                                              const int (&drow)[10], const int (&dchk)[10], float sl2, int lane,
+                                              int w) {
+  auto stage = [&](auto S) -> char* {
+    if constexpr (S % kLatStages == 0) return st0;
+    else if constexpr (S % kLatStages == 1) return st1;
+    else return st2;
+  };
+  dsa_issue_rows(st0, kvb, sidx, kbeg, kend, kbeg, drow, dchk, w);
+  if (ntiles > 1) dsa_issue_rows(st1, kvb, sidx, kbeg, kend, kbeg + kTile, drow, dchk, w);
+  for (int t0 = 0; t0 < ntiles; t0 += kLatStages) {
+    auto step = [&](auto S) {
+      const int t = t0 + S;
+      if (t >= ntiles) return false;
+      if (t + 1 < ntiles) wait_vmcnt<10>();
+      else wait_vmcnt<0>();
+      lds_barrier();
+      if (t + 2 < ntiles)
+        dsa_issue_rows(stage(std::integral_constant<int, S + 2>()), kvb, sidx, kbeg, kend, kbeg + (t + 2) * kTile,
+                       drow, dchk, w);
+      dsa_tile(st, qb, stage(S), kbeg + t * kTile, kend, sl2, lane, w);
+      return true;
+    };
+    if (!unroll_while<0, kLatStages>(step)) break;
+  }
+}
 
 __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
-  __shared__ __attribute__((aligned(16))) f16 vts[4 * kVTileHalfs];
-  __shared__ __attribute__((aligned(16))) float sx[2][4 * kSSlot];
+  __shared__ __attribute__((aligned(16))) char st0[kLatStageBytes], st1[kLatStageBytes], st2[kLatStageBytes];
+  __shared__ int sidx[kChunk];
   const int item = blockIdx.x;                  // (b * 4 + hb) * kNChunk + chunk
   const int chunk = item % kNChunk;
   const int hb = (item / kNChunk) % 4;
@@ -435,75 +564,33 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   if (kbeg >= cnt) return;                      // whole workgroup
   const int kend = min(cnt, kbeg + kChunk);
   const int ntiles = (kend - kbeg + kTile - 1) / kTile;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int r = lane & 31, g = lane >> 5, dc = lane & 15, kg = lane >> 4;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 31, g = lane >> 5;
 
-  const f16* qrow = a.q + ((size_t)b * kH + hb * 32 + r) * kDK;
-  half8 qb[9];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) qb[s] = as_h8(ld16(qrow + 128 * w + 64 * g + 8 * s));
-  qb[8] = as_h8(ld16(qrow + kDC + 16 * w + 8 * g));
-
-  const f16* kvb = a.kv + (size_t)b * a.L * kDK;
+  // The chunk's selected positions, clamped into the cache.
   const int* ip = a.idx + (size_t)b * kTopK;
-  auto row_of = [&](int key) {
-    const int p = ip[min(key, kend - 1)];
-    return kvb + (size_t)min(max(p, 0), a.L - 1) * kDK;
-  };
-  auto issue = [&](u32x4 (&kr)[9], u32x4 (&vr)[8], int t) {
-    const int key0 = kbeg + t * kTile;
-    const f16* kp = row_of(key0 + r);
+  if (threadIdx.x < kChunk) sidx[threadIdx.x] = min(max(ip[min(kbeg + (int)threadIdx.x, kend - 1)], 0), a.L - 1);
+
+  // Q^T operand of k-step c: head r's dims 16c + 8g .. 16c + 8g + 7 (chunk 2c + g of the query row).
+  const f16* qrow = a.q + ((size_t)b * kH + hb * 32 + r) * kDK;
+  half8 qb[36];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) kr[s] = ld16(kp + 128 * w + 64 * g + 8 * s);
-    kr[8] = ld16(kp + kDC + 16 * w + 8 * g);
+  for (int c = 0; c < 36; ++c) qb[c] = as_h8(ld16(qrow + 16 * c + 8 * g));
+
+  // This wave's DMA instructions j = w + 4q: the (row, chunk) its lane fetches for each.
+  int drow[10], dchk[10];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int key = key0 + kg * 8 + j;
-      vr[j] = sel16(key < kend, ld16(row_of(key) + 128 * w + 8 * dc));
-    }
-  };
-  f16* vt = vts + w * kVTileHalfs;
+  for (int q = 0; q < 10; ++q) {
+    const int slot = 64 * (w + 4 * q) + lane;
+    const int rr = slot / (kLatChunks + 1), cc = slot % (kLatChunks + 1);
+    drow[q] = rr < kTile ? rr : kTile - 1;
+    dchk[q] = (rr < kTile && cc < kLatChunks) ? cc : 0;
+  }
+  __syncthreads();                              // sidx
+  const f16* kvb = a.kv + (size_t)b * a.L * kDK;
   RowState st;
   row_state_init(st);
-  auto compute = [&](const u32x4 (&kr)[9], const u32x4 (&vr)[8], int t, int buf) {
-    store_vt(vt, vr, dc, kg);
-    floatx16 sp = floatx16{};
-#pragma unroll
-    for (int s = 0; s < 9; ++s) sp = mfma32(as_h8(kr[s]), qb[s], sp);
-    float* slot = sx[buf];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) slot[w * kSSlot + i * 64 + lane] = sp[i];
-    __syncthreads();
-    floatx16 s;
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      s[i] = ((slot[i * 64 + lane] + slot[kSSlot + i * 64 + lane]) + slot[2 * kSSlot + i * 64 + lane]) +
-             slot[3 * kSSlot + i * 64 + lane];
-    const int key0 = kbeg + t * kTile;
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int key = key0 + 8 * blk + 4 * g + c;
-        s[4 * blk + c] = key < kend ? s[4 * blk + c] * a.sl2 : kNegInf;
-      }
-    half8 pb[2];
-    softmax_update(st, s, 1.f, pb);
-    pv_tile(st, vt, pb, lane);
-  };
-  {
-    u32x4 kA[9], vA[8], kB[9], vB[8];
-    issue(kA, vA, 0);
-    int t = 0;
-    while (true) {
-      if (t + 1 < ntiles) issue(kB, vB, t + 1);
-      compute(kA, vA, t, t & 1);
-      if (++t >= ntiles) break;
-      if (t + 1 < ntiles) issue(kA, vA, t + 1);
-      compute(kB, vB, t, t & 1);
-      if (++t >= ntiles) break;
-    }
-  }
+  dsa_ring_walk(st0, st1, st2, st, qb, kvb, sidx, kbeg, kend, ntiles, drow, dchk, a.sl2, lane, w);
   // Partial: O[head][128w + d'] for this wave's value dims; m and l are identical in all waves.
   float* po = a.po + (size_t)item * 32 * kDC;
   const float ltot = st.l + xor32(st.l);
