@@ -31,3 +31,38 @@ def test_prefix_parity(shape, dist, seed):
     em, ea = nerr(o, r)
     print(f"  err max {em:.3e} mean {ea:.3e}")
     assert em <= 1e-2
+
+
+# More than 64 rows per KV head (prefix row blocks, then whole-suffix items that merge the prefix partials).
+ROWS_CASES = [
+    (dict(N=64, P=16384, S=2048, S_min=128), "outlier", 110),              # C2, the headline configuration
+    (dict(N=32, P=16384, S=40, S_min=0), "randn", 111),                    # long prefix, short or empty suffixes
+    (dict(N=100, P=3000, S=500, S_min=1, Hq=24, Hkv=8), "randn", 112),     # G = 3: requests straddle row blocks
+    (dict(N=24, P=5000, S=700), "randn", 113),                             # equal suffix lengths
+]
+
+
+def _head_is_zero():
+    from vmk import api
+    ws = api.workspace(0, "cuda")
+    return int(ws[: 4 << 20].count_nonzero().item()) == 0
+
+
+@pytest.mark.parametrize("shape,dist,seed", ROWS_CASES)
+def test_prefix_rows_parity(shape, dist, seed):
+    test_prefix_parity(shape, dist, seed)
+    assert _head_is_zero(), "the workspace head must be zero after every call"
+
+
+def test_prefix_rows_empty_suffixes():
+    """Every suffix empty: every row is the prefix alone."""
+    import prefix_mi355x
+    inp = prefix.make_inputs(dict(N=32, P=2000, S=64, S_min=0), seed=114, device="cuda")
+    inp["slens"].zero_()
+    out = prefix_mi355x.kernel(**inp)
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy().astype(np.float64)
+    r = oracle.prefix.ref64(**inp)
+    em, _ = nerr(o, r)
+    assert em <= 1e-2
+    assert _head_is_zero()
