@@ -41,10 +41,18 @@ __device__ __forceinline__ u32x4 sel16(bool keep, u32x4 x) {
   return u32x4{keep ? x[0] : 0u, keep ? x[1] : 0u, keep ? x[2] : 0u, keep ? x[3] : 0u};
 }
 
-// Q^T operand for 128 head-dims of one row (qrow must be a valid row); zeros when !valid.
+// One all-zero fp16 row (256 bytes, zero-initialised at load time and never written): the K/V source of every key
+// outside the sequence, so a tile's spare rows are zeros and p = 0 never meets a non-finite value of a foreign row,
+// and the Q source of rows outside the workgroup's range.
+__device__ const f16 g_zero_row[128] = {};
+
+// Q^T operand for 128 head-dims of one row (qrow must be a valid row); zeros when !valid, read from g_zero_row rather
+// than selected after the load, so nothing waits for these loads before the first MFMA that uses them (a select would
+// make the compiler wait for them right away, ahead of the first tile's DMA).
 __device__ __forceinline__ void load_qt(half8 (&qb)[8], const f16* qrow, int g, bool valid) {
+  const f16* p = valid ? qrow : g_zero_row;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) qb[s] = as_h8(sel16(valid, ld16(qrow + 64 * g + 8 * s)));
+  for (int s = 0; s < 8; ++s) qb[s] = as_h8(ldg16(p + 64 * g + 8 * s));
 }
 
 // K operand: 128 bytes of the lane's key row (head-dims 64*g .. 64*g+63 of the 128-dim slice at krow).
@@ -170,9 +178,6 @@ __device__ __forceinline__ void wait_vmem_dyn(int n) {
 #undef VMK_WAIT_CASE
 }
 
-// One all-zero fp16 row (256 bytes, zero-initialised at load time and never written): the K/V source of every key
-// outside the sequence, so a tile's spare rows are zeros and p = 0 never meets a non-finite value of a foreign row.
-__device__ const f16 g_zero_row[128] = {};
 
 // Runs f(integral_constant<int, I>) for I = 0 .. N-1 in order while it returns true; false if one returned false.
 template <int I, int N, class F>

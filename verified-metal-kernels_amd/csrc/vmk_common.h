@@ -72,6 +72,17 @@ __device__ __forceinline__ half8 as_h8(u32x4 u) { return __builtin_bit_cast(half
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// Loads through a global (address space 1) pointer: p must point to global memory.  A pointer chosen between two
+// global objects is generic to the compiler, whose flat loads also count as LDS operations and order against them.
+__device__ __forceinline__ u32x4 ldg16(const void* p) {
+  return *reinterpret_cast<const u32x4 __attribute__((address_space(1)))*>(
+      (const void __attribute__((address_space(1)))*)(p));
+}
+__device__ __forceinline__ uint32_t ldg4(const void* p) {
+  return *reinterpret_cast<const uint32_t __attribute__((address_space(1)))*>(
+      (const void __attribute__((address_space(1)))*)(p));
+}
+
 // 16-bit lane i (0..7) of eight 16-byte rows -> one 16-byte column (row j in 16-bit lane j).
 __device__ __forceinline__ u32x4 column8(const u32x4 (&r)[8], int i) {
   const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;

@@ -25,19 +25,30 @@ struct SpecArgs {
 // positions, preloaded as up to kMaskWords 32-bit words (kd <= 32 * kMaskWords).
 constexpr int kMaskWords = 8;
 
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+
+// The mask words are a vector value, not an array: an array member makes the compiler keep the whole struct in LDS
+// and fetch the words one dependent round trip at a time before the first tile.
 struct SpecSrc {
   const f16* kbase;
   const f16* vbase;
-  uint32_t mw[kMaskWords];
-  int kend, tail0;
+  u32x8 mw;          // the row's mask words; words at or past nw are not used
+  int nw, kend, tail0;
   float scale;
   __device__ const f16* krow(int key) const { return key < kend ? kbase + (size_t)key * 128 : g_zero_row; }
   __device__ const f16* vrow(int key) const { return key < kend ? vbase + (size_t)key * 128 : g_zero_row; }
   __device__ uint32_t bit(int j) const {          // bit j of the row's mask, 0 <= j < 32 * kMaskWords
+    const int wi = j >> 5;
     uint32_t w = mw[0];
 #pragma unroll
-    for (int i = 1; i < kMaskWords; ++i) w = (j >> 5) == i ? mw[i] : w;
-    return (w >> (j & 31)) & 1u;
+    for (int i = 1; i < kMaskWords; ++i) w = wi == i ? mw[i] : w;
+    return wi < nw ? (w >> (j & 31)) & 1u : 0u;
+  }
+  // Loads the nw (1 .. kMaskWords) mask words at mrow; every address stays inside the row.
+  __device__ void load_mask(const uint32_t* mrow, int n) {
+    nw = n;
+#pragma unroll
+    for (int i = 0; i < kMaskWords; ++i) mw[i] = ldg4(mrow + min(i, n - 1));
   }
   __device__ void mask(floatx16& s, int key0, int g) const {
     if (key0 + kTile <= tail0 && key0 + kTile <= kend) return;   // whole tile visible (same for the whole wave)
@@ -71,8 +82,7 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   src.kbase = a.k + kvoff;
   src.vbase = a.v + kvoff;
   const uint32_t* mrow = a.bits + (size_t)(b * a.kd + di) * a.W;
-#pragma unroll
-  for (int i = 0; i < kMaskWords; ++i) src.mw[i] = i < a.W ? mrow[i] : 0u;
+  src.load_mask(mrow, a.W);
   const int kbeg = split * a.chunk;
   src.kend = min(a.L, kbeg + a.chunk);
   src.tail0 = a.L - a.kd;
@@ -110,8 +120,7 @@ __global__ __launch_bounds__(64 * NW) void spec_partial_rows_kernel(SpecArgs a) 
   src.kbase = a.k + kvoff;
   src.vbase = a.v + kvoff;
   const uint32_t* mrow = a.bits + (size_t)(b * a.kd + di) * a.W;
-#pragma unroll
-  for (int i = 0; i < kMaskWords; ++i) src.mw[i] = i < a.W ? mrow[i] : 0u;
+  src.load_mask(mrow, a.W);
   const int kbeg = split * a.chunk;
   src.kend = min(a.L, kbeg + a.chunk);
   src.tail0 = a.L - a.kd;
