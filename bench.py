@@ -34,7 +34,7 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16 MFMA
 METRIC = "µs/call per op + achieved HBM GB/s (% of MI355X peak) at bench shapes"
 HEADLINE = "C2"
-DOMINANT = {"prefix": "prefix_partial", "spec": "spec_partial", "dsa": "dsa_indexer"}
+DOMINANT = {"prefix": "prefix_partial", "spec": "spec_partial", "dsa": "dsa_indexer", "decode": "spec_partial"}
 
 
 def log(*a):
@@ -42,10 +42,12 @@ def log(*a):
 
 
 def config_table():
-    from vmk.ops import dsa, prefix, spec
+    from vmk.ops import decode, dsa, prefix, spec
     return [("C1", "prefix", *prefix.CONFIGS["C1"]), ("C2", "prefix", *prefix.CONFIGS["C2"]),
             ("C3", "spec", *spec.CONFIGS["C3"]), ("C4", "spec", *spec.CONFIGS["C4"]),
-            ("C5", "dsa", *dsa.CONFIGS["C5"])]
+            ("C5", "dsa", *dsa.CONFIGS["C5"]),
+            ("D1", "decode", *decode.CONFIGS["D1"]), ("D2", "decode", *decode.CONFIGS["D2"]),
+            ("D3", "decode", *decode.CONFIGS["D3"])]
 
 
 class HipEvents:
@@ -83,21 +85,25 @@ def call_op(opname, inp):
         return vmk.prefix_decode(inp["q"], inp["kp"], inp["vp"], inp["ks"], inp["vs"], inp.get("slens"))
     if opname == "spec":
         return vmk.spec_verify(inp["q"], inp["k"], inp["v"], inp["words"])
+    if opname == "decode":
+        return vmk.decode(inp["q"], inp["k"], inp["v"], inp.get("lens"))
     return vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], inp.get("lens"))
 
 
 def std_op(opname, inp):
     """The PyTorch standard op used by the reference's output check (L1_REF of each op)."""
-    from vmk.ops import dsa, prefix, spec
+    from vmk.ops import decode, dsa, prefix, spec
     if opname == "prefix":
         return prefix.torch_naive(**{k: inp[k] for k in ("q", "kp", "vp", "ks", "vs", "slens")})
     if opname == "spec":
         return spec.torch_sdpa(inp["q"], inp["k"], inp["v"], inp["bits"])
+    if opname == "decode":
+        return decode.torch_sdpa(inp["q"], inp["k"], inp["v"], inp.get("lens"))
     return dsa.torch_fp32_ref(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], inp.get("lens"))
 
 
 def op_bytes_flops(opname, shape, inp_host):
-    from vmk.ops import dsa, prefix, spec
+    from vmk.ops import decode, dsa, prefix, spec
     if opname == "prefix":
         sl = None if inp_host.get("slens") is None else inp_host["slens"].numpy()
         total = prefix.algorithmic_bytes(shape, sl)
@@ -107,6 +113,11 @@ def op_bytes_flops(opname, shape, inp_host):
         total = spec.algorithmic_bytes(shape)
         out = shape["B"] * shape["k"] * spec.HQ * spec.D * 2
         return total, total - out, spec.flops(shape)
+    if opname == "decode":
+        ln = None if inp_host.get("lens") is None else inp_host["lens"].numpy()
+        total = decode.algorithmic_bytes(shape, ln)
+        out = shape["B"] * decode.HQ * decode.D * 2
+        return total, total - out, decode.flops(shape, ln)
     total = dsa.algorithmic_bytes(shape)
     B, L = shape["B"], shape["L"]
     indexer = B * L * dsa.DI * 2 + B * dsa.HI * dsa.DI * 2 + B * dsa.HI * 4    # ik + iq + w
@@ -119,7 +130,8 @@ def distinct_sets(opname, inp0, total_bytes):
     import torch
     n = max(2, int(math.ceil((1 << 30) / max(total_bytes, 1))))
     sets = [inp0]
-    big = {"prefix": ("q", "kp", "vp", "ks", "vs"), "spec": ("q", "k", "v"), "dsa": ("q", "kv", "iq", "ik")}[opname]
+    big = {"prefix": ("q", "kp", "vp", "ks", "vs"), "spec": ("q", "k", "v"), "dsa": ("q", "kv", "iq", "ik"),
+           "decode": ("q", "k", "v")}[opname]
     g = torch.Generator(device="cuda")
     g.manual_seed(1234)
     for _ in range(n - 1):
@@ -158,6 +170,13 @@ def cpu_baseline(opname, shape, dist, inp_host, total_bytes):
             oracle.spec.ref64(inp_host["q"][:1], inp_host["k"][:1], inp_host["v"][:1], inp_host["bits"][:1])
             dt = (time.perf_counter() - t0) * B
             sample = f"batch 0 of {B}, time scaled x{B}"
+        elif opname == "decode":
+            B = shape["B"]
+            t0 = time.perf_counter()
+            oracle.decode.ref64(inp_host["q"][:1], inp_host["k"][:1], inp_host["v"][:1],
+                                None if inp_host.get("lens") is None else inp_host["lens"][:1])
+            dt = (time.perf_counter() - t0) * B
+            sample = f"request 0 of {B}, time scaled x{B}"
         else:
             B = shape["B"]
             t0 = time.perf_counter()
@@ -249,7 +268,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="C1,C2,C3,C4,C5")
+    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle timings")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="first run a plain streaming kernel that reads BYTES and writes BYTES (torch.bitwise_not "

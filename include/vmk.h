@@ -51,6 +51,19 @@ int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mas
                     int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, void* workspace,
                     size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------------------- single-token decode
+ * No kernel module of the reference ships this op: it is the plain decode that the reference benchmarks against
+ * llama.cpp (llama_cpp/test-backend-ops.patch:79-83: 32 q / 8 kv heads, D = 128) and reports at parity
+ * (POST.md:42-46).  It is the verify path with one query row per request and no mask.
+ *   q     (B, Hq, D)       fp16   one token per request
+ *   k, v  (B, Hkv, L, D)   fp16   cache; the token's own key/value is its last position in use
+ *   lens  (B,)             int32  positions in use per request (clamped to [1, L]), or NULL: all L
+ *   out   (B, Hq, D)       fp16
+ * D must be 128, Hq a multiple of Hkv, L >= 1. */
+size_t vmk_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t L);
+int vmk_decode(const void* q, const void* k, const void* v, const void* lens, void* out, int64_t B, int64_t Hq,
+               int64_t Hkv, int64_t D, int64_t L, void* workspace, size_t ws_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------------------------- shared-prefix decode
  * Replaces kernel(q, kp, vp, ks, vs) of kernels/prefix_opus55_v8.py:282-355 (op contract ops/prefix.py:1-4, 57-70).
  *   q       (N, Hq, D)        fp16   one decode token per request

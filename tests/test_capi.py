@@ -49,6 +49,9 @@ def test_workspace_queries_reject_bad_shapes(lib):
     assert lib.vmk_spec_workspace_size(4, 8, 32, 8, 128, 32768) > 0
     assert lib.vmk_prefix_workspace_size(8, 32, 8, 128, 0, 0, 0) == 0     # no keys at all
     assert lib.vmk_prefix_workspace_size(8, 32, 8, 128, 2048, 256, 0) > 0
+    assert lib.vmk_decode_workspace_size(2, 32, 8, 64, 100) == 0          # D != 128
+    assert lib.vmk_decode_workspace_size(2, 32, 8, 128, 0) == 0           # no cache positions
+    assert lib.vmk_decode_workspace_size(2, 32, 8, 128, 65536) > 0
     assert lib.vmk_dsa_workspace_size(0, 100) == 0
     assert lib.vmk_dsa_workspace_size(4, 65536) > 4 * 65536 * 4
 
@@ -65,6 +68,10 @@ def test_entry_points_reject_before_launch(lib):
     rc = lib.vmk_prefix_decode(fake, fake, fake, fake, fake, None, fake, 4, 32, 8, 128, 100, 10, 1, fake, 1 << 30,
                                None)
     assert rc == 1 and b"slens" in lib.vmk_last_error()
+    rc = lib.vmk_decode(fake, fake, None, None, fake, 2, 32, 8, 128, 100, fake, 1 << 30, None)
+    assert rc == 1 and b"null pointer" in lib.vmk_last_error()
+    rc = lib.vmk_decode(fake, fake, fake, None, fake, 2, 32, 8, 128, 100, fake, 64, None)
+    assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
     rc = lib.vmk_dsa_decode(fake, fake, fake, fake, fake, None, fake, fake, fake, 2, 5000, fake, 1024, None)
     assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
     rc = lib.vmk_dsa_decode(fake, fake, fake, fake, None, None, fake, fake, fake, 2, 5000, fake, 1 << 30, None)
@@ -88,3 +95,6 @@ def test_kernel_modules_reject_bf16():
     x = torch.zeros(1, 1, 32, 128, dtype=torch.bfloat16)
     with pytest.raises(TypeError):
         spec_mi355x.kernel(x, x, x, torch.ones(1, 1, dtype=torch.int32))
+    import decode_mi355x
+    with pytest.raises(TypeError):
+        decode_mi355x.kernel(x[:, 0], x, x)

@@ -13,9 +13,9 @@ import torch
 import torch.nn.functional as F
 
 import oracle
-from oracle import dsa as odsa, prefix as oprefix, spec as ospec
+from oracle import decode as odecode, dsa as odsa, prefix as oprefix, spec as ospec
 from oracle.common import softmax_attend, to64
-from vmk.ops import dsa, prefix, spec
+from vmk.ops import decode, dsa, prefix, spec
 
 
 def t64(x):
@@ -371,6 +371,78 @@ def test_topk_set_check_accepts_boundary_swaps_only():
     assert not odsa.topk_set_check(bad, 2048, s, 5000)[0]
     assert not odsa.topk_set_check(top[:2047], 2047, s, 5000)[0]
     assert odsa.topk_set_check(np.arange(1500)[::-1], 1500, s, 1500)[0]
+
+
+DECODE_SHAPES = [(dict(B=2, L=37), "randn"), (dict(B=1, L=1), "randn"), (dict(B=4, L=90, L_min=1), "randn"),
+                 (dict(B=2, L=300, Hq=8, Hkv=2), "needle"), (dict(B=3, L=64, L_min=30), "nan_inf")]
+
+
+def decode_vs_torch(ref, shape, seed=0, dist="randn"):
+    inp = decode.make_inputs(shape, seed=seed, dist=dist)
+    m = decode.valid_mask(inp["k"].shape[2], inp["lens"], "cpu")
+    o = F.scaled_dot_product_attention(t64(inp["q"])[:, :, None], t64(inp["k"]), t64(inp["v"]), attn_mask=m,
+                                       enable_gqa=True)[:, :, 0]
+    return np.allclose(ref(**inp), o.numpy(), rtol=1e-9, atol=1e-9, equal_nan=True)
+
+
+def decode_as_spec(ref, shape, seed=0):
+    """Decode of request b equals spec with one draft (bit 0: the draft sees itself) over the first lens[b] cache
+    positions."""
+    inp = decode.make_inputs(shape, seed=seed)
+    r = ref(**inp)
+    for b in range(inp["q"].shape[0]):
+        n = inp["k"].shape[2] if inp["lens"] is None else int(inp["lens"][b])
+        r2 = ospec.ref64(inp["q"][b:b + 1, None], inp["k"][b:b + 1, :, :n], inp["v"][b:b + 1, :, :n],
+                         torch.ones(1, 1, dtype=torch.int32))[0, 0]
+        if not np.allclose(r[b], r2, rtol=1e-12, atol=1e-12):
+            return False
+    return True
+
+
+def decode_closed_forms(ref, seed=0):
+    """q = 0 gives the mean of V over the positions in use; lens = 1 returns V row 0."""
+    inp = decode.make_inputs(dict(B=3, L=50, L_min=1), seed=seed)
+    inp["q"] = torch.zeros_like(inp["q"])
+    v, G = to64(inp["v"]), decode.HQ // decode.HKV
+    r = ref(**inp)
+    for b in range(3):
+        n = int(inp["lens"][b])
+        if not np.allclose(r[b], np.repeat(v[b, :, :n].mean(1), G, 0), rtol=1e-12, atol=1e-12):
+            return False
+    inp = decode.make_inputs(dict(B=2, L=20), seed=seed + 1)
+    inp["lens"] = torch.ones(2, dtype=torch.int32)
+    return np.allclose(ref(**inp), np.repeat(to64(inp["v"])[:, :, 0], G, 1), rtol=1e-12, atol=1e-12)
+
+
+def decode_mutant(kind):
+    def out(q, k, v, lens=None):
+        if kind == "lens_ignored":
+            return odecode.ref64(q, k, v, None)
+        if kind == "lens_off_by_one":
+            return odecode.ref64(q, k, v, None if lens is None else lens - 1)
+        if kind == "gqa_transposed":                    # head h reads KV head h % Hkv instead of h // G
+            Hkv = k.shape[1]
+            idx = torch.arange(q.shape[1]).reshape(Hkv, -1).t().reshape(-1)
+            return odecode.ref64(q[:, idx], k, v, lens)[:, torch.argsort(idx)]
+        if kind == "no_scale":
+            return odecode.ref64(q * math.sqrt(q.shape[-1]), k, v, lens)
+    return out
+
+
+@pytest.mark.parametrize("shape,dist", DECODE_SHAPES)
+def test_decode_vs_torch_sdpa(shape, dist):
+    assert decode_vs_torch(odecode.ref64, shape, dist=dist)
+
+
+def test_decode_identities():
+    assert decode_as_spec(odecode.ref64, dict(B=3, L=70, L_min=1))
+    assert decode_closed_forms(odecode.ref64)
+
+
+@pytest.mark.parametrize("kind", ["lens_ignored", "lens_off_by_one", "gqa_transposed", "no_scale"])
+def test_decode_checks_catch_planted_mistakes(kind):
+    bad = decode_mutant(kind)
+    assert not (all(decode_vs_torch(bad, s, dist=d) for s, d in DECODE_SHAPES) and decode_closed_forms(bad))
 
 
 def test_oracle_is_test_infrastructure():

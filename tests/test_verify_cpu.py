@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 KDIR = os.path.join(os.path.dirname(HERE), "verified-metal-kernels_amd", "kernels")
 
 
-@pytest.mark.parametrize("name", ["spec_mi355x.py", "prefix_mi355x.py", "dsa_mi355x.py"])
+@pytest.mark.parametrize("name", ["spec_mi355x.py", "prefix_mi355x.py", "dsa_mi355x.py", "decode_mi355x.py"])
 def test_gate_accepts_shipped_kernels(name):
     assert verify.gate(open(os.path.join(KDIR, name)).read()) == []
 

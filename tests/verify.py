@@ -46,7 +46,7 @@ import numpy as np  # noqa: E402
 
 from vmk.ops import KEYS, load_op  # noqa: E402
 
-ORACLE = {"prefix": "oracle.prefix", "spec": "oracle.spec", "dsa": "oracle.dsa"}
+ORACLE = {"prefix": "oracle.prefix", "spec": "oracle.spec", "dsa": "oracle.dsa", "decode": "oracle.decode"}
 
 
 def cand_inputs(opname, inp):

@@ -12,7 +12,8 @@ struct SpecArgs {
   const f16* q;            // (B, kd, Hq, 128)
   const f16* k;            // (B, Hkv, L, 128)
   const f16* v;
-  const uint32_t* bits;    // (B, kd, W)
+  const uint32_t* bits;    // (B, kd, W), or null: every cache position visible to every query row (plain decode)
+  const int* lens;         // (B,) cache positions in use per batch entry (clamped to [kd, L]), or null: all L
   float* part_o;           // [item][32*WR][128], item = (grp * nrb + rb) * nsplit + split
   float* part_ml;          // [item][32*WR][2]
   f16* out;                // (B, kd, Hq, 128)
@@ -44,8 +45,15 @@ struct SpecSrc {
     for (int i = 1; i < kMaskWords; ++i) w = wi == i ? mw[i] : w;
     return wi < nw ? (w >> (j & 31)) & 1u : 0u;
   }
-  // Loads the nw (1 .. kMaskWords) mask words at mrow; every address stays inside the row.
+  // Loads the nw (1 .. kMaskWords) mask words at mrow; every address stays inside the row.  mrow == null: the whole
+  // tail is visible.
   __device__ void load_mask(const uint32_t* mrow, int n) {
+    if (!mrow) {
+      nw = kMaskWords;
+#pragma unroll
+      for (int i = 0; i < kMaskWords; ++i) mw[i] = ~0u;
+      return;
+    }
     nw = n;
 #pragma unroll
     for (int i = 0; i < kMaskWords; ++i) mw[i] = ldg4(mrow + min(i, n - 1));
@@ -64,6 +72,11 @@ struct SpecSrc {
   }
 };
 
+// Cache positions of batch entry b: lens[b] clamped to [kd, L] (the query rows are the last kd of them), or L.
+__device__ __forceinline__ int batch_len(const SpecArgs& a, int b) {
+  return a.lens ? min(max(a.lens[b], a.kd), a.L) : a.L;
+}
+
 // One workgroup = WR x WK waves: WR row blocks of 32 rows, WK waves interleaving the key tiles of one split.
 __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
@@ -81,13 +94,13 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   const size_t kvoff = (size_t)grp * a.L * 128;
   src.kbase = a.k + kvoff;
   src.vbase = a.v + kvoff;
-  const uint32_t* mrow = a.bits + (size_t)(b * a.kd + di) * a.W;
-  src.load_mask(mrow, a.W);
+  src.load_mask(a.bits ? a.bits + (size_t)(b * a.kd + di) * a.W : nullptr, a.W);
+  const int Lb = batch_len(a, b);
   const int kbeg = split * a.chunk;
-  src.kend = min(a.L, kbeg + a.chunk);
-  src.tail0 = a.L - a.kd;
+  src.kend = min(Lb, kbeg + a.chunk);
+  src.tail0 = Lb - a.kd;
   src.scale = a.sl2;
-  const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
+  const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
   const size_t rows_wg = 32 * a.WR;
   auto qrow = [&](int r) {
     const int qr = row0 + r, i = qr / a.G, gg = qr % a.G;
@@ -119,13 +132,13 @@ __global__ __launch_bounds__(64 * NW) void spec_partial_rows_kernel(SpecArgs a) 
   const size_t kvoff = (size_t)grp * a.L * 128;
   src.kbase = a.k + kvoff;
   src.vbase = a.v + kvoff;
-  const uint32_t* mrow = a.bits + (size_t)(b * a.kd + di) * a.W;
-  src.load_mask(mrow, a.W);
+  src.load_mask(a.bits ? a.bits + (size_t)(b * a.kd + di) * a.W : nullptr, a.W);
+  const int Lb = batch_len(a, b);
   const int kbeg = split * a.chunk;
-  src.kend = min(a.L, kbeg + a.chunk);
-  src.tail0 = a.L - a.kd;
+  src.kend = min(Lb, kbeg + a.chunk);
+  src.tail0 = Lb - a.kd;
   src.scale = a.sl2;
-  const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
+  const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
   const size_t rows_wg = 32 * NW;
   attend_wg_rows<NW>(smem, src,
                      [&](int r) {
@@ -197,6 +210,29 @@ extern "C" size_t vmk_spec_workspace_size(int64_t B, int64_t kd, int64_t Hq, int
   return kWsHead + (p.po_floats + p.pml_floats) * sizeof(float) + 256;
 }
 
+// Partial launch (key split or row split by the plan) and LSE-combine launch of one spec/decode call.
+static int spec_launch(SpecArgs& a, const SpecPlan& p, void* workspace, hipStream_t s) {
+  a.part_o = (float*)align_up((char*)workspace + kWsHead, 256);
+  a.part_ml = a.part_o + p.po_floats;
+  a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;
+  a.sl2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
+  const unsigned items = (unsigned)(a.B * a.Hkv * p.nrb * p.nsplit);
+  prof_before(kKSpecPartial, s);
+  if (!p.rows_mode)
+    hipLaunchKernelGGL(spec_partial_kernel, dim3(items), dim3(256), 0, s, a);
+  else if (p.WR == 4)
+    hipLaunchKernelGGL(spec_partial_rows_kernel<4>, dim3(items), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(spec_partial_rows_kernel<8>, dim3(items), dim3(512), 0, s, a);
+  prof_after(kKSpecPartial, s);
+  VMK_CHECK_HIP(hipGetLastError());
+  prof_before(kKSpecCombine, s);
+  hipLaunchKernelGGL(spec_combine_kernel, dim3((unsigned)(a.B * a.Hkv * a.kd * a.G)), dim3(128), 0, s, a);
+  prof_after(kKSpecCombine, s);
+  VMK_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
 extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out,
                                int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W,
                                void* workspace, size_t ws_bytes, void* stream) {
@@ -213,26 +249,34 @@ extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, cons
   SpecPlan p = spec_plan(B, kd, Hq, Hkv, L);
   SpecArgs a;
   a.q = (const f16*)q; a.k = (const f16*)k; a.v = (const f16*)v; a.bits = (const uint32_t*)mask_words;
+  a.lens = nullptr;
   a.out = (f16*)out;
-  a.part_o = (float*)align_up((char*)workspace + kWsHead, 256);
-  a.part_ml = a.part_o + p.po_floats;
   a.B = (int)B; a.kd = (int)kd; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = (int)W;
-  a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;
-  a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
-  hipStream_t s = (hipStream_t)stream;
-  const unsigned items = (unsigned)(B * Hkv * p.nrb * p.nsplit);
-  prof_before(kKSpecPartial, s);
-  if (!p.rows_mode)
-    hipLaunchKernelGGL(spec_partial_kernel, dim3(items), dim3(256), 0, s, a);
-  else if (p.WR == 4)
-    hipLaunchKernelGGL(spec_partial_rows_kernel<4>, dim3(items), dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(spec_partial_rows_kernel<8>, dim3(items), dim3(512), 0, s, a);
-  prof_after(kKSpecPartial, s);
-  VMK_CHECK_HIP(hipGetLastError());
-  prof_before(kKSpecCombine, s);
-  hipLaunchKernelGGL(spec_combine_kernel, dim3((unsigned)(B * Hkv * kd * (Hq / Hkv))), dim3(128), 0, s, a);
-  prof_after(kKSpecCombine, s);
-  VMK_CHECK_HIP(hipGetLastError());
-  return 0;
+  return spec_launch(a, p, workspace, (hipStream_t)stream);
+}
+
+// Plain single-token decode: the verify path with one query row per request and no mask (the row's own position is
+// the last of the cache, visible like every other).
+extern "C" size_t vmk_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t L) {
+  return vmk_spec_workspace_size(B, 1, Hq, Hkv, D, L);
+}
+
+extern "C" int vmk_decode(const void* q, const void* k, const void* v, const void* lens, void* out, int64_t B,
+                          int64_t Hq, int64_t Hkv, int64_t D, int64_t L, void* workspace, size_t ws_bytes,
+                          void* stream) {
+  VMK_CHECK(q && k && v && out, "null pointer argument");
+  VMK_CHECK(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/batch sizes");
+  VMK_CHECK(D == 128, "only head_dim 128 is supported");
+  VMK_CHECK(L >= 1, "L must be at least 1");
+  VMK_CHECK(Hq / Hkv <= 1 << 20 && B * Hkv * L <= (int64_t)1 << 40, "sizes out of range");
+  VMK_CHECK(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "tensors must be 16-byte aligned");
+  const size_t need = vmk_decode_workspace_size(B, Hq, Hkv, D, L);
+  VMK_CHECK(workspace && ws_bytes >= need, "workspace too small (query vmk_decode_workspace_size)");
+  SpecPlan p = spec_plan(B, 1, Hq, Hkv, L);
+  SpecArgs a;
+  a.q = (const f16*)q; a.k = (const f16*)k; a.v = (const f16*)v; a.bits = nullptr;
+  a.lens = (const int*)lens;
+  a.out = (f16*)out;
+  a.B = (int)B; a.kd = 1; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = 1;
+  return spec_launch(a, p, workspace, (hipStream_t)stream);
 }

@@ -4,5 +4,5 @@ Host side of the C-ABI library libvmk.so (HIP kernels in ../csrc, declared in in
 tensors on a ROCm device; every call launches on torch's current stream and returns without synchronising.
 """
 from .lib import VmkError, load  # noqa: F401
-from .api import (spec_verify, prefix_decode, dsa_decode, dsa_indexer_select, dsa_sparse_mla,  # noqa: F401
+from .api import (spec_verify, decode, prefix_decode, dsa_decode, dsa_indexer_select, dsa_sparse_mla,  # noqa: F401
                   workspace, device_ok)

@@ -85,6 +85,32 @@ def spec_verify(q, k, v, words, out=None):
     return out
 
 
+def decode(q, k, v, lens=None, out=None):
+    """Single-token decode: q (B, Hq, 128) fp16, k/v (B, Hkv, L, 128) fp16, lens (B,) int32 or None (all L in use).
+    Returns out (B, Hq, 128) fp16."""
+    _need(q, "q", torch.float16, 3)
+    _need(k, "k", torch.float16, 4)
+    _need(v, "v", torch.float16, 4)
+    B, Hq, D = q.shape
+    Hkv, L = k.shape[1], k.shape[2]
+    if tuple(k.shape) != (B, Hkv, L, D) or tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"k/v shape {tuple(k.shape)}/{tuple(v.shape)} do not match q {tuple(q.shape)}")
+    if lens is not None:
+        _need(lens, "lens", torch.int32, 1)
+        if lens.shape[0] != B:
+            raise ValueError("lens must have B entries")
+    device_ok(q.device)
+    if out is None:
+        out = torch.empty_like(q)
+    ws_n = lib.load().vmk_decode_workspace_size(B, Hq, Hkv, D, L)
+    if ws_n == 0:
+        raise lib.VmkError(f"unsupported decode shape B={B} Hq={Hq} Hkv={Hkv} D={D} L={L}")
+    ws = workspace(ws_n, q.device)
+    lib.call("vmk_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), 0 if lens is None else lens.data_ptr(),
+             out.data_ptr(), B, Hq, Hkv, D, L, ws.data_ptr(), ws.numel(), _stream(q))
+    return out
+
+
 def prefix_decode(q, kp, vp, ks, vs, slens=None, out=None):
     """q (N, Hq, 128), kp/vp (Hkv, P, 128), ks/vs (N, Hkv, S, 128) fp16, slens (N,) int32 or None.
     Returns out (N, Hq, 128) fp16."""

@@ -22,6 +22,8 @@ _SIGS = {
     "vmk_profile_next": [_c_vp, _c_vp, ctypes.c_int],
     "vmk_spec_workspace_size": [_c_i64] * 6,
     "vmk_spec_verify": [_c_vp] * 5 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
+    "vmk_decode_workspace_size": [_c_i64] * 5,
+    "vmk_decode": [_c_vp] * 5 + [_c_i64] * 5 + [_c_vp, _c_sz, _c_vp],
     "vmk_prefix_workspace_size": [_c_i64] * 7,
     "vmk_prefix_decode": [_c_vp] * 7 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_workspace_size": [_c_i64] * 2,
@@ -30,7 +32,7 @@ _SIGS = {
     "vmk_dsa_decode": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
 }
 _RET = {"vmk_last_error": ctypes.c_char_p, "vmk_spec_workspace_size": _c_sz, "vmk_prefix_workspace_size": _c_sz,
-        "vmk_dsa_workspace_size": _c_sz}
+        "vmk_dsa_workspace_size": _c_sz, "vmk_decode_workspace_size": _c_sz}
 
 
 class VmkError(RuntimeError):
