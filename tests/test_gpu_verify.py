@@ -1,5 +1,6 @@
-"""The three-layer verifier (tests/verify.py) on the GPU: every libvmk kernel module is CORRECT, and both calibration
-cheats are REJECTED by the layer that is meant to catch them (README.md:109-112 of the reference)."""
+"""The verifier (tests/verify.py) on the GPU: every libvmk kernel module is CORRECT, and the calibration cheats are
+REJECTED by the layer that is meant to catch them (README.md:109-112 of the reference; the L4 fixture is this
+build's)."""
 import json
 import os
 import subprocess
@@ -46,3 +47,14 @@ def test_prefix_cheat_rejected(tmp_path):
     assert rep["verdict"] == "REJECTED" and rc == 1
     assert rep["L1_pass"] == rep["L1_n"]
     assert rep["L2_pass"] < rep["L2_n"] or rep["L3_pass"] < rep["L3_n"]
+
+
+@pytest.mark.timeout(900)
+def test_batch_dependent_decode_rejected_only_by_l4(tmp_path):
+    """The L4 calibration fixture is exact on every call but cuts the keys into B + 1 chunks: every other layer
+    accepts it and the row-invariance layer rejects it."""
+    rc, rep = run_verify(os.path.join(HERE, "wrong_kernels", "decode_cheat_batch_split.py"), tmp_path, "--skip-gate")
+    assert rep["verdict"] == "REJECTED" and rc == 1
+    for layer in ("L1", "L2", "L3", "X"):
+        assert rep[f"{layer}_pass"] == rep[f"{layer}_n"], (layer, [c for c in rep[layer] if not c["ok"]])
+    assert rep["L4_pass"] == 0

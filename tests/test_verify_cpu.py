@@ -72,3 +72,40 @@ def test_missing_cases_are_failures_without_gpu(tmp_path, monkeypatch):
     monkeypatch.setattr(verify, "cases", lambda op, extra=True: [("L1", 0, dict(B=1, L=8, k=8), "randn", 100)])
     rep = verify.judge("spec", out)
     assert rep["verdict"] == "REJECTED" and rep["L1_pass"] == 0 and "missing" in rep["L1"][0]["error"]
+
+
+@pytest.mark.parametrize("opname", ["prefix", "spec", "dsa", "decode"])
+def test_l4_row_inputs_slice_one_batch_row(opname):
+    """row_inputs(i) is batch row i of every per-row input (CPU tensors, the smallest L4-like shape of each op)."""
+    from vmk.ops import KEYS, load_op
+    op = load_op(opname)
+    shape, dist = {"prefix": (dict(N=3, P=40, S=9, S_min=1), "randn"), "spec": (dict(B=3, L=40, k=5), "randn"),
+                   "dsa": (dict(B=3, L=300), "ragged"), "decode": (dict(B=3, L=50, L_min=1), "randn")}[opname]
+    inp = {k: v for k, v in op.make_inputs(shape, seed=1, dist=dist).items() if k in KEYS[opname]}
+    assert op.L4_CASES
+    for i in range(3):
+        r = op.row_inputs(inp, i)
+        assert set(r) == set(inp)
+        for k, v in inp.items():
+            if v is None:
+                assert r[k] is None
+            elif opname == "prefix" and k in ("kp", "vp"):
+                assert r[k] is v                              # the shared prefix is not sliced
+            else:
+                assert r[k].shape[0] == 1 and (r[k][0] == v[i]).all()
+
+
+def test_l4_judgement_flags_the_differing_rows():
+    full = np.arange(24, dtype=np.float16).reshape(4, 6)
+    rows = full.copy()
+    meta = {"L4_0": dict(ok=True, n_out=1, n_rows=4)}
+    assert verify.l4_case(meta, {"L4_0__full0": full, "L4_0__rows0": rows}, 0, {}, "randn")["ok"]
+    rows[2, 3] = np.float16(-0.0) if full[2, 3] == 0 else -full[2, 3]
+    c = verify.l4_case(meta, {"L4_0__full0": full, "L4_0__rows0": rows}, 0, {}, "randn")
+    assert not c["ok"] and c["rows_differing"] == [2]
+    nan = full.copy()
+    nan[1, 1] = np.nan
+    same = verify.l4_case(meta, {"L4_0__full0": nan, "L4_0__rows0": nan.copy()}, 0, {}, "randn")
+    assert same["ok"]                                          # bit comparison: equal NaN bits are equal
+    missing = verify.l4_case({}, {}, 0, {}, "randn")
+    assert not missing["ok"] and "missing" in missing["error"]

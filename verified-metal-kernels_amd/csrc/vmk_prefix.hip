@@ -4,12 +4,14 @@
 // (kernels/prefix_opus55_v8.py:28-108, 109-208, 211-261) behind the kernel(q, kp, vp, ks, vs) contract of
 // ops/prefix.py:1-4, plus optional ragged suffix lengths.
 //
-// Launch 1 (one grid, two item kinds):
-//   prefix items (KV head h, row block, split): all N*G query rows of head h against a chunk of the shared prefix;
-//     the prefix tile is staged once per workgroup for up to 128 rows, so the prefix is streamed from HBM once per
-//     row block instead of once per request;
-//   suffix items (request n, KV head h, chunk): the G rows of request n against its own suffix rows.
-// Launch 2: per output row, log-sum-exp merge of the prefix partials of its KV head and its own suffix partials.
+// Launch 1 (prefix_rows_kernel): items (KV head h, row block of 32*NW of the N*G rows, prefix chunk) stream the chunk
+//   once through an LDS ring shared by NW waves of 32 rows each, so the prefix is read from HBM once per row block
+//   instead of once per request.
+// Launch 2 (prefix_partial_kernel): items (request n, KV head h, suffix chunk) attend the G rows of request n to its
+//   own suffix rows.  When a suffix is one chunk, the item also merges the finished prefix partials of its rows and
+//   writes the output.
+// Launch 3 (prefix_combine_kernel, only when a suffix spans several chunks or there is no prefix): per output row,
+//   the log-sum-exp merge of its prefix and suffix partials.
 #include "attn_core.h"
 #include "vmk_internal.h"
 
@@ -28,12 +30,12 @@ struct PrefixArgs {
   float* po_s;             // suffix partials [n][h][split][32][128]
   float* pml_s;
   int N, Hq, Hkv, G, P, S;
-  int WRp, WKp, nrb_p, nsplit_p, chunk_p;   // prefix plan
+  int WRp, nrb_p, nsplit_p, chunk_p;   // prefix plan
   int nsplit_s, chunk_s;                    // suffix plan (WR = 1, WK = 4)
   int n_prefix_items;
-  int item0;               // first item handled by the key-split kernel (n_prefix_items when prefix rows run apart)
   int2* order;             // (N,) (request, suffix length) by decreasing length (written by the prefix launch), or null
   int fuse;                // 1: suffix items are whole suffixes and merge the (finished) prefix partials themselves
+  int merge;               // 1: whole-suffix partials are merged with the prefix partials by prefix_merge_kernel
   float sl2;
 };
 
@@ -165,73 +167,54 @@ __device__ __forceinline__ void merge_prefetched_row(const PrefixArgs& a, const 
   out[1] = (f16)(num.y / den);
 }
 
-__global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
-  const int item = a.item0 + blockIdx.x;
+// Suffix item `sitem` (request, KV head, suffix chunk) of 4 waves.  Fused: the prefix partials are finished (an
+// earlier launch) and the item writes its rows' outputs; otherwise it writes its partial to po_s / pml_s.
+__device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int sitem) {
   RangeSrc src;
   src.scale = a.sl2;
-  if (item < a.n_prefix_items) {
-    const int split = item % a.nsplit_p;
-    const int rb = (item / a.nsplit_p) % a.nrb_p;
-    const int h = item / (a.nsplit_p * a.nrb_p);
-    const size_t off = (size_t)h * a.P * 128;
-    src.kbase = a.kp + off;
-    src.vbase = a.vp + off;
-    const int kbeg = split * a.chunk_p;
-    src.kend = min(a.P, kbeg + a.chunk_p);
-    const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
-    const int row0 = rb * a.WRp * 32;
-    const size_t rows_wg = 32 * a.WRp;
-    auto qrow = [&](int r) {
-      const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
-      return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
-    };
-    float* po = a.po_p + (size_t)item * rows_wg * 128;
-    float* pml = a.pml_p + (size_t)item * rows_wg * 2;
-    if (a.WKp == 4)
-      attend_wg<1, 4>(smem, src, qrow, a.N * a.G - row0, kbeg, ntiles, po, pml);
-    else
-      attend_wg<2, 2>(smem, src, qrow, a.N * a.G - row0, kbeg, ntiles, po, pml);
-  } else {
-    const int sitem = item - a.n_prefix_items;
-    const int split = sitem % a.nsplit_s;
-    int nh = sitem / a.nsplit_s, sn = 0;
-    if (a.order) {                                        // long suffixes are dispatched first
-      const int2 o = a.order[nh / a.Hkv];
-      nh = o.x * a.Hkv + nh % a.Hkv;
-      sn = o.y;
-    }
-    const int n = nh / a.Hkv, h = nh % a.Hkv;
-    const int kbeg = split * a.chunk_s;
-    if (!a.order) sn = suffix_len(a, n);
-    if (kbeg >= sn && !a.fuse) return;                    // whole workgroup: nothing of this suffix is here
-    const size_t off = ((size_t)n * a.Hkv + h) * a.S * 128;
-    src.kbase = a.ks + off;
-    src.vbase = a.vs + off;
-    src.kend = min(sn, kbeg + a.chunk_s);
-    const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
-    auto qrow = [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; };
-    if (!a.fuse) {
-      const size_t pi = (size_t)nh * a.nsplit_s + split;
-      attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, a.po_s + pi * 32 * 128, a.pml_s + pi * 32 * 2);
-      return;
-    }
-    // Whole suffix: keep the partial in LDS (past the merge slots) and merge it with the prefix partials here.
-    float* lpo = reinterpret_cast<float*>(smem + kFuseOff);
-    float* lpml = lpo + 32 * 128;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (a.G <= 4 && a.nsplit_p <= kPrefetchSplits) {          // wave w finishes row w
-      PrefixRow pr;
-      if (wave < a.G) prefetch_prefix_row(a, pr, n, h, wave, lane);
-      attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
-      __syncthreads();
-      if (wave < a.G) merge_prefetched_row(a, pr, lpo, lpml, n, h, wave, lane);
-    } else {
-      attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
-      __syncthreads();
-      merge_prefix_rows(a, lpo, lpml, n, h);
-    }
+  const int split = sitem % a.nsplit_s;
+  int nh = sitem / a.nsplit_s, sn = 0;
+  if (a.order) {                                        // long suffixes are dispatched first
+    const int2 o = a.order[nh / a.Hkv];
+    nh = o.x * a.Hkv + nh % a.Hkv;
+    sn = o.y;
   }
+  const int n = nh / a.Hkv, h = nh % a.Hkv;
+  const int kbeg = split * a.chunk_s;
+  if (!a.order) sn = suffix_len(a, n);
+  if (kbeg >= sn && !a.fuse && !a.merge) return;        // whole workgroup: nothing of this suffix is here
+  const size_t off = ((size_t)n * a.Hkv + h) * a.S * 128;
+  src.kbase = a.ks + off;
+  src.vbase = a.vs + off;
+  src.kend = min(sn, kbeg + a.chunk_s);
+  const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
+  auto qrow = [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; };
+  if (!a.fuse) {
+    const size_t pi = (size_t)nh * a.nsplit_s + split;
+    attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, a.po_s + pi * 32 * 128, a.pml_s + pi * 32 * 2);
+    return;
+  }
+  // Whole suffix: keep the partial in LDS (past the merge slots) and merge it with the prefix partials here.
+  float* lpo = reinterpret_cast<float*>(smem + kFuseOff);
+  float* lpml = lpo + 32 * 128;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (a.G <= 4 && a.nsplit_p <= kPrefetchSplits) {          // wave w finishes row w
+    PrefixRow pr;
+    if (wave < a.G) prefetch_prefix_row(a, pr, n, h, wave, lane);
+    attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
+    __syncthreads();
+    if (wave < a.G) merge_prefetched_row(a, pr, lpo, lpml, n, h, wave, lane);
+  } else {
+    attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
+    __syncthreads();
+    merge_prefix_rows(a, lpo, lpml, n, h);
+  }
+}
+
+// Suffix items, after the prefix launch has written the prefix partials.
+__global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
+  suffix_item(a, smem, blockIdx.x);
 }
 
 // Prefix items when N*G > 64: NW waves own 32 of the N*G rows each and share one LDS ring, so the prefix chunk is
@@ -270,10 +253,7 @@ __device__ void build_suffix_order(const PrefixArgs& a, uint32_t* cnt /* LDS, 25
 }
 
 template <int NW>
-__global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kRowsSmemBytes];
-  const int item = blockIdx.x;
-  if (item == 0 && a.order) build_suffix_order<64 * NW>(a, reinterpret_cast<uint32_t*>(smem));
+__device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem, int item) {
   const int split = item % a.nsplit_p;
   const int rb = (item / a.nsplit_p) % a.nrb_p;
   const int h = item / (a.nsplit_p * a.nrb_p);
@@ -294,6 +274,42 @@ __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
                      },
                      a.N * a.G - row0, kbeg, ntiles, a.po_p + (size_t)item * rows_wg * 128,
                      a.pml_p + (size_t)item * rows_wg * 2);
+}
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kRowsSmemBytes];
+  if (blockIdx.x == 0 && a.order) build_suffix_order<64 * NW>(a, reinterpret_cast<uint32_t*>(smem));
+  prefix_rows_item<NW>(a, smem, blockIdx.x);
+}
+
+// Both item kinds in one grid when a KV head has at most 128 rows: prefix items (4 waves sharing a ring) first, then
+// suffix items writing their partials.  No item depends on another.
+constexpr int kMixedSmemBytes = kRowsSmemBytes > kAttnSmemBytes ? kRowsSmemBytes : kAttnSmemBytes;
+__global__ __launch_bounds__(256) void prefix_mixed_kernel(PrefixArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kMixedSmemBytes];
+  if ((int)blockIdx.x < a.n_prefix_items)
+    prefix_rows_item<4>(a, smem, blockIdx.x);
+  else
+    suffix_item(a, smem, blockIdx.x - a.n_prefix_items);
+}
+
+// After a mixed launch with whole suffixes: the final merge of the G rows of (request, KV head), by the functions a
+// fused suffix item uses and from the same partial values, so the output bits do not depend on which path ran.
+__global__ __launch_bounds__(256) void prefix_merge_kernel(PrefixArgs a) {
+  const int nh = blockIdx.x, n = nh / a.Hkv, h = nh % a.Hkv;
+  const float* lpo = a.po_s + (size_t)nh * 32 * 128;        // one suffix split per (request, KV head)
+  const float* lpml = a.pml_s + (size_t)nh * 32 * 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (a.G <= 4 && a.nsplit_p <= kPrefetchSplits) {
+    if (wave < a.G) {
+      PrefixRow pr;
+      prefetch_prefix_row(a, pr, n, h, wave, lane);
+      merge_prefetched_row(a, pr, lpo, lpml, n, h, wave, lane);
+    }
+  } else {
+    merge_prefix_rows(a, lpo, lpml, n, h);
+  }
 }
 
 // One workgroup (128 threads = head-dims) per output row (n, hq): merge the prefix splits of KV head h and the
@@ -326,30 +342,26 @@ __global__ __launch_bounds__(128) void prefix_combine_kernel(PrefixArgs a) {
 }
 
 struct PrefixPlan {
-  bool rows_mode;
-  int WRp, WKp, nrb_p, nsplit_p, chunk_p, nsplit_s, chunk_s;
+  int WRp, nrb_p, nsplit_p, chunk_p, nsplit_s, chunk_s;
   size_t po_p, pml_p, po_s, pml_s, order;
   int n_prefix_items, n_items;
   bool fuse;
 };
 
+// Every choice that shapes a row's arithmetic depends on P, S and G only, never on N: a request's rows go through
+// the same prefix chunks, tile order and merges whatever batch they are in, so a batch row is bit-equal to the same
+// request alone.  N only sets how many row blocks there are (and the row-block width, which groups rows that share
+// a ring without changing any row's arithmetic).
 static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int64_t S) {
   PrefixPlan p;
   const int64_t G = Hq / Hkv, R = N * G;
-  p.rows_mode = R > 64;
-  if (p.rows_mode) { p.WRp = R <= 128 ? 4 : 8; p.WKp = 1; }   // row-split: WRp = waves sharing one ring
-  else if (R <= 32) { p.WRp = 1; p.WKp = 4; }
-  else { p.WRp = 2; p.WKp = 2; }
+  p.WRp = R <= 128 ? 4 : 8;                                  // waves sharing one ring, 32 rows each
   const int64_t rows_wg = 32 * p.WRp;
   p.nrb_p = (int)((R + rows_wg - 1) / rows_wg);
-  // Prefix chunks of at most 1024 keys, fewer when that spreads the prefix over ~256 workgroups.
-  int64_t chunk = 1024;
-  if (P > 0) {
-    const int64_t want = std::max<int64_t>(1, 256 / std::max<int64_t>(1, Hkv * p.nrb_p));
-    chunk = std::min<int64_t>(chunk, (P + want - 1) / want);
-    chunk = std::max<int64_t>(chunk, kTile * p.WKp);
-    chunk = (chunk + kTile - 1) / kTile * kTile;
-  }
+  // Prefix chunks of P/32 keys in whole tiles, within [128, 1024] (C1: 128, C2: 512).
+  int64_t chunk = (P + 31) / 32;
+  chunk = (chunk + kTile - 1) / kTile * kTile;
+  chunk = std::min<int64_t>(1024, std::max<int64_t>(128, chunk));
   p.chunk_p = (int)chunk;
   p.nsplit_p = P > 0 ? (int)((P + chunk - 1) / chunk) : 0;
   p.n_prefix_items = (int)(Hkv * p.nrb_p * p.nsplit_p);
@@ -365,8 +377,8 @@ static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int
   p.po_s = (size_t)N * Hkv * p.nsplit_s * 32 * 128;
   p.pml_s = (size_t)N * Hkv * p.nsplit_s * 32 * 2;
   p.order = (size_t)2 * N;
-  // With the prefix partials finished by an earlier launch, whole-suffix items finish their rows themselves.
-  p.fuse = p.rows_mode && p.n_prefix_items > 0 && p.nsplit_s == 1;
+  // With the prefix partials finished by the prefix launch, whole-suffix items finish their rows themselves.
+  p.fuse = p.n_prefix_items > 0 && p.nsplit_s == 1;
   return p;
 }
 
@@ -408,28 +420,39 @@ extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, 
   a.po_s = (float*)align_up(a.pml_p + p.pml_p, 256);
   a.pml_s = (float*)align_up(a.po_s + p.po_s, 256);
   // The schedule order is built by the prefix launch, so only when that runs before the suffix items.
-  a.order = (ragged && p.rows_mode && p.n_prefix_items > 0) ? (int2*)align_up(a.pml_s + p.pml_s, 256) : nullptr;
-  a.fuse = p.fuse ? 1 : 0;
+  // Up to 128 rows per KV head, prefix and suffix items share one launch; a merge (or combine) launch follows.
+  // Beyond, the prefix launch runs first and whole-suffix items merge its partials themselves.
+  const bool mixed = p.WRp == 4;
+  // The schedule order is built by the prefix launch, so only when that runs before the suffix items.
+  a.order = (ragged && p.n_prefix_items > 0 && !mixed) ? (int2*)align_up(a.pml_s + p.pml_s, 256) : nullptr;
+  a.fuse = p.fuse && !mixed ? 1 : 0;
+  a.merge = p.fuse && mixed ? 1 : 0;
   a.N = (int)N; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.P = (int)P; a.S = (int)S;
-  a.WRp = p.WRp; a.WKp = p.WKp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;
+  a.WRp = p.WRp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;
   a.nsplit_s = p.nsplit_s; a.chunk_s = p.chunk_s; a.n_prefix_items = p.n_prefix_items;
-  a.item0 = p.rows_mode ? p.n_prefix_items : 0;
   a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   prof_before(kKPrefixPartial, s);
-  if (p.rows_mode && p.n_prefix_items > 0) {
-    if (p.WRp == 4)
-      hipLaunchKernelGGL(prefix_rows_kernel<4>, dim3((unsigned)p.n_prefix_items), dim3(256), 0, s, a);
-    else
+  if (mixed) {
+    hipLaunchKernelGGL(prefix_mixed_kernel, dim3((unsigned)p.n_items), dim3(256), 0, s, a);
+    VMK_CHECK_HIP(hipGetLastError());
+  } else {
+    if (p.n_prefix_items > 0) {
       hipLaunchKernelGGL(prefix_rows_kernel<8>, dim3((unsigned)p.n_prefix_items), dim3(512), 0, s, a);
-    VMK_CHECK_HIP(hipGetLastError());
-  }
-  if (p.n_items - a.item0 > 0) {
-    hipLaunchKernelGGL(prefix_partial_kernel, dim3((unsigned)(p.n_items - a.item0)), dim3(256), 0, s, a);
-    VMK_CHECK_HIP(hipGetLastError());
+      VMK_CHECK_HIP(hipGetLastError());
+    }
+    if (p.n_items > p.n_prefix_items) {
+      hipLaunchKernelGGL(prefix_partial_kernel, dim3((unsigned)(p.n_items - p.n_prefix_items)), dim3(256), 0, s, a);
+      VMK_CHECK_HIP(hipGetLastError());
+    }
   }
   prof_after(kKPrefixPartial, s);
-  if (!p.fuse) {
+  if (a.merge) {
+    prof_before(kKPrefixCombine, s);
+    hipLaunchKernelGGL(prefix_merge_kernel, dim3((unsigned)(N * Hkv)), dim3(256), 0, s, a);
+    prof_after(kKPrefixCombine, s);
+    VMK_CHECK_HIP(hipGetLastError());
+  } else if (!a.fuse) {
     prof_before(kKPrefixCombine, s);
     hipLaunchKernelGGL(prefix_combine_kernel, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
     prof_after(kKPrefixCombine, s);

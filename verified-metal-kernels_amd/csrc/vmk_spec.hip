@@ -184,14 +184,12 @@ static SpecPlan spec_plan(int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_
   const int64_t rows_wg = 32 * p.WR;
   p.nrb = (int)((R + rows_wg - 1) / rows_wg);
   const int64_t base = B * Hkv * p.nrb;
-  const int64_t max_split = (L + kTile * p.WK - 1) / (kTile * p.WK);
-  // Both kinds hold one CU's LDS: aim at ~256 long-lived workgroups, and keep the fp32 partials (which grow with the
-  // rows) under ~8 % of the K/V stream.
-  int64_t ns = (256 + base - 1) / base;     // about one long-lived workgroup per CU
-  const int64_t cap = std::max<int64_t>(1, (int64_t)(0.08 * (double)L / (double)(p.nrb * rows_wg)));
-  ns = std::max<int64_t>(1, std::min(ns, std::min(max_split, cap)));
-  int64_t chunk = (L + ns - 1) / ns;
-  chunk = (chunk + kTile - 1) / kTile * kTile;
+  // The split size depends on the rows of one group (kd * G) only, never on B: a batch entry goes through the same
+  // key splits, tile order and merge as the same entry alone, so its rows are bit-equal (batch invariance).  Key
+  // split: 2048 keys up to 16 rows (decode: 256 workgroups once B * Hkv * L reaches 2^19), then 128 keys per row
+  // (C3: 4096), which keeps the fp32 partials at 1/64 of the K/V bytes.  Row split: 4096 keys, 16 per row beyond.
+  const int64_t chunk = p.rows_mode ? std::max<int64_t>(4096, 16 * R)
+                                    : std::min<int64_t>(8192, std::max<int64_t>(2048, 128 * R));
   p.chunk = (int)chunk;
   p.nsplit = (int)((L + chunk - 1) / chunk);
   const size_t items = (size_t)base * p.nsplit;

@@ -26,6 +26,13 @@ L3_CASES = [(dict(B=2, L=8192), "randn"), (dict(B=1, L=32768), "randn"), (dict(B
 # This build's ragged extension: lens ~ U[L_min, L].
 EXTRA = [(dict(B=6, L=5000, L_min=1), "randn"), (dict(B=8, L=2048, L_min=1), "needle"),
          (dict(B=3, L=40000, L_min=30000), "randn")]
+# Row invariance (L4): every request decoded alone (B = 1) must give the same bits as in the batch.
+L4_CASES = [(dict(B=8, L=8192), "randn"), (dict(B=6, L=5000, L_min=1), "randn"), (dict(B=4, L=16384), "needle")]
+
+
+def row_inputs(inp, i):
+    """Request i alone."""
+    return {k: (x[i:i + 1] if x is not None else None) for k, x in inp.items()}
 
 
 def make_inputs(shape, seed=0, dist="randn", device="cpu"):

@@ -137,6 +137,19 @@ L3_CASES = [(dict(N=8, P=1024, S=128), "randn"), (dict(N=8, P=32768, S=1024), "r
 # Cases this build adds for its own extensions (ragged suffixes, K outliers); judged like L2.
 EXTRA = [(dict(N=5, P=700, S=300, S_min=1), "randn"), (dict(N=16, P=2048, S=512, S_min=128), "outlier"),
          (dict(N=3, P=1, S=64, S_min=1), "randn")]
+# Row invariance (L4, ONE-PAGER.md:13-14): every request computed alone (N = 1) must give the same bits as in the
+# batch.  The C2 and C1 shapes, a prefix of many chunks with suffixes split over two chunks, and odd sizes.
+L4_CASES = [(dict(N=64, P=16384, S=2048, S_min=128), "outlier"), (dict(N=8, P=2048, S=256), "randn"),
+            (dict(N=20, P=40000, S=3000, S_min=1), "randn"), (dict(N=33, P=300, S=10), "randn")]
+
+
+def row_inputs(inp, i):
+    """Request i alone: its query, suffix rows and length, with the shared prefix unchanged."""
+    out = dict(inp)
+    for k in ("q", "ks", "vs", "slens"):
+        if inp.get(k) is not None:
+            out[k] = inp[k][i:i + 1]
+    return out
 
 
 def algorithmic_bytes(shape, slens=None):

@@ -158,6 +158,14 @@ L3_CASES = [(dict(B=1, L=1024, k=8), "randn"), (dict(B=1, L=32768, k=8), "randn"
 # Cases this build adds for kd > 32 (multi-word masks) and the bounded tree; judged like L2.
 EXTRA = [(dict(B=2, L=4096, k=64), "tree_bd"), (dict(B=1, L=70, k=64), "needle_masked"),
          (dict(B=1, L=5000, k=33), "randn"), (dict(B=2, L=3000, k=64), "chain")]
+# Row invariance (L4): every batch entry verified alone (B = 1) must give the same bits as in the batch.
+L4_CASES = [(dict(B=4, L=32768, k=8), "chain"), (dict(B=2, L=65536, k=64), "tree_bd"),
+            (dict(B=3, L=5000, k=5), "randn"), (dict(B=5, L=777, k=33), "randn")]
+
+
+def row_inputs(inp, i):
+    """Batch entry i alone."""
+    return {k: (x[i:i + 1] if x is not None else None) for k, x in inp.items()}
 
 
 def algorithmic_bytes(shape):
