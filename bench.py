@@ -34,7 +34,8 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16 MFMA
 METRIC = "µs/call per op + achieved HBM GB/s (% of MI355X peak) at bench shapes"
 HEADLINE = "C2"
-DOMINANT = {"prefix": "prefix_partial", "spec": "spec_partial", "dsa": "dsa_indexer", "decode": "spec_partial"}
+DOMINANT = {"prefix": "prefix_partial", "spec": "spec_partial", "dsa": "dsa_indexer", "decode": "spec_partial",
+            "prefix_paged": "prefix_partial"}
 
 
 def log(*a):
@@ -42,12 +43,12 @@ def log(*a):
 
 
 def config_table():
-    from vmk.ops import decode, dsa, prefix, spec
+    from vmk.ops import decode, dsa, prefix, prefix_paged, spec
     return [("C1", "prefix", *prefix.CONFIGS["C1"]), ("C2", "prefix", *prefix.CONFIGS["C2"]),
             ("C3", "spec", *spec.CONFIGS["C3"]), ("C4", "spec", *spec.CONFIGS["C4"]),
             ("C5", "dsa", *dsa.CONFIGS["C5"]),
             ("D1", "decode", *decode.CONFIGS["D1"]), ("D2", "decode", *decode.CONFIGS["D2"]),
-            ("D3", "decode", *decode.CONFIGS["D3"])]
+            ("D3", "decode", *decode.CONFIGS["D3"]), ("P2", "prefix_paged", *prefix_paged.CONFIGS["P2"])]
 
 
 class HipEvents:
@@ -87,14 +88,19 @@ def call_op(opname, inp):
         return vmk.spec_verify(inp["q"], inp["k"], inp["v"], inp["words"])
     if opname == "decode":
         return vmk.decode(inp["q"], inp["k"], inp["v"], inp.get("lens"))
+    if opname == "prefix_paged":
+        return vmk.prefix_decode_paged(inp["q"], inp["k_pages"], inp["v_pages"], inp["prefix_pages"],
+                                       inp["suffix_pages"], inp.get("slens"))
     return vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], inp.get("lens"))
 
 
 def std_op(opname, inp):
     """The PyTorch standard op used by the reference's output check (L1_REF of each op)."""
-    from vmk.ops import decode, dsa, prefix, spec
+    from vmk.ops import decode, dsa, prefix, prefix_paged, spec
     if opname == "prefix":
         return prefix.torch_naive(**{k: inp[k] for k in ("q", "kp", "vp", "ks", "vs", "slens")})
+    if opname == "prefix_paged":
+        return prefix_paged.torch_naive(**inp)
     if opname == "spec":
         return spec.torch_sdpa(inp["q"], inp["k"], inp["v"], inp["bits"])
     if opname == "decode":
@@ -103,7 +109,12 @@ def std_op(opname, inp):
 
 
 def op_bytes_flops(opname, shape, inp_host):
-    from vmk.ops import decode, dsa, prefix, spec
+    from vmk.ops import decode, dsa, prefix, prefix_paged, spec
+    if opname == "prefix_paged":
+        sl = None if inp_host.get("slens") is None else inp_host["slens"].numpy()
+        total = prefix_paged.algorithmic_bytes(shape, sl)
+        out = shape["N"] * prefix.HQ * prefix.D * 2
+        return total, total - out, prefix_paged.flops(shape, sl)
     if opname == "prefix":
         sl = None if inp_host.get("slens") is None else inp_host["slens"].numpy()
         total = prefix.algorithmic_bytes(shape, sl)
@@ -131,7 +142,7 @@ def distinct_sets(opname, inp0, total_bytes):
     n = max(2, int(math.ceil((1 << 30) / max(total_bytes, 1))))
     sets = [inp0]
     big = {"prefix": ("q", "kp", "vp", "ks", "vs"), "spec": ("q", "k", "v"), "dsa": ("q", "kv", "iq", "ik"),
-           "decode": ("q", "k", "v")}[opname]
+           "decode": ("q", "k", "v"), "prefix_paged": ("q", "k_pages", "v_pages")}[opname]
     g = torch.Generator(device="cuda")
     g.manual_seed(1234)
     for _ in range(n - 1):
@@ -170,6 +181,15 @@ def cpu_baseline(opname, shape, dist, inp_host, total_bytes):
             oracle.spec.ref64(inp_host["q"][:1], inp_host["k"][:1], inp_host["v"][:1], inp_host["bits"][:1])
             dt = (time.perf_counter() - t0) * B
             sample = f"batch 0 of {B}, time scaled x{B}"
+        elif opname == "prefix_paged":
+            N = shape["N"]
+            ns = min(N, 8)
+            sub = dict(inp_host, q=inp_host["q"][:ns], suffix_pages=inp_host["suffix_pages"][:ns],
+                       slens=None if inp_host.get("slens") is None else inp_host["slens"][:ns])
+            t0 = time.perf_counter()
+            oracle.prefix_paged.ref64(**sub)
+            dt = (time.perf_counter() - t0) * N / ns
+            sample = f"requests 0-{ns - 1} of {N}, time scaled x{N / ns:g}"
         elif opname == "decode":
             B = shape["B"]
             t0 = time.perf_counter()
@@ -204,7 +224,7 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     snap = {k: v.clone() for k, v in inp0.items() if isinstance(v, torch.Tensor)}
     out = call_op(opname, inp0)
     torch.cuda.synchronize()
-    mutated = [k for k, v in snap.items() if not torch.equal(v, inp0[k])]
+    mutated = [k for k, v in snap.items() if not torch.equal(v.view(torch.uint8), inp0[k].view(torch.uint8))]  # bits
     ref = std_op(opname, inp0)
     torch.cuda.synchronize()
     ok = (not mutated) and out.shape == ref.shape and bool(
@@ -268,7 +288,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3")
+    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle timings")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="first run a plain streaming kernel that reads BYTES and writes BYTES (torch.bitwise_not "

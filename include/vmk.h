@@ -78,6 +78,25 @@ int vmk_prefix_decode(const void* q, const void* kp, const void* vp, const void*
                       const void* slens, void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t P,
                       int64_t S, int64_t ragged, void* workspace, size_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------------------- paged shared prefix
+ * No kernel of the reference covers it: README.md:141-142 leaves the paged-cache variant of the shared-prefix kernel
+ * out of the package.  Same op as vmk_prefix_decode with the keys and values in a page pool (the layout FlashInfer
+ * calls HND):
+ *   k_pages, v_pages  (num_pages, Hkv, page_size, D)  fp16   page pool; page_size a multiple of 32
+ *   prefix_pages      (P / page_size,)                int32  the shared prefix's pages (P a whole number of pages)
+ *   suffix_pages      (N, max_suffix_pages)           int32  each request's suffix pages
+ *   slens             (N,)                            int32  suffix rows in use (clamped to [0, max_suffix_pages *
+ *                                                            page_size]), or NULL: every suffix is full
+ * A page id outside [0, num_pages) is an absent page: its rows are left out of the softmax (no memory is read for
+ * it).  With every page present the output is bit-equal to vmk_prefix_decode on the gathered cache with
+ * S = max_suffix_pages * page_size. */
+size_t vmk_prefix_paged_workspace_size(int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int64_t page_size,
+                                       int64_t max_suffix_pages);
+int vmk_prefix_decode_paged(const void* q, const void* k_pages, const void* v_pages, const void* prefix_pages,
+                            const void* suffix_pages, const void* slens, void* out, int64_t N, int64_t Hq,
+                            int64_t Hkv, int64_t D, int64_t num_pages, int64_t page_size, int64_t P,
+                            int64_t max_suffix_pages, void* workspace, size_t ws_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------------------------- DSA decode
  * Replaces kernel(q, kv, iq, ik, w, lens) of kernels/dsa_opus55_v7.py:946-977 (op contract ops/dsa.py:1-9, 53-83).
  *   q     (B, 128, 576)  fp16    absorbed queries (512 latent + 64 rope)

@@ -52,6 +52,9 @@ def test_workspace_queries_reject_bad_shapes(lib):
     assert lib.vmk_decode_workspace_size(2, 32, 8, 64, 100) == 0          # D != 128
     assert lib.vmk_decode_workspace_size(2, 32, 8, 128, 0) == 0           # no cache positions
     assert lib.vmk_decode_workspace_size(2, 32, 8, 128, 65536) > 0
+    assert lib.vmk_prefix_paged_workspace_size(8, 32, 8, 128, 2048, 48, 4) == 0     # page size not a multiple of 32
+    assert lib.vmk_prefix_paged_workspace_size(8, 32, 8, 128, 2000, 64, 4) == 0     # P not a whole number of pages
+    assert lib.vmk_prefix_paged_workspace_size(8, 32, 8, 128, 2048, 64, 4) > 0
     assert lib.vmk_dsa_workspace_size(0, 100) == 0
     assert lib.vmk_dsa_workspace_size(4, 65536) > 4 * 65536 * 4
 
@@ -72,6 +75,12 @@ def test_entry_points_reject_before_launch(lib):
     assert rc == 1 and b"null pointer" in lib.vmk_last_error()
     rc = lib.vmk_decode(fake, fake, fake, None, fake, 2, 32, 8, 128, 100, fake, 64, None)
     assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
+    rc = lib.vmk_prefix_decode_paged(fake, fake, fake, None, fake, None, fake, 4, 32, 8, 128, 100, 64, 128, 2, fake,
+                                     1 << 30, None)
+    assert rc == 1 and b"null pointer" in lib.vmk_last_error()
+    rc = lib.vmk_prefix_decode_paged(fake, fake, fake, fake, fake, None, fake, 4, 32, 8, 128, 100, 48, 96, 2, fake,
+                                     1 << 30, None)
+    assert rc == 1 and b"page_size" in lib.vmk_last_error()
     rc = lib.vmk_dsa_decode(fake, fake, fake, fake, fake, None, fake, fake, fake, 2, 5000, fake, 1024, None)
     assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
     rc = lib.vmk_dsa_decode(fake, fake, fake, fake, None, None, fake, fake, fake, 2, 5000, fake, 1 << 30, None)

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from vmk.ops import KEYS, decode, dsa, prefix, spec
+from vmk.ops import KEYS, decode, dsa, prefix, prefix_paged, spec
 
 pytestmark = pytest.mark.gpu
 
@@ -55,3 +55,11 @@ def test_dsa_rows_alone_equal_batch(shape, dist):
     import dsa_mi355x
     print(f"dsa L4 {shape} {dist}", flush=True)
     assert run(dsa_mi355x.kernel, dsa, shape, dist, 34) == []
+
+
+@pytest.mark.parametrize("shape,dist", [(dict(N=64, P=16384, S=2048, S_min=128, ps=64), "outlier"),
+                                        (dict(N=12, P=3072, S=2500, S_min=1, ps=128, absent=2), "randn")])
+def test_prefix_paged_rows_alone_equal_batch(shape, dist):
+    import prefix_paged_mi355x
+    print(f"prefix_paged L4 {shape} {dist}", flush=True)
+    assert run(prefix_paged_mi355x.kernel, prefix_paged, shape, dist, 35) == []

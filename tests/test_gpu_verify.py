@@ -24,7 +24,8 @@ def run_verify(path, tmp_path, *extra):
 
 
 @pytest.mark.timeout(900)
-@pytest.mark.parametrize("name", ["spec_mi355x.py", "prefix_mi355x.py", "dsa_mi355x.py", "decode_mi355x.py"])
+@pytest.mark.parametrize("name", ["spec_mi355x.py", "prefix_mi355x.py", "dsa_mi355x.py", "decode_mi355x.py",
+                                  "prefix_paged_mi355x.py"])
 def test_kernel_module_is_correct(name, tmp_path):
     rc, rep = run_verify(os.path.join(KDIR, name), tmp_path)
     assert rep["verdict"] == "CORRECT" and rc == 0

@@ -13,9 +13,9 @@ import torch
 import torch.nn.functional as F
 
 import oracle
-from oracle import decode as odecode, dsa as odsa, prefix as oprefix, spec as ospec
+from oracle import decode as odecode, dsa as odsa, prefix as oprefix, prefix_paged as opaged, spec as ospec
 from oracle.common import softmax_attend, to64
-from vmk.ops import decode, dsa, prefix, spec
+from vmk.ops import decode, dsa, prefix, prefix_paged, spec
 
 
 def t64(x):
@@ -443,6 +443,83 @@ def test_decode_identities():
 def test_decode_checks_catch_planted_mistakes(kind):
     bad = decode_mutant(kind)
     assert not (all(decode_vs_torch(bad, s, dist=d) for s, d in DECODE_SHAPES) and decode_closed_forms(bad))
+
+
+PAGED_SHAPES = [(dict(N=3, P=128, S=77, ps=32), "randn"), (dict(N=4, P=192, S=200, S_min=0, ps=64), "randn"),
+                (dict(N=2, P=0, S=90, ps=32), "randn"), (dict(N=4, P=384, S=256, ps=96), "nan_inf"),
+                (dict(N=3, P=256, S=130, S_min=1, ps=128), "needle_suffix")]
+
+
+def paged_equals_contiguous(ref, shape, seed=0, dist="randn"):
+    """With every page present the op is the contiguous op on the same draws (the generator scatters those draws):
+    the paged oracle must give the contiguous oracle's float64 bits."""
+    inp = prefix_paged.make_inputs(shape, seed=seed, dist=dist)
+    c = prefix.make_inputs({k: v for k, v in shape.items() if k != "ps"}, seed=seed, dist=dist)
+    if inp["slens"] is not None and c["slens"] is None:
+        c["slens"] = inp["slens"]
+    return np.array_equal(ref(**inp), oprefix.ref64(**c), equal_nan=True)
+
+
+def paged_absent_vs_torch(ref, shape, seed=0):
+    """Absent pages: torch float64 SDPA over a dense cache from which the absent pages' rows are deleted."""
+    inp = prefix_paged.make_inputs(shape, seed=seed)
+    kpool, vpool = t64(inp["k_pages"]), t64(inp["v_pages"])
+    num_pages, Hkv, ps, d = kpool.shape
+    pp, sp = inp["prefix_pages"].tolist(), inp["suffix_pages"].tolist()
+    S = len(sp[0]) * ps
+    outs = []
+    for n in range(inp["q"].shape[0]):
+        sn = S if inp["slens"] is None else min(max(int(inp["slens"][n]), 0), S)
+        rows_k, rows_v = [], []
+        for j, p in enumerate(pp):
+            if 0 <= p < num_pages:
+                rows_k.append(kpool[p]), rows_v.append(vpool[p])
+        for j, p in enumerate(sp[n]):
+            take = min(ps, sn - j * ps)
+            if take > 0 and 0 <= p < num_pages:
+                rows_k.append(kpool[p, :, :take]), rows_v.append(vpool[p, :, :take])
+        k, v = torch.cat(rows_k, 1), torch.cat(rows_v, 1)
+        outs.append(F.scaled_dot_product_attention(t64(inp["q"][n:n + 1])[:, :, None], k[None], v[None],
+                                                   enable_gqa=True)[0, :, 0])
+    return np.allclose(ref(**inp), torch.stack(outs).numpy(), rtol=1e-9, atol=1e-9, equal_nan=True)
+
+
+def paged_mutant(kind):
+    def out(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None):
+        pp, sp = prefix_pages.clone(), suffix_pages.clone()
+        if kind == "table_order_ignored":              # pages taken in pool order instead of table order
+            pp = pp.sort().values
+            sp = sp.sort(1).values
+        elif kind == "absent_as_page0":                 # an absent page read as page 0
+            pp, sp = pp.clamp(min=0), sp.clamp(min=0)
+        elif kind == "slens_ignored":
+            slens = None
+        return opaged.ref64(q, k_pages, v_pages, pp, sp, slens)
+    return out
+
+
+@pytest.mark.parametrize("shape,dist", PAGED_SHAPES)
+def test_paged_oracle_equals_contiguous(shape, dist):
+    assert paged_equals_contiguous(opaged.ref64, shape, dist=dist)
+
+
+def test_paged_oracle_absent_pages_vs_torch():
+    assert paged_absent_vs_torch(opaged.ref64, dict(N=6, P=3072, S=500, S_min=0, ps=64, absent=3), seed=5)
+    assert paged_absent_vs_torch(opaged.ref64, dict(N=5, P=640, S=40, ps=32, absent=2), seed=6)
+
+
+def test_paged_standard_op_vs_oracle():
+    inp = prefix_paged.make_inputs(dict(N=6, P=3072, S=500, S_min=0, ps=64, absent=3), seed=5)
+    d = {k: (v.double() if v is not None and v.dtype == torch.float16 else v) for k, v in inp.items()}
+    assert np.allclose(prefix_paged.torch_naive(**d).numpy(), opaged.ref64(**inp), rtol=1e-9, atol=1e-9)
+
+
+@pytest.mark.parametrize("kind", ["table_order_ignored", "absent_as_page0", "slens_ignored"])
+def test_paged_checks_catch_planted_mistakes(kind):
+    bad = paged_mutant(kind)
+    ok = all(paged_equals_contiguous(bad, s, dist=d) for s, d in PAGED_SHAPES) and \
+        paged_absent_vs_torch(bad, dict(N=6, P=3072, S=500, S_min=0, ps=64, absent=3), seed=5)
+    assert not ok
 
 
 def test_oracle_is_test_infrastructure():

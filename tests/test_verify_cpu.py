@@ -14,7 +14,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 KDIR = os.path.join(os.path.dirname(HERE), "verified-metal-kernels_amd", "kernels")
 
 
-@pytest.mark.parametrize("name", ["spec_mi355x.py", "prefix_mi355x.py", "dsa_mi355x.py", "decode_mi355x.py"])
+@pytest.mark.parametrize("name", ["spec_mi355x.py", "prefix_mi355x.py", "dsa_mi355x.py", "decode_mi355x.py",
+                                  "prefix_paged_mi355x.py"])
 def test_gate_accepts_shipped_kernels(name):
     assert verify.gate(open(os.path.join(KDIR, name)).read()) == []
 
@@ -74,13 +75,14 @@ def test_missing_cases_are_failures_without_gpu(tmp_path, monkeypatch):
     assert rep["verdict"] == "REJECTED" and rep["L1_pass"] == 0 and "missing" in rep["L1"][0]["error"]
 
 
-@pytest.mark.parametrize("opname", ["prefix", "spec", "dsa", "decode"])
+@pytest.mark.parametrize("opname", ["prefix", "spec", "dsa", "decode", "prefix_paged"])
 def test_l4_row_inputs_slice_one_batch_row(opname):
     """row_inputs(i) is batch row i of every per-row input (CPU tensors, the smallest L4-like shape of each op)."""
     from vmk.ops import KEYS, load_op
     op = load_op(opname)
     shape, dist = {"prefix": (dict(N=3, P=40, S=9, S_min=1), "randn"), "spec": (dict(B=3, L=40, k=5), "randn"),
-                   "dsa": (dict(B=3, L=300), "ragged"), "decode": (dict(B=3, L=50, L_min=1), "randn")}[opname]
+                   "dsa": (dict(B=3, L=300), "ragged"), "decode": (dict(B=3, L=50, L_min=1), "randn"),
+                   "prefix_paged": (dict(N=3, P=64, S=40, S_min=1, ps=32), "randn")}[opname]
     inp = {k: v for k, v in op.make_inputs(shape, seed=1, dist=dist).items() if k in KEYS[opname]}
     assert op.L4_CASES
     for i in range(3):
@@ -89,7 +91,8 @@ def test_l4_row_inputs_slice_one_batch_row(opname):
         for k, v in inp.items():
             if v is None:
                 assert r[k] is None
-            elif opname == "prefix" and k in ("kp", "vp"):
+            elif (opname, k) in (("prefix", "kp"), ("prefix", "vp"), ("prefix_paged", "k_pages"),
+                                 ("prefix_paged", "v_pages"), ("prefix_paged", "prefix_pages")):
                 assert r[k] is v                              # the shared prefix is not sliced
             else:
                 assert r[k].shape[0] == 1 and (r[k][0] == v[i]).all()
@@ -109,3 +112,9 @@ def test_l4_judgement_flags_the_differing_rows():
     assert same["ok"]                                          # bit comparison: equal NaN bits are equal
     missing = verify.l4_case({}, {}, 0, {}, "randn")
     assert not missing["ok"] and "missing" in missing["error"]
+
+
+def test_infer_op_takes_the_longest_op_name():
+    assert verify.infer_op("x/prefix_paged_mi355x.py") == "prefix_paged"
+    assert verify.infer_op("prefix_mi355x.py") == "prefix"
+    assert verify.infer_op("kernel.py") is None

@@ -48,7 +48,8 @@ import numpy as np  # noqa: E402
 
 from vmk.ops import KEYS, load_op  # noqa: E402
 
-ORACLE = {"prefix": "oracle.prefix", "spec": "oracle.spec", "dsa": "oracle.dsa", "decode": "oracle.decode"}
+ORACLE = {"prefix": "oracle.prefix", "spec": "oracle.spec", "dsa": "oracle.dsa", "decode": "oracle.decode",
+          "prefix_paged": "oracle.prefix_paged"}
 
 
 def cand_inputs(opname, inp):
@@ -333,11 +334,10 @@ def summary(rep, max_fail=6):
 
 
 def infer_op(path):
+    """The longest op name that the file name starts with (prefix_paged_x.py is prefix_paged, not prefix)."""
     base = os.path.basename(path)
-    for op in KEYS:
-        if base.startswith(op + "_"):
-            return op
-    return None
+    hits = [op for op in KEYS if base.startswith(op + "_")]
+    return max(hits, key=len) if hits else None
 
 
 def main(argv=None):

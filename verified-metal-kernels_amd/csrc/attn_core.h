@@ -45,6 +45,8 @@ __device__ __forceinline__ u32x4 sel16(bool keep, u32x4 x) {
 // outside the sequence, so a tile's spare rows are zeros and p = 0 never meets a non-finite value of a foreign row,
 // and the Q source of rows outside the workgroup's range.
 __device__ const f16 g_zero_row[128] = {};
+// One zero tile (32 rows): the K or V tile of a key range that has no memory (an absent page of a paged cache).
+__device__ __attribute__((aligned(16))) const f16 g_zero_tile[32 * 128] = {};
 
 // Q^T operand for 128 head-dims of one row (qrow must be a valid row); zeros when !valid, read from g_zero_row rather
 // than selected after the load, so nothing waits for these loads before the first MFMA that uses them (a select would
@@ -237,11 +239,12 @@ __device__ __forceinline__ void issue_dma(char* __restrict__ stage, const Src& s
   const int j = i & 7;
   char* dst = stage + (i < 8 ? 0 : 8192) + j * 1024;
   const char* gp;
+  const f16* tile = i < 8 ? src.ktile(key0) : src.vtile(key0);
   if (full) {
-    gp = reinterpret_cast<const char*>((i < 8 ? src.kbase : src.vbase) + (size_t)key0 * 128) + off;
+    gp = reinterpret_cast<const char*>(tile) + off;
   } else {
     const int row = 4 * j + (lane >> 4);
-    gp = reinterpret_cast<const char*>(i < 8 ? src.krow(key0 + row) : src.vrow(key0 + row)) + (off & 255);
+    gp = reinterpret_cast<const char*>(key0 + row < src.kend ? tile + row * 128 : g_zero_row) + (off & 255);
   }
   __builtin_amdgcn_global_load_lds(VMK_GPTR(gp), VMK_LPTR(dst), 16, 0, 0);
 }
@@ -354,9 +357,9 @@ __device__ __forceinline__ void ring_walk(char* ring, const Src& src, int kbeg, 
 // (NS - 1 tiles in flight while one is computed; NS <= 4 keeps the wait counts within vmcnt's range), unrolled by NS
 // so every stage offset is a compile-time constant.  ring is this wave's ring (DMA destinations); base is the LDS
 // address the read offsets of tl are relative to (they include the ring's offset from it).
-// The key source `src` provides: kbase / vbase (row 0 of the sequence part), krow(key) / vrow(key) (in-bounds row
-// pointers; keys at or past kend give g_zero_row), kend, scale (log2-domain softmax scale) and mask(s, key0, g)
-// (masked scores of the raw S^T tile -> -inf).
+// The key source `src` provides: ktile(key0) / vtile(key0) (the 32 contiguous K / V rows of the tile starting at
+// key0, a multiple of 32 from the range start; rows at or past kend are not read), kend, scale (log2-domain softmax
+// scale) and mask(s, key0, g) (masked scores of the raw S^T tile -> -inf).
 template <int NS, class Src>
 __device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], char* __restrict__ ring,
                                           const char* __restrict__ base, const TileLanes& tl, const Src& src,

@@ -125,8 +125,8 @@ struct IkSrc {
   const f16* kbase;
   const f16* vbase;
   int kend;
-  __device__ const f16* krow(int key) const { return key < kend ? kbase + (size_t)key * kDI : g_zero_row; }
-  __device__ const f16* vrow(int key) const { return krow(key); }
+  __device__ const f16* ktile(int key0) const { return kbase + (size_t)key0 * kDI; }
+  __device__ const f16* vtile(int key0) const { return ktile(key0); }
 };
 
 // S = iq . ik^T per 32-position tile (M = 64 heads as two 32-row MFMA tiles, N = positions, K = 128 dims), then

@@ -19,10 +19,13 @@ namespace vmk {
 
 struct PrefixArgs {
   const f16* q;            // (N, Hq, 128)
-  const f16* kp;           // (Hkv, P, 128)
-  const f16* vp;
-  const f16* ks;           // (N, Hkv, S, 128)
+  const f16* kp;           // (Hkv, P, 128); paged: the K page pool (num_pages, Hkv, ps, 128)
+  const f16* vp;           // paged: the V page pool
+  const f16* ks;           // (N, Hkv, S, 128); paged: unused
   const f16* vs;
+  const int* prefix_pages; // paged: (P / ps,) page ids of the shared prefix
+  const int* suffix_pages; // paged: (N, max_sp) page ids of each request's suffix (S = max_sp * ps)
+  int ps, max_sp, num_pages;
   const int* slens;        // (N,) or null
   f16* out;                // (N, Hq, 128)
   float* po_p;             // prefix partials [h][rb][split][32*WRp][128]
@@ -44,8 +47,8 @@ struct RangeSrc {
   const f16* vbase;
   int kend;
   float scale;
-  __device__ const f16* krow(int key) const { return key < kend ? kbase + (size_t)key * 128 : g_zero_row; }
-  __device__ const f16* vrow(int key) const { return key < kend ? vbase + (size_t)key * 128 : g_zero_row; }
+  __device__ const f16* ktile(int key0) const { return kbase + (size_t)key0 * 128; }
+  __device__ const f16* vtile(int key0) const { return vbase + (size_t)key0 * 128; }
   __device__ void mask(floatx16& s, int key0, int g) const {
     if (key0 + kTile <= kend) return;                      // whole tile inside (same for the whole wave)
 #pragma unroll
@@ -57,6 +60,58 @@ struct RangeSrc {
       }
   }
 };
+
+// Keys [kbeg, kend) of one KV head of a sequence in a paged cache: pages of ps rows (ps a multiple of 32, so a tile
+// never straddles two pages) laid out (num_pages, Hkv, ps, 128), the sequence's pages listed in `table`.  Lane i
+// holds the id of the range's i-th page (a range of at most 2048 keys spans at most 64 pages), so a tile finds its
+// page with one readlane.  An id outside [0, num_pages) is an absent page: its tiles read a zero tile and its keys
+// are masked out.
+struct PagedSrc {
+  const f16* kpool;        // page 0 of this KV head
+  const f16* vpool;
+  size_t page_stride;      // elements from one page to the next (Hkv * ps * 128)
+  int ps, first, npages, kend;
+  int pid;                 // this lane's page id: table[first + lane]
+  float scale;
+  __device__ int page(int key0) const { return __builtin_amdgcn_readlane(pid, key0 / ps - first); }
+  __device__ bool present(int p) const { return (unsigned)p < (unsigned)npages; }
+  __device__ const f16* ktile(int key0) const {
+    const int p = page(key0);
+    return present(p) ? kpool + (size_t)p * page_stride + (size_t)(key0 % ps) * 128 : g_zero_tile;
+  }
+  __device__ const f16* vtile(int key0) const {
+    const int p = page(key0);
+    return present(p) ? vpool + (size_t)p * page_stride + (size_t)(key0 % ps) * 128 : g_zero_tile;
+  }
+  __device__ void mask(floatx16& s, int key0, int g) const {
+    const bool here = present(page(key0));
+    if (here && key0 + kTile <= kend) return;              // whole tile inside (same for the whole wave)
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int key = key0 + 8 * blk + 4 * g + c;
+        s[4 * blk + c] = here && key < kend ? s[4 * blk + c] : kNegInf;
+      }
+  }
+};
+
+__device__ __forceinline__ PagedSrc paged_src(const PrefixArgs& a, const int* table, int ntable, int h, int kbeg,
+                                              int kend) {
+  PagedSrc s;
+  s.kpool = a.kp + (size_t)h * a.ps * 128;
+  s.vpool = a.vp + (size_t)h * a.ps * 128;
+  s.page_stride = (size_t)a.Hkv * a.ps * 128;
+  s.ps = a.ps;
+  s.first = kbeg / a.ps;
+  s.npages = a.num_pages;
+  s.kend = kend;
+  s.scale = a.sl2;
+  const int idx = s.first + (int)(threadIdx.x & 63);
+  const int last = kend > kbeg ? (kend - 1) / a.ps : -1;
+  s.pid = idx <= last && idx < ntable ? table[idx] : -1;
+  return s;
+}
 
 // Suffix length of request n, clamped to [0, S] so that a bad length can never read past its own rows.
 __device__ __forceinline__ int suffix_len(const PrefixArgs& a, int n) {
@@ -167,26 +222,10 @@ __device__ __forceinline__ void merge_prefetched_row(const PrefixArgs& a, const 
   out[1] = (f16)(num.y / den);
 }
 
-// Suffix item `sitem` (request, KV head, suffix chunk) of 4 waves.  Fused: the prefix partials are finished (an
-// earlier launch) and the item writes its rows' outputs; otherwise it writes its partial to po_s / pml_s.
-__device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int sitem) {
-  RangeSrc src;
-  src.scale = a.sl2;
-  const int split = sitem % a.nsplit_s;
-  int nh = sitem / a.nsplit_s, sn = 0;
-  if (a.order) {                                        // long suffixes are dispatched first
-    const int2 o = a.order[nh / a.Hkv];
-    nh = o.x * a.Hkv + nh % a.Hkv;
-    sn = o.y;
-  }
-  const int n = nh / a.Hkv, h = nh % a.Hkv;
-  const int kbeg = split * a.chunk_s;
-  if (!a.order) sn = suffix_len(a, n);
-  if (kbeg >= sn && !a.fuse && !a.merge) return;        // whole workgroup: nothing of this suffix is here
-  const size_t off = ((size_t)n * a.Hkv + h) * a.S * 128;
-  src.kbase = a.ks + off;
-  src.vbase = a.vs + off;
-  src.kend = min(sn, kbeg + a.chunk_s);
+// The walk and merge of a suffix item over key source src (keys [kbeg, src.kend)).
+template <class Src>
+__device__ __forceinline__ void suffix_walk(const PrefixArgs& a, char* smem, const Src& src, int n, int h, int nh,
+                                            int split, int kbeg) {
   const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
   auto qrow = [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; };
   if (!a.fuse) {
@@ -211,14 +250,44 @@ __device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int
   }
 }
 
-// Suffix items, after the prefix launch has written the prefix partials.
-__global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
-  suffix_item(a, smem, blockIdx.x);
+// Suffix item `sitem` (request, KV head, suffix chunk) of 4 waves.  Fused: the prefix partials are finished (an
+// earlier launch) and the item writes its rows' outputs; otherwise it writes its partial to po_s / pml_s.
+template <bool kPaged>
+__device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int sitem) {
+  const int split = sitem % a.nsplit_s;
+  int nh = sitem / a.nsplit_s, sn = 0;
+  if (a.order) {                                        // long suffixes are dispatched first
+    const int2 o = a.order[nh / a.Hkv];
+    nh = o.x * a.Hkv + nh % a.Hkv;
+    sn = o.y;
+  }
+  const int n = nh / a.Hkv, h = nh % a.Hkv;
+  const int kbeg = split * a.chunk_s;
+  if (!a.order) sn = suffix_len(a, n);
+  if (kbeg >= sn && !a.fuse && !a.merge) return;        // whole workgroup: nothing of this suffix is here
+  const int kend = min(sn, kbeg + a.chunk_s);
+  if constexpr (kPaged) {
+    suffix_walk(a, smem, paged_src(a, a.suffix_pages + (size_t)n * a.max_sp, a.max_sp, h, kbeg, kend), n, h, nh,
+                split, kbeg);
+  } else {
+    RangeSrc src;
+    src.scale = a.sl2;
+    const size_t off = ((size_t)n * a.Hkv + h) * a.S * 128;
+    src.kbase = a.ks + off;
+    src.vbase = a.vs + off;
+    src.kend = kend;
+    suffix_walk(a, smem, src, n, h, nh, split, kbeg);
+  }
 }
 
-// Prefix items when N*G > 64: NW waves own 32 of the N*G rows each and share one LDS ring, so the prefix chunk is
-// streamed from HBM once per 32*NW rows.
+
+// Suffix items, after the prefix launch has written the prefix partials.
+template <bool kPaged>
+__global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
+  suffix_item<kPaged>(a, smem, blockIdx.x);
+}
+
 // Counting sort of the requests by decreasing suffix length (256 buckets), run by one workgroup of the prefix
 // launch so the suffix launch can dispatch its longest items first.  Only the schedule depends on it: every item
 // computes the same values whatever order it runs in.
@@ -252,46 +321,57 @@ __device__ void build_suffix_order(const PrefixArgs& a, uint32_t* cnt /* LDS, 25
   __syncthreads();
 }
 
-template <int NW>
+// Prefix item (KV head h, row block rb, prefix chunk): NW waves own 32 of the N*G rows each and share one LDS ring,
+// so the prefix chunk is streamed from HBM once per 32*NW rows.
+template <int NW, bool kPaged>
 __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem, int item) {
   const int split = item % a.nsplit_p;
   const int rb = (item / a.nsplit_p) % a.nrb_p;
   const int h = item / (a.nsplit_p * a.nrb_p);
-  RangeSrc src;
-  src.scale = a.sl2;
-  const size_t off = (size_t)h * a.P * 128;
-  src.kbase = a.kp + off;
-  src.vbase = a.vp + off;
   const int kbeg = split * a.chunk_p;
-  src.kend = min(a.P, kbeg + a.chunk_p);
-  const int ntiles = (src.kend - kbeg + kTile - 1) / kTile;
+  const int kend = min(a.P, kbeg + a.chunk_p);
+  const int ntiles = (kend - kbeg + kTile - 1) / kTile;
   const int row0 = rb * NW * 32;
   const size_t rows_wg = 32 * NW;
-  attend_wg_rows<NW>(smem, src,
-                     [&](int r) {
-                       const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
-                       return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
-                     },
-                     a.N * a.G - row0, kbeg, ntiles, a.po_p + (size_t)item * rows_wg * 128,
-                     a.pml_p + (size_t)item * rows_wg * 2);
+  auto walk = [&](const auto& src) {
+    attend_wg_rows<NW>(smem, src,
+                       [&](int r) {
+                         const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
+                         return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
+                       },
+                       a.N * a.G - row0, kbeg, ntiles, a.po_p + (size_t)item * rows_wg * 128,
+                       a.pml_p + (size_t)item * rows_wg * 2);
+  };
+  if constexpr (kPaged) {
+    walk(paged_src(a, a.prefix_pages, a.P / a.ps, h, kbeg, kend));
+  } else {
+    RangeSrc src;
+    src.scale = a.sl2;
+    const size_t off = (size_t)h * a.P * 128;
+    src.kbase = a.kp + off;
+    src.vbase = a.vp + off;
+    src.kend = kend;
+    walk(src);
+  }
 }
 
-template <int NW>
+template <int NW, bool kPaged>
 __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kRowsSmemBytes];
   if (blockIdx.x == 0 && a.order) build_suffix_order<64 * NW>(a, reinterpret_cast<uint32_t*>(smem));
-  prefix_rows_item<NW>(a, smem, blockIdx.x);
+  prefix_rows_item<NW, kPaged>(a, smem, blockIdx.x);
 }
 
 // Both item kinds in one grid when a KV head has at most 128 rows: prefix items (4 waves sharing a ring) first, then
 // suffix items writing their partials.  No item depends on another.
 constexpr int kMixedSmemBytes = kRowsSmemBytes > kAttnSmemBytes ? kRowsSmemBytes : kAttnSmemBytes;
+template <bool kPaged>
 __global__ __launch_bounds__(256) void prefix_mixed_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kMixedSmemBytes];
   if ((int)blockIdx.x < a.n_prefix_items)
-    prefix_rows_item<4>(a, smem, blockIdx.x);
+    prefix_rows_item<4, kPaged>(a, smem, blockIdx.x);
   else
-    suffix_item(a, smem, blockIdx.x - a.n_prefix_items);
+    suffix_item<kPaged>(a, smem, blockIdx.x - a.n_prefix_items);
 }
 
 // After a mixed launch with whole suffixes: the final merge of the G rows of (request, KV head), by the functions a
@@ -382,6 +462,59 @@ static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int
   return p;
 }
 
+// Plan, workspace carve-up and launches of one prefix call (contiguous or paged; a's K/V pointers are set).
+template <bool kPaged>
+static int prefix_launch(PrefixArgs& a, const void* q, void* out, const void* slens, bool ragged, int64_t N,
+                         int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int64_t S, void* workspace, hipStream_t s) {
+  PrefixPlan p = prefix_plan(N, Hq, Hkv, P, S);
+  a.q = (const f16*)q;
+  a.slens = ragged ? (const int*)slens : nullptr;
+  a.out = (f16*)out;
+  a.po_p = (float*)align_up((char*)workspace + kWsHead, 256);
+  a.pml_p = (float*)align_up(a.po_p + p.po_p, 256);
+  a.po_s = (float*)align_up(a.pml_p + p.pml_p, 256);
+  a.pml_s = (float*)align_up(a.po_s + p.po_s, 256);
+  // Up to 128 rows per KV head, prefix and suffix items share one launch; a merge (or combine) launch follows.
+  // Beyond, the prefix launch runs first and whole-suffix items merge its partials themselves.
+  const bool mixed = p.WRp == 4;
+  // The schedule order is built by the prefix launch, so only when that runs before the suffix items.
+  a.order = (ragged && p.n_prefix_items > 0 && !mixed) ? (int2*)align_up(a.pml_s + p.pml_s, 256) : nullptr;
+  a.fuse = p.fuse && !mixed ? 1 : 0;
+  a.merge = p.fuse && mixed ? 1 : 0;
+  a.N = (int)N; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.P = (int)P; a.S = (int)S;
+  a.WRp = p.WRp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;
+  a.nsplit_s = p.nsplit_s; a.chunk_s = p.chunk_s; a.n_prefix_items = p.n_prefix_items;
+  a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
+  prof_before(kKPrefixPartial, s);
+  if (mixed) {
+    hipLaunchKernelGGL(prefix_mixed_kernel<kPaged>, dim3((unsigned)p.n_items), dim3(256), 0, s, a);
+    VMK_CHECK_HIP(hipGetLastError());
+  } else {
+    if (p.n_prefix_items > 0) {
+      hipLaunchKernelGGL((prefix_rows_kernel<8, kPaged>), dim3((unsigned)p.n_prefix_items), dim3(512), 0, s, a);
+      VMK_CHECK_HIP(hipGetLastError());
+    }
+    if (p.n_items > p.n_prefix_items) {
+      hipLaunchKernelGGL(prefix_partial_kernel<kPaged>, dim3((unsigned)(p.n_items - p.n_prefix_items)), dim3(256),
+                         0, s, a);
+      VMK_CHECK_HIP(hipGetLastError());
+    }
+  }
+  prof_after(kKPrefixPartial, s);
+  if (a.merge) {
+    prof_before(kKPrefixCombine, s);
+    hipLaunchKernelGGL(prefix_merge_kernel, dim3((unsigned)(N * Hkv)), dim3(256), 0, s, a);
+    prof_after(kKPrefixCombine, s);
+    VMK_CHECK_HIP(hipGetLastError());
+  } else if (!a.fuse) {
+    prof_before(kKPrefixCombine, s);
+    hipLaunchKernelGGL(prefix_combine_kernel, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
+    prof_after(kKPrefixCombine, s);
+    VMK_CHECK_HIP(hipGetLastError());
+  }
+  return 0;
+}
+
 }  // namespace vmk
 
 using namespace vmk;
@@ -410,53 +543,46 @@ extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, 
             "tensors must be 16-byte aligned");
   const size_t need = vmk_prefix_workspace_size(N, Hq, Hkv, D, P, S, ragged);
   VMK_CHECK(workspace && ws_bytes >= need, "workspace too small (query vmk_prefix_workspace_size)");
-  PrefixPlan p = prefix_plan(N, Hq, Hkv, P, S);
   PrefixArgs a;
   a.q = (const f16*)q; a.kp = (const f16*)kp; a.vp = (const f16*)vp; a.ks = (const f16*)ks; a.vs = (const f16*)vs;
-  a.slens = ragged ? (const int*)slens : nullptr;
-  a.out = (f16*)out;
-  a.po_p = (float*)align_up((char*)workspace + kWsHead, 256);
-  a.pml_p = (float*)align_up(a.po_p + p.po_p, 256);
-  a.po_s = (float*)align_up(a.pml_p + p.pml_p, 256);
-  a.pml_s = (float*)align_up(a.po_s + p.po_s, 256);
-  // The schedule order is built by the prefix launch, so only when that runs before the suffix items.
-  // Up to 128 rows per KV head, prefix and suffix items share one launch; a merge (or combine) launch follows.
-  // Beyond, the prefix launch runs first and whole-suffix items merge its partials themselves.
-  const bool mixed = p.WRp == 4;
-  // The schedule order is built by the prefix launch, so only when that runs before the suffix items.
-  a.order = (ragged && p.n_prefix_items > 0 && !mixed) ? (int2*)align_up(a.pml_s + p.pml_s, 256) : nullptr;
-  a.fuse = p.fuse && !mixed ? 1 : 0;
-  a.merge = p.fuse && mixed ? 1 : 0;
-  a.N = (int)N; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.P = (int)P; a.S = (int)S;
-  a.WRp = p.WRp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;
-  a.nsplit_s = p.nsplit_s; a.chunk_s = p.chunk_s; a.n_prefix_items = p.n_prefix_items;
-  a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
-  hipStream_t s = (hipStream_t)stream;
-  prof_before(kKPrefixPartial, s);
-  if (mixed) {
-    hipLaunchKernelGGL(prefix_mixed_kernel, dim3((unsigned)p.n_items), dim3(256), 0, s, a);
-    VMK_CHECK_HIP(hipGetLastError());
-  } else {
-    if (p.n_prefix_items > 0) {
-      hipLaunchKernelGGL(prefix_rows_kernel<8>, dim3((unsigned)p.n_prefix_items), dim3(512), 0, s, a);
-      VMK_CHECK_HIP(hipGetLastError());
-    }
-    if (p.n_items > p.n_prefix_items) {
-      hipLaunchKernelGGL(prefix_partial_kernel, dim3((unsigned)(p.n_items - p.n_prefix_items)), dim3(256), 0, s, a);
-      VMK_CHECK_HIP(hipGetLastError());
-    }
-  }
-  prof_after(kKPrefixPartial, s);
-  if (a.merge) {
-    prof_before(kKPrefixCombine, s);
-    hipLaunchKernelGGL(prefix_merge_kernel, dim3((unsigned)(N * Hkv)), dim3(256), 0, s, a);
-    prof_after(kKPrefixCombine, s);
-    VMK_CHECK_HIP(hipGetLastError());
-  } else if (!a.fuse) {
-    prof_before(kKPrefixCombine, s);
-    hipLaunchKernelGGL(prefix_combine_kernel, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
-    prof_after(kKPrefixCombine, s);
-    VMK_CHECK_HIP(hipGetLastError());
-  }
-  return 0;
+  a.prefix_pages = a.suffix_pages = nullptr;
+  a.ps = a.max_sp = a.num_pages = 0;
+  return prefix_launch<false>(a, q, out, slens, ragged != 0, N, Hq, Hkv, D, P, S, workspace, (hipStream_t)stream);
+}
+
+extern "C" size_t vmk_prefix_paged_workspace_size(int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t P,
+                                                  int64_t page_size, int64_t max_suffix_pages) {
+  if (page_size < 32 || page_size % 32 || page_size > (1 << 20) || P < 0 || P % page_size || max_suffix_pages < 0)
+    return 0;
+  return vmk_prefix_workspace_size(N, Hq, Hkv, D, P, page_size * max_suffix_pages, 1);
+}
+
+extern "C" int vmk_prefix_decode_paged(const void* q, const void* k_pages, const void* v_pages,
+                                       const void* prefix_pages, const void* suffix_pages, const void* slens,
+                                       void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t num_pages,
+                                       int64_t page_size, int64_t P, int64_t max_suffix_pages, void* workspace,
+                                       size_t ws_bytes, void* stream) {
+  VMK_CHECK(q && out && k_pages && v_pages && (P == 0 || prefix_pages) && (max_suffix_pages == 0 || suffix_pages),
+            "null pointer argument");
+  VMK_CHECK(N > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/request sizes");
+  VMK_CHECK(D == 128, "only head_dim 128 is supported");
+  VMK_CHECK(Hq / Hkv <= 32, "at most 32 query heads per KV head");
+  VMK_CHECK(page_size >= 32 && page_size % 32 == 0 && page_size <= (1 << 20), "page_size must be a multiple of 32");
+  VMK_CHECK(P >= 0 && P % page_size == 0, "P must be a whole number of pages");
+  VMK_CHECK(max_suffix_pages >= 0 && P + page_size * max_suffix_pages > 0, "no keys: P and max_suffix_pages are 0");
+  VMK_CHECK(num_pages > 0 && num_pages < (1 << 30) && num_pages * Hkv * page_size <= ((int64_t)1 << 34),
+            "num_pages out of range");
+  VMK_CHECK(P < (1 << 30) && page_size * max_suffix_pages < (1 << 30) && N * (Hq / Hkv) < (1 << 20),
+            "sizes out of range");
+  VMK_CHECK(aligned16(q) && aligned16(out) && aligned16(k_pages) && aligned16(v_pages),
+            "tensors must be 16-byte aligned");
+  const int64_t S = page_size * max_suffix_pages;
+  const size_t need = vmk_prefix_paged_workspace_size(N, Hq, Hkv, D, P, page_size, max_suffix_pages);
+  VMK_CHECK(workspace && ws_bytes >= need, "workspace too small (query vmk_prefix_paged_workspace_size)");
+  PrefixArgs a;
+  a.q = (const f16*)q; a.kp = (const f16*)k_pages; a.vp = (const f16*)v_pages; a.ks = a.vs = nullptr;
+  a.prefix_pages = (const int*)prefix_pages;
+  a.suffix_pages = (const int*)suffix_pages;
+  a.ps = (int)page_size; a.max_sp = (int)max_suffix_pages; a.num_pages = (int)num_pages;
+  return prefix_launch<true>(a, q, out, slens, slens != nullptr, N, Hq, Hkv, D, P, S, workspace, (hipStream_t)stream);
 }

@@ -1,0 +1,18 @@
+"""Shared-prefix decode over a paged cache on MI355X: the `kernel(q, k_pages, v_pages, prefix_pages, suffix_pages,
+slens)` module of the prefix_paged op contract (vmk.ops.prefix_paged).
+
+One call = libvmk's prefix launches with page-table tile addressing (vmk_prefix_decode_paged)."""
+import torch
+
+import vmk
+
+
+def kernel(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None):
+    if q.dtype == torch.bfloat16 or k_pages.dtype == torch.bfloat16 or v_pages.dtype == torch.bfloat16:
+        raise TypeError("prefix_paged kernel reads fp16 inputs; bf16 is not supported")
+    q, k_pages, v_pages = (x.to(torch.float16).contiguous() for x in (q, k_pages, v_pages))
+    prefix_pages = prefix_pages.to(device=q.device, dtype=torch.int32).contiguous()
+    suffix_pages = suffix_pages.to(device=q.device, dtype=torch.int32).contiguous()
+    if slens is not None:
+        slens = slens.to(device=q.device, dtype=torch.int32).contiguous()
+    return vmk.prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens)

@@ -1,8 +1,9 @@
-"""vmk: MI355X (gfx950) kernels for shared-prefix decode, speculative verification and DSA decode.
+"""vmk: MI355X (gfx950) kernels for shared-prefix decode (contiguous or paged cache), speculative verification,
+single-token decode and DSA decode.
 
 Host side of the C-ABI library libvmk.so (HIP kernels in ../csrc, declared in include/vmk.h).  Tensors are torch
 tensors on a ROCm device; every call launches on torch's current stream and returns without synchronising.
 """
 from .lib import VmkError, load  # noqa: F401
-from .api import (spec_verify, decode, prefix_decode, dsa_decode, dsa_indexer_select, dsa_sparse_mla,  # noqa: F401
-                  workspace, device_ok)
+from .api import (spec_verify, decode, prefix_decode, prefix_decode_paged, dsa_decode,  # noqa: F401
+                  dsa_indexer_select, dsa_sparse_mla, workspace, device_ok)

@@ -143,6 +143,42 @@ def prefix_decode(q, kp, vp, ks, vs, slens=None, out=None):
     return out
 
 
+def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None, out=None):
+    """Shared-prefix decode over a paged cache.  q (N, Hq, 128) fp16; k_pages/v_pages (num_pages, Hkv, page_size,
+    128) fp16 with page_size a multiple of 32; prefix_pages (P / page_size,) int32; suffix_pages (N, max_sp) int32;
+    slens (N,) int32 or None (full suffixes).  Page ids outside [0, num_pages) are absent pages (left out).
+    Returns out (N, Hq, 128) fp16."""
+    _need(q, "q", torch.float16, 3)
+    for t, n in ((k_pages, "k_pages"), (v_pages, "v_pages")):
+        _need(t, n, torch.float16, 4)
+    _need(prefix_pages, "prefix_pages", torch.int32, 1)
+    _need(suffix_pages, "suffix_pages", torch.int32, 2)
+    N, Hq, D = q.shape
+    num_pages, Hkv, ps = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
+    if tuple(k_pages.shape) != (num_pages, Hkv, ps, D) or tuple(v_pages.shape) != tuple(k_pages.shape):
+        raise ValueError("k_pages/v_pages shapes do not match")
+    if suffix_pages.shape[0] != N:
+        raise ValueError("suffix_pages must have N rows")
+    if slens is not None:
+        _need(slens, "slens", torch.int32, 1)
+        if slens.shape[0] != N:
+            raise ValueError("slens must have N entries")
+    P, max_sp = prefix_pages.shape[0] * ps, suffix_pages.shape[1]
+    device_ok(q.device)
+    if out is None:
+        out = torch.empty_like(q)
+    ws_n = lib.load().vmk_prefix_paged_workspace_size(N, Hq, Hkv, D, P, ps, max_sp)
+    if ws_n == 0:
+        raise lib.VmkError(f"unsupported paged prefix shape N={N} Hq={Hq} Hkv={Hkv} D={D} P={P} page_size={ps} "
+                           f"max_suffix_pages={max_sp}")
+    ws = workspace(ws_n, q.device)
+    lib.call("vmk_prefix_decode_paged", q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
+             prefix_pages.data_ptr() if P else 0, suffix_pages.data_ptr() if max_sp else 0,
+             0 if slens is None else slens.data_ptr(), out.data_ptr(), N, Hq, Hkv, D, num_pages, ps, P, max_sp,
+             ws.data_ptr(), ws.numel(), _stream(q))
+    return out
+
+
 DSA_H, DSA_DK, DSA_DC, DSA_HI, DSA_DI, DSA_TOPK = 128, 576, 512, 64, 128, 2048
 
 

@@ -26,12 +26,15 @@ _SIGS = {
     "vmk_decode": [_c_vp] * 5 + [_c_i64] * 5 + [_c_vp, _c_sz, _c_vp],
     "vmk_prefix_workspace_size": [_c_i64] * 7,
     "vmk_prefix_decode": [_c_vp] * 7 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
+    "vmk_prefix_paged_workspace_size": [_c_i64] * 7,
+    "vmk_prefix_decode_paged": [_c_vp] * 7 + [_c_i64] * 8 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_workspace_size": [_c_i64] * 2,
     "vmk_dsa_indexer_select": [_c_vp] * 6 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_sparse_mla": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_decode": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
 }
 _RET = {"vmk_last_error": ctypes.c_char_p, "vmk_spec_workspace_size": _c_sz, "vmk_prefix_workspace_size": _c_sz,
+        "vmk_prefix_paged_workspace_size": _c_sz,
         "vmk_dsa_workspace_size": _c_sz, "vmk_decode_workspace_size": _c_sz}
 
 
