@@ -48,7 +48,8 @@ def config_table():
             ("C3", "spec", *spec.CONFIGS["C3"]), ("C4", "spec", *spec.CONFIGS["C4"]),
             ("C5", "dsa", *dsa.CONFIGS["C5"]),
             ("D1", "decode", *decode.CONFIGS["D1"]), ("D2", "decode", *decode.CONFIGS["D2"]),
-            ("D3", "decode", *decode.CONFIGS["D3"]), ("P2", "prefix_paged", *prefix_paged.CONFIGS["P2"])]
+            ("D3", "decode", *decode.CONFIGS["D3"]), ("P2", "prefix_paged", *prefix_paged.CONFIGS["P2"]),
+            ("C2b", "prefix", *prefix.CONFIGS["C2b"])]
 
 
 class HipEvents:
@@ -148,7 +149,7 @@ def distinct_sets(opname, inp0, total_bytes):
     for _ in range(n - 1):
         s = dict(inp0)
         for k in big:
-            s[k] = torch.randn(inp0[k].shape, device="cuda", generator=g, dtype=torch.float32).half()
+            s[k] = torch.randn(inp0[k].shape, device="cuda", generator=g, dtype=torch.float32).to(inp0[k].dtype)
         sets.append(s)
     return sets
 
@@ -288,7 +289,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2")
+    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2,C2b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle timings")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="first run a plain streaming kernel that reads BYTES and writes BYTES (torch.bitwise_not "

@@ -98,12 +98,19 @@ def test_python_wrappers_validate_shapes_without_gpu():
         vmk.spec_verify(q.float(), q, q, q)
 
 
-def test_kernel_modules_reject_bf16():
+def test_bf16_reaches_the_bf16_entry_points_and_dsa_rejects_it():
+    """bf16 inputs pass through the kernel modules to the _bf16 entry points (here: rejected as CPU tensors, after the
+    dtype dispatch); float32 q is rejected; DSA stays fp16 only."""
     import torch
+    import vmk
+    import dsa_mi355x
     import spec_mi355x
     x = torch.zeros(1, 1, 32, 128, dtype=torch.bfloat16)
-    with pytest.raises(TypeError):
+    with pytest.raises(ValueError, match="ROCm device"):
         spec_mi355x.kernel(x, x, x, torch.ones(1, 1, dtype=torch.int32))
-    import decode_mi355x
     with pytest.raises(TypeError):
-        decode_mi355x.kernel(x[:, 0], x, x)
+        vmk.decode(x[:, 0].float(), x, x)
+    y = torch.zeros(1, 2100, 576, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        dsa_mi355x.kernel(y[:, :128], y, torch.zeros(1, 64, 128, dtype=torch.bfloat16),
+                          torch.zeros(1, 2100, 128, dtype=torch.bfloat16), torch.zeros(1, 64), None)

@@ -55,8 +55,9 @@ def test_spec_parity(shape, dist, seed):
     torch.cuda.synchronize()
     o = out.float().cpu().numpy().astype(np.float64)
     r = oracle.spec.ref64(**inp)
-    assert out.shape == tuple(r.shape) and out.dtype == torch.float16
-    assert same_pattern(o, r), (np.isnan(o).sum(), np.isnan(r).sum(), np.isinf(o).sum(), np.isinf(r).sum())
+    assert out.shape == tuple(r.shape) and out.dtype == inp["q"].dtype
+    kind = "bf16" if out.dtype == torch.bfloat16 else "fp16"
+    assert same_pattern(o, r, kind), (np.isnan(o).sum(), np.isnan(r).sum(), np.isinf(o).sum(), np.isinf(r).sum())
     em, ea = nerr(o, r)
     print(f"  err max {em:.3e} mean {ea:.3e}")
     assert em <= 1e-2

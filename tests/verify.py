@@ -187,7 +187,7 @@ def child_outputs(opname, kernel_path, out):
 
 
 # ------------------------------------------------------------------------------------------------ parent side
-from judge import nerr, pattern  # noqa: E402
+from judge import kind_of, nerr, pattern  # noqa: E402
 
 
 def to64(a):
@@ -247,7 +247,7 @@ def judge(opname, outpath):
         if layer in ("L2", "X"):
             pat_ok, emax, emean, s = True, 0.0, 0.0, None
             for j, (o, rr) in enumerate(zip(outs, r)):
-                half = "float32" not in m["dtypes"][j]
+                half = kind_of(m["dtypes"][j])
                 pn, pi = pattern(o, half)
                 rn, ri = pattern(rr, half)
                 pj = bool((pn == rn).all() and (pi == ri).all())
@@ -303,7 +303,8 @@ def l4_case(meta, arrs, i, shape, dist):
     for j in range(m["n_out"]):
         full, rows = arrs[f"{key}__full{j}"], arrs[f"{key}__rows{j}"]
         if full.shape != rows.shape or full.dtype != rows.dtype:
-            case.update(ok=False, error=f"output {j}: batch {full.shape} {full.dtype} vs rows {rows.shape} {rows.dtype}")
+            case.update(ok=False,
+                        error=f"output {j}: batch {full.shape} {full.dtype} vs rows {rows.shape} {rows.dtype}")
             return case
         fb = full.reshape(full.shape[0], -1).view(np.uint8)
         rb = rows.reshape(rows.shape[0], -1).view(np.uint8)

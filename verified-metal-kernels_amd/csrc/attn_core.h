@@ -51,10 +51,12 @@ __device__ __attribute__((aligned(16))) const f16 g_zero_tile[32 * 128] = {};
 // Q^T operand for 128 head-dims of one row (qrow must be a valid row); zeros when !valid, read from g_zero_row rather
 // than selected after the load, so nothing waits for these loads before the first MFMA that uses them (a select would
 // make the compiler wait for them right away, ahead of the first tile's DMA).
-__device__ __forceinline__ void load_qt(half8 (&qb)[8], const f16* qrow, int g, bool valid) {
+// V is the operand type (half8 or bf16x8); qrow points at the row's raw 16-bit elements.
+template <class V>
+__device__ __forceinline__ void load_qt(V (&qb)[8], const f16* qrow, int g, bool valid) {
   const f16* p = valid ? qrow : g_zero_row;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) qb[s] = as_h8(ldg16(p + 64 * g + 8 * s));
+  for (int s = 0; s < 8; ++s) qb[s] = as_v8<V>(ldg16(p + 64 * g + 8 * s));
 }
 
 // K operand: 128 bytes of the lane's key row (head-dims 64*g .. 64*g+63 of the 128-dim slice at krow).
@@ -99,10 +101,12 @@ __device__ __forceinline__ floatx16 qk_tile(const u32x4 (&kr)[8], const half8 (&
 // Online-softmax update of raw scores s (masked keys = -inf); p = exp2(scale * s - m) with m in the scaled (log2)
 // domain, so the scale costs one FMA per score.  Returns P^T operands.
 // The reference point m only moves when a tile's max exceeds it by more than 8 (a factor 256): p = exp2(.) then
-// stays <= 256, which fp16 P and the fp32 sums hold exactly as well as p <= 1, and the O rescale is skipped for the
-// whole wave unless some row moved.  Guard: while a row has seen only -inf, the subtrahend is 0 so exp2(-inf) = 0
-// and a NaN score still yields NaN.  scale must be positive (max commutes with it).
-__device__ __forceinline__ void softmax_update(RowState& st, floatx16& s, float scale, half8 (&pb)[2]) {
+// stays <= 256, which fp16 (or bf16) P and the fp32 sums hold as well as p <= 1, and the O rescale is skipped for
+// the whole wave unless some row moved.  Guard: while a row has seen only -inf, the subtrahend is 0 so exp2(-inf) = 0
+// and a NaN score still yields NaN.  scale must be positive (max commutes with it).  P is rounded to the operand type
+// V of the values it multiplies.
+template <class V>
+__device__ __forceinline__ void softmax_update(RowState& st, floatx16& s, float scale, V (&pb)[2]) {
   float tmax = s[0];
 #pragma unroll
   for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
@@ -124,8 +128,8 @@ __device__ __forceinline__ void softmax_update(RowState& st, floatx16& s, float 
   }
   st.l += lsum;
   st.m = mnew;
-  pb[0] = pack8(s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7]);
-  pb[1] = pack8(s[8], s[9], s[10], s[11], s[12], s[13], s[14], s[15]);
+  pb[0] = pack8v<V>(s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7]);
+  pb[1] = pack8v<V>(s[8], s[9], s[10], s[11], s[12], s[13], s[14], s[15]);
 }
 
 // O^T += V^T . P^T using the transposed V tile in LDS.
@@ -162,8 +166,6 @@ __device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >>
 #define VMK_GPTR(p) ((const void __attribute__((address_space(1)))*)(p))
 #define VMK_LPTR(p) ((void __attribute__((address_space(3)))*)(p))
 
-// Waits until at most n of this wave's vector-memory operations are outstanding (loads return in order).  An asm
-// statement with a memory clobber, so the compiler neither drops it nor moves LDS accesses across it.
 // Waits until at most n (0 <= n <= 63; larger counts wait for everything) of this wave's vector-memory operations
 // are outstanding (loads return in order).  An asm statement with a memory clobber, so the compiler neither drops it
 // nor moves LDS accesses across it.
@@ -276,8 +278,8 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
 // Read schedule: the 8 K operands and the first 4 transposed V halves are issued up front (12 <= 15 outstanding
 // LDS reads, the counter's limit), the other 12 V halves two after each of the first six QK MFMAs, so their latency
 // hides behind the QK chain and the softmax instead of being paid read by read.
-template <class Src>
-__device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)[8], const char* __restrict__ stage,
+template <class Src, class V>
+__device__ __forceinline__ void compute_tile_lds(RowState& st, const V (&qb)[8], const char* __restrict__ stage,
                                                  const TileLanes& tl, const Src& src, int key0, int lane) {
   const int g = lane >> 5;
   u32x4 kk[8];
@@ -292,7 +294,7 @@ __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)
       for (int rr = 0; rr < 2; ++rr) vv[dt][t][rr] = lds_read_tr16(stage + tl.v[2 * dt + rr] + 4096 * t);
   floatx16 s = floatx16{};
 #pragma unroll
-  for (int t = 0; t < 8; ++t) s = mfma32(as_h8(kk[t]), qb[t], s);
+  for (int t = 0; t < 8; ++t) s = mfma32(as_v8<V>(kk[t]), qb[t], s);
   __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);     // DS reads: K operands, V halves of d-tile 0
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
@@ -302,13 +304,13 @@ __device__ __forceinline__ void compute_tile_lds(RowState& st, const half8 (&qb)
   __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   __builtin_amdgcn_sched_barrier(0);
   src.mask(s, key0, g);
-  half8 pb[2];
+  V pb[2];
   softmax_update(st, s, src.scale, pb);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const half8 va = as_h8(u32x4{vv[dt][t][0][0], vv[dt][t][0][1], vv[dt][t][1][0], vv[dt][t][1][1]});
+      const V va = as_v8<V>(u32x4{vv[dt][t][0][0], vv[dt][t][0][1], vv[dt][t][1][0], vv[dt][t][1][1]});
       st.o[dt] = mfma32(va, pb[t], st.o[dt]);
     }
 }
@@ -360,8 +362,8 @@ __device__ __forceinline__ void ring_walk(char* ring, const Src& src, int kbeg, 
 // The key source `src` provides: ktile(key0) / vtile(key0) (the 32 contiguous K / V rows of the tile starting at
 // key0, a multiple of 32 from the range start; rows at or past kend are not read), kend, scale (log2-domain softmax
 // scale) and mask(s, key0, g) (masked scores of the raw S^T tile -> -inf).
-template <int NS, class Src>
-__device__ __forceinline__ void wave_walk(RowState& st, const half8 (&qb)[8], char* __restrict__ ring,
+template <int NS, class Src, class V>
+__device__ __forceinline__ void wave_walk(RowState& st, const V (&qb)[8], char* __restrict__ ring,
                                           const char* __restrict__ base, const TileLanes& tl, const Src& src,
                                           int kbeg, int t0, int ntiles, int tstep, int lane) {
   static_assert(NS >= 2 && NS <= 4, "1 to 3 tiles in flight");
@@ -433,7 +435,7 @@ constexpr int kAttnSmemBytes = 8 * kStageBytes;
 constexpr int kAttnSlotsEnd = 4 * kSlotBytes;
 static_assert(kAttnSlotsEnd <= kAttnSmemBytes, "merge slots must fit in the stage memory");
 
-template <int WR, int WK, int NSW = 2, class Src, class QRow>
+template <int WR, int WK, int NSW = 2, class V = half8, class Src, class QRow>
 __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow, int nrows, int kbeg, int ntiles,
                                           float* po, float* pml) {
   static_assert(WR * WK == 4 && WR * WK * NSW <= 8, "four waves, rings within the stage memory");
@@ -441,7 +443,7 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
   const int wr = wave % WR, wk = wave / WR;
   const int r = lane & 31, g = lane >> 5;
   const int row = wr * 32 + r;
-  half8 qb[8];
+  V qb[8];
   load_qt(qb, qrow(row < nrows ? row : 0), g, row < nrows);
   RowState st;
   row_state_init(st);
@@ -500,8 +502,8 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
 // part(i, ml, o) sets ml -> (m, l) and o -> the partial's O row of partial i (0 <= i < nparts).  The m/l of a batch
 // of NT partials are fetched in parallel and their weights shared through LDS, so that the O loads of the
 // accumulation loop are independent of each other and can all be in flight together.
-template <int NT, int PER, class Part>
-__device__ __forceinline__ void combine_row(int nparts, Part part, f16* out) {
+template <int NT, int PER, class Part, class E>
+__device__ __forceinline__ void combine_row(int nparts, Part part, E* out) {
   __shared__ float sw[NT], sl[NT], red[NT / 64];
   const int tid = threadIdx.x;
   float M = kNegInf;
@@ -548,7 +550,7 @@ __device__ __forceinline__ void combine_row(int nparts, Part part, f16* out) {
     }
   }
 #pragma unroll
-  for (int k = 0; k < PER; ++k) out[tid + k * NT] = (f16)(num[k] / den);
+  for (int k = 0; k < PER; ++k) out[tid + k * NT] = (E)(num[k] / den);
 }
 
 // ---- one workgroup of NW waves sharing a ring of kRowsStages stages: wave w owns rows [32w, 32w+32) and every wave
@@ -559,13 +561,13 @@ __device__ __forceinline__ void combine_row(int nparts, Part part, f16* out) {
 constexpr int kRowsStages = 8;
 constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
 
-template <int NW, class Src, class QRow>
+template <int NW, class V = half8, class Src, class QRow>
 __device__ __forceinline__ void attend_wg_rows(char* smem, const Src& src, QRow qrow, int nrows, int kbeg,
                                                int ntiles, float* po, float* pml) {
   static_assert(16 % NW == 0, "the 16 DMA instructions of a tile must split evenly over the waves");
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row = wave * 32 + (lane & 31);
-  half8 qb[8];
+  V qb[8];
   load_qt(qb, qrow(row < nrows ? row : 0), lane >> 5, row < nrows);
   RowState st;
   row_state_init(st);

@@ -8,6 +8,8 @@ namespace vmk {
 
 typedef _Float16 f16;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -26,6 +28,17 @@ constexpr float kNegInf = -__builtin_huge_valf();
 __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
+// The same with bf16 operands (same operand and result layout).
+__device__ __forceinline__ floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Element type of an 8-wide MFMA operand vector (half8 -> _Float16, bf16x8 -> __bf16): the attention core is written
+// once over the operand type V; keys, values and queries are moved as raw 16-bit bits and only interpreted here.
+template <class V> struct ElemOf;
+template <> struct ElemOf<half8> { typedef f16 type; };
+template <> struct ElemOf<bf16x8> { typedef bf16 type; };
+template <class V> using elem_t = typename ElemOf<V>::type;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -99,5 +112,12 @@ __device__ __forceinline__ half8 pack8(float a0, float a1, float a2, float a3, f
                                        float a7) {
   return half8{(f16)a0, (f16)a1, (f16)a2, (f16)a3, (f16)a4, (f16)a5, (f16)a6, (f16)a7};
 }
+// Eight floats rounded to the operand type V (round to nearest even).
+template <class V>
+__device__ __forceinline__ V pack8v(float a0, float a1, float a2, float a3, float a4, float a5, float a6, float a7) {
+  typedef elem_t<V> E;
+  return V{(E)a0, (E)a1, (E)a2, (E)a3, (E)a4, (E)a5, (E)a6, (E)a7};
+}
+template <class V> __device__ __forceinline__ V as_v8(u32x4 u) { return __builtin_bit_cast(V, u); }
 
 }  // namespace vmk

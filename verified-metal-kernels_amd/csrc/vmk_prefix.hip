@@ -126,6 +126,7 @@ static_assert(kFuseOff + (32 * 128 + 64) * 4 <= kAttnSmemBytes, "fused partial m
 // floats, lpml (m, l) pairs) with the prefix partials of those rows.  One wave per row, two head-dims per lane.
 // Lane s holds the (m, l) of prefix partial b0 + s; the O rows are fetched 16 partials at a time with independent
 // loads (one memory round trip per 16), weighted with the lane-broadcast weights.
+template <class E>
 __device__ void merge_prefix_rows(const PrefixArgs& a, const float* lpo, const float* lpml, int n, int h) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int np = a.P > 0 ? a.nsplit_p : 0;
@@ -171,9 +172,9 @@ __device__ void merge_prefix_rows(const PrefixArgs& a, const float* lpo, const f
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
     den += ws * ls;
-    f16* out = a.out + ((size_t)n * a.Hq + h * a.G + gg) * 128 + 2 * lane;
-    out[0] = (f16)(num.x / den);
-    out[1] = (f16)(num.y / den);
+    E* out = reinterpret_cast<E*>(a.out) + ((size_t)n * a.Hq + h * a.G + gg) * 128 + 2 * lane;
+    out[0] = (E)(num.x / den);
+    out[1] = (E)(num.y / den);
   }
 }
 
@@ -198,6 +199,7 @@ __device__ __forceinline__ void prefetch_prefix_row(const PrefixArgs& a, PrefixR
 }
 
 // Final output of row gg of request n, KV head h, from the suffix partial in LDS and the prefetched prefix row.
+template <class E>
 __device__ __forceinline__ void merge_prefetched_row(const PrefixArgs& a, const PrefixRow& pr, const float* lpo,
                                                      const float* lpml, int n, int h, int gg, int lane) {
   const int np = a.nsplit_p;
@@ -217,20 +219,20 @@ __device__ __forceinline__ void merge_prefetched_row(const PrefixArgs& a, const 
     num.y += wj * pr.v[j].y;
   }
   den = wave_sum(den) + ws * ls;
-  f16* out = a.out + ((size_t)n * a.Hq + h * a.G + gg) * 128 + 2 * lane;
-  out[0] = (f16)(num.x / den);
-  out[1] = (f16)(num.y / den);
+  E* out = reinterpret_cast<E*>(a.out) + ((size_t)n * a.Hq + h * a.G + gg) * 128 + 2 * lane;
+  out[0] = (E)(num.x / den);
+  out[1] = (E)(num.y / den);
 }
 
 // The walk and merge of a suffix item over key source src (keys [kbeg, src.kend)).
-template <class Src>
+template <class V, class Src>
 __device__ __forceinline__ void suffix_walk(const PrefixArgs& a, char* smem, const Src& src, int n, int h, int nh,
                                             int split, int kbeg) {
   const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
   auto qrow = [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; };
   if (!a.fuse) {
     const size_t pi = (size_t)nh * a.nsplit_s + split;
-    attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, a.po_s + pi * 32 * 128, a.pml_s + pi * 32 * 2);
+    attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, a.po_s + pi * 32 * 128, a.pml_s + pi * 32 * 2);
     return;
   }
   // Whole suffix: keep the partial in LDS (past the merge slots) and merge it with the prefix partials here.
@@ -240,19 +242,19 @@ __device__ __forceinline__ void suffix_walk(const PrefixArgs& a, char* smem, con
   if (a.G <= 4 && a.nsplit_p <= kPrefetchSplits) {          // wave w finishes row w
     PrefixRow pr;
     if (wave < a.G) prefetch_prefix_row(a, pr, n, h, wave, lane);
-    attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
+    attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
     __syncthreads();
-    if (wave < a.G) merge_prefetched_row(a, pr, lpo, lpml, n, h, wave, lane);
+    if (wave < a.G) merge_prefetched_row<elem_t<V>>(a, pr, lpo, lpml, n, h, wave, lane);
   } else {
-    attend_wg<1, 4>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
+    attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
     __syncthreads();
-    merge_prefix_rows(a, lpo, lpml, n, h);
+    merge_prefix_rows<elem_t<V>>(a, lpo, lpml, n, h);
   }
 }
 
 // Suffix item `sitem` (request, KV head, suffix chunk) of 4 waves.  Fused: the prefix partials are finished (an
 // earlier launch) and the item writes its rows' outputs; otherwise it writes its partial to po_s / pml_s.
-template <bool kPaged>
+template <bool kPaged, class V>
 __device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int sitem) {
   const int split = sitem % a.nsplit_s;
   int nh = sitem / a.nsplit_s, sn = 0;
@@ -267,7 +269,7 @@ __device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int
   if (kbeg >= sn && !a.fuse && !a.merge) return;        // whole workgroup: nothing of this suffix is here
   const int kend = min(sn, kbeg + a.chunk_s);
   if constexpr (kPaged) {
-    suffix_walk(a, smem, paged_src(a, a.suffix_pages + (size_t)n * a.max_sp, a.max_sp, h, kbeg, kend), n, h, nh,
+    suffix_walk<V>(a, smem, paged_src(a, a.suffix_pages + (size_t)n * a.max_sp, a.max_sp, h, kbeg, kend), n, h, nh,
                 split, kbeg);
   } else {
     RangeSrc src;
@@ -276,16 +278,16 @@ __device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int
     src.kbase = a.ks + off;
     src.vbase = a.vs + off;
     src.kend = kend;
-    suffix_walk(a, smem, src, n, h, nh, split, kbeg);
+    suffix_walk<V>(a, smem, src, n, h, nh, split, kbeg);
   }
 }
 
 
 // Suffix items, after the prefix launch has written the prefix partials.
-template <bool kPaged>
+template <bool kPaged, class V>
 __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
-  suffix_item<kPaged>(a, smem, blockIdx.x);
+  suffix_item<kPaged, V>(a, smem, blockIdx.x);
 }
 
 // Counting sort of the requests by decreasing suffix length (256 buckets), run by one workgroup of the prefix
@@ -323,7 +325,7 @@ __device__ void build_suffix_order(const PrefixArgs& a, uint32_t* cnt /* LDS, 25
 
 // Prefix item (KV head h, row block rb, prefix chunk): NW waves own 32 of the N*G rows each and share one LDS ring,
 // so the prefix chunk is streamed from HBM once per 32*NW rows.
-template <int NW, bool kPaged>
+template <int NW, bool kPaged, class V>
 __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem, int item) {
   const int split = item % a.nsplit_p;
   const int rb = (item / a.nsplit_p) % a.nrb_p;
@@ -334,7 +336,7 @@ __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem
   const int row0 = rb * NW * 32;
   const size_t rows_wg = 32 * NW;
   auto walk = [&](const auto& src) {
-    attend_wg_rows<NW>(smem, src,
+    attend_wg_rows<NW, V>(smem, src,
                        [&](int r) {
                          const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
                          return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
@@ -355,27 +357,28 @@ __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem
   }
 }
 
-template <int NW, bool kPaged>
+template <int NW, bool kPaged, class V>
 __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kRowsSmemBytes];
   if (blockIdx.x == 0 && a.order) build_suffix_order<64 * NW>(a, reinterpret_cast<uint32_t*>(smem));
-  prefix_rows_item<NW, kPaged>(a, smem, blockIdx.x);
+  prefix_rows_item<NW, kPaged, V>(a, smem, blockIdx.x);
 }
 
 // Both item kinds in one grid when a KV head has at most 128 rows: prefix items (4 waves sharing a ring) first, then
 // suffix items writing their partials.  No item depends on another.
 constexpr int kMixedSmemBytes = kRowsSmemBytes > kAttnSmemBytes ? kRowsSmemBytes : kAttnSmemBytes;
-template <bool kPaged>
+template <bool kPaged, class V>
 __global__ __launch_bounds__(256) void prefix_mixed_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kMixedSmemBytes];
   if ((int)blockIdx.x < a.n_prefix_items)
-    prefix_rows_item<4, kPaged>(a, smem, blockIdx.x);
+    prefix_rows_item<4, kPaged, V>(a, smem, blockIdx.x);
   else
-    suffix_item<kPaged>(a, smem, blockIdx.x - a.n_prefix_items);
+    suffix_item<kPaged, V>(a, smem, blockIdx.x - a.n_prefix_items);
 }
 
 // After a mixed launch with whole suffixes: the final merge of the G rows of (request, KV head), by the functions a
 // fused suffix item uses and from the same partial values, so the output bits do not depend on which path ran.
+template <class E>
 __global__ __launch_bounds__(256) void prefix_merge_kernel(PrefixArgs a) {
   const int nh = blockIdx.x, n = nh / a.Hkv, h = nh % a.Hkv;
   const float* lpo = a.po_s + (size_t)nh * 32 * 128;        // one suffix split per (request, KV head)
@@ -385,15 +388,16 @@ __global__ __launch_bounds__(256) void prefix_merge_kernel(PrefixArgs a) {
     if (wave < a.G) {
       PrefixRow pr;
       prefetch_prefix_row(a, pr, n, h, wave, lane);
-      merge_prefetched_row(a, pr, lpo, lpml, n, h, wave, lane);
+      merge_prefetched_row<E>(a, pr, lpo, lpml, n, h, wave, lane);
     }
   } else {
-    merge_prefix_rows(a, lpo, lpml, n, h);
+    merge_prefix_rows<E>(a, lpo, lpml, n, h);
   }
 }
 
 // One workgroup (128 threads = head-dims) per output row (n, hq): merge the prefix splits of KV head h and the
 // suffix chunks of request n.
+template <class E>
 __global__ __launch_bounds__(128) void prefix_combine_kernel(PrefixArgs a) {
   const int rowg = blockIdx.x;                 // n * Hq + hq
   const int n = rowg / a.Hq, hq = rowg % a.Hq;
@@ -418,7 +422,7 @@ __global__ __launch_bounds__(128) void prefix_combine_kernel(PrefixArgs a) {
                           o = a.po_s + base * 128;
                         }
                       },
-                      a.out + (size_t)rowg * 128);
+                      reinterpret_cast<E*>(a.out) + (size_t)rowg * 128);
 }
 
 struct PrefixPlan {
@@ -463,7 +467,7 @@ static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int
 }
 
 // Plan, workspace carve-up and launches of one prefix call (contiguous or paged; a's K/V pointers are set).
-template <bool kPaged>
+template <bool kPaged, class V>
 static int prefix_launch(PrefixArgs& a, const void* q, void* out, const void* slens, bool ragged, int64_t N,
                          int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int64_t S, void* workspace, hipStream_t s) {
   PrefixPlan p = prefix_plan(N, Hq, Hkv, P, S);
@@ -487,28 +491,28 @@ static int prefix_launch(PrefixArgs& a, const void* q, void* out, const void* sl
   a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
   prof_before(kKPrefixPartial, s);
   if (mixed) {
-    hipLaunchKernelGGL(prefix_mixed_kernel<kPaged>, dim3((unsigned)p.n_items), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((prefix_mixed_kernel<kPaged, V>), dim3((unsigned)p.n_items), dim3(256), 0, s, a);
     VMK_CHECK_HIP(hipGetLastError());
   } else {
     if (p.n_prefix_items > 0) {
-      hipLaunchKernelGGL((prefix_rows_kernel<8, kPaged>), dim3((unsigned)p.n_prefix_items), dim3(512), 0, s, a);
+      hipLaunchKernelGGL((prefix_rows_kernel<8, kPaged, V>), dim3((unsigned)p.n_prefix_items), dim3(512), 0, s, a);
       VMK_CHECK_HIP(hipGetLastError());
     }
     if (p.n_items > p.n_prefix_items) {
-      hipLaunchKernelGGL(prefix_partial_kernel<kPaged>, dim3((unsigned)(p.n_items - p.n_prefix_items)), dim3(256),
-                         0, s, a);
+      hipLaunchKernelGGL((prefix_partial_kernel<kPaged, V>), dim3((unsigned)(p.n_items - p.n_prefix_items)),
+                         dim3(256), 0, s, a);
       VMK_CHECK_HIP(hipGetLastError());
     }
   }
   prof_after(kKPrefixPartial, s);
   if (a.merge) {
     prof_before(kKPrefixCombine, s);
-    hipLaunchKernelGGL(prefix_merge_kernel, dim3((unsigned)(N * Hkv)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(prefix_merge_kernel<elem_t<V>>, dim3((unsigned)(N * Hkv)), dim3(256), 0, s, a);
     prof_after(kKPrefixCombine, s);
     VMK_CHECK_HIP(hipGetLastError());
   } else if (!a.fuse) {
     prof_before(kKPrefixCombine, s);
-    hipLaunchKernelGGL(prefix_combine_kernel, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
+    hipLaunchKernelGGL(prefix_combine_kernel<elem_t<V>>, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
     prof_after(kKPrefixCombine, s);
     VMK_CHECK_HIP(hipGetLastError());
   }
@@ -527,10 +531,10 @@ extern "C" size_t vmk_prefix_workspace_size(int64_t N, int64_t Hq, int64_t Hkv, 
   return kWsHead + (p.po_p + p.pml_p + p.po_s + p.pml_s + p.order) * sizeof(float) + 5 * 256;
 }
 
-extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, const void* ks, const void* vs,
-                                 const void* slens, void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D,
-                                 int64_t P, int64_t S, int64_t ragged, void* workspace, size_t ws_bytes,
-                                 void* stream) {
+template <class V>
+static int prefix_decode(const void* q, const void* kp, const void* vp, const void* ks, const void* vs,
+                         const void* slens, void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t P,
+                         int64_t S, int64_t ragged, void* workspace, size_t ws_bytes, void* stream) {
   VMK_CHECK(q && out && (P == 0 || (kp && vp)) && (S == 0 || (ks && vs)), "null pointer argument");
   VMK_CHECK(N > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/request sizes");
   VMK_CHECK(D == 128, "only head_dim 128 is supported");
@@ -547,7 +551,23 @@ extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, 
   a.q = (const f16*)q; a.kp = (const f16*)kp; a.vp = (const f16*)vp; a.ks = (const f16*)ks; a.vs = (const f16*)vs;
   a.prefix_pages = a.suffix_pages = nullptr;
   a.ps = a.max_sp = a.num_pages = 0;
-  return prefix_launch<false>(a, q, out, slens, ragged != 0, N, Hq, Hkv, D, P, S, workspace, (hipStream_t)stream);
+  return prefix_launch<false, V>(a, q, out, slens, ragged != 0, N, Hq, Hkv, D, P, S, workspace, (hipStream_t)stream);
+}
+
+extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, const void* ks, const void* vs,
+                                 const void* slens, void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D,
+                                 int64_t P, int64_t S, int64_t ragged, void* workspace, size_t ws_bytes,
+                                 void* stream) {
+  return prefix_decode<half8>(q, kp, vp, ks, vs, slens, out, N, Hq, Hkv, D, P, S, ragged, workspace, ws_bytes,
+                              stream);
+}
+
+extern "C" int vmk_prefix_decode_bf16(const void* q, const void* kp, const void* vp, const void* ks, const void* vs,
+                                      const void* slens, void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t P, int64_t S, int64_t ragged, void* workspace, size_t ws_bytes,
+                                      void* stream) {
+  return prefix_decode<bf16x8>(q, kp, vp, ks, vs, slens, out, N, Hq, Hkv, D, P, S, ragged, workspace, ws_bytes,
+                               stream);
 }
 
 extern "C" size_t vmk_prefix_paged_workspace_size(int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t P,
@@ -557,11 +577,11 @@ extern "C" size_t vmk_prefix_paged_workspace_size(int64_t N, int64_t Hq, int64_t
   return vmk_prefix_workspace_size(N, Hq, Hkv, D, P, page_size * max_suffix_pages, 1);
 }
 
-extern "C" int vmk_prefix_decode_paged(const void* q, const void* k_pages, const void* v_pages,
-                                       const void* prefix_pages, const void* suffix_pages, const void* slens,
-                                       void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t num_pages,
-                                       int64_t page_size, int64_t P, int64_t max_suffix_pages, void* workspace,
-                                       size_t ws_bytes, void* stream) {
+template <class V>
+static int prefix_decode_paged(const void* q, const void* k_pages, const void* v_pages, const void* prefix_pages,
+                               const void* suffix_pages, const void* slens, void* out, int64_t N, int64_t Hq,
+                               int64_t Hkv, int64_t D, int64_t num_pages, int64_t page_size, int64_t P,
+                               int64_t max_suffix_pages, void* workspace, size_t ws_bytes, void* stream) {
   VMK_CHECK(q && out && k_pages && v_pages && (P == 0 || prefix_pages) && (max_suffix_pages == 0 || suffix_pages),
             "null pointer argument");
   VMK_CHECK(N > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/request sizes");
@@ -584,5 +604,24 @@ extern "C" int vmk_prefix_decode_paged(const void* q, const void* k_pages, const
   a.prefix_pages = (const int*)prefix_pages;
   a.suffix_pages = (const int*)suffix_pages;
   a.ps = (int)page_size; a.max_sp = (int)max_suffix_pages; a.num_pages = (int)num_pages;
-  return prefix_launch<true>(a, q, out, slens, slens != nullptr, N, Hq, Hkv, D, P, S, workspace, (hipStream_t)stream);
+  return prefix_launch<true, V>(a, q, out, slens, slens != nullptr, N, Hq, Hkv, D, P, S, workspace,
+                                (hipStream_t)stream);
+}
+
+extern "C" int vmk_prefix_decode_paged(const void* q, const void* k_pages, const void* v_pages,
+                                       const void* prefix_pages, const void* suffix_pages, const void* slens,
+                                       void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t num_pages,
+                                       int64_t page_size, int64_t P, int64_t max_suffix_pages, void* workspace,
+                                       size_t ws_bytes, void* stream) {
+  return prefix_decode_paged<half8>(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, out, N, Hq, Hkv, D,
+                                    num_pages, page_size, P, max_suffix_pages, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_prefix_decode_paged_bf16(const void* q, const void* k_pages, const void* v_pages,
+                                            const void* prefix_pages, const void* suffix_pages, const void* slens,
+                                            void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D,
+                                            int64_t num_pages, int64_t page_size, int64_t P, int64_t max_suffix_pages,
+                                            void* workspace, size_t ws_bytes, void* stream) {
+  return prefix_decode_paged<bf16x8>(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, out, N, Hq, Hkv, D,
+                                     num_pages, page_size, P, max_suffix_pages, workspace, ws_bytes, stream);
 }

@@ -78,6 +78,8 @@ __device__ __forceinline__ int batch_len(const SpecArgs& a, int b) {
 }
 
 // One workgroup = WR x WK waves: WR row blocks of 32 rows, WK waves interleaving the key tiles of one split.
+// V is the operand type: half8 (fp16 inputs) or bf16x8 (bf16 inputs).
+template <class V>
 __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
   const int item = blockIdx.x;
@@ -109,14 +111,14 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
   float* po = a.part_o + (size_t)item * rows_wg * 128;
   float* pml = a.part_ml + (size_t)item * rows_wg * 2;
   if (a.WK == 4)
-    attend_wg<1, 4>(smem, src, qrow, R - row0, kbeg, ntiles, po, pml);
+    attend_wg<1, 4, 2, V>(smem, src, qrow, R - row0, kbeg, ntiles, po, pml);
   else
-    attend_wg<2, 2>(smem, src, qrow, R - row0, kbeg, ntiles, po, pml);
+    attend_wg<2, 2, 2, V>(smem, src, qrow, R - row0, kbeg, ntiles, po, pml);
 }
 
 // Row-split variant for kd*G > 64 rows: NW waves own 32 rows each and share one LDS ring, so every K/V tile of the
 // split is streamed from HBM once per workgroup of 32*NW rows.
-template <int NW>
+template <int NW, class V>
 __global__ __launch_bounds__(64 * NW) void spec_partial_rows_kernel(SpecArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kRowsSmemBytes];
   const int item = blockIdx.x;
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(64 * NW) void spec_partial_rows_kernel(SpecArgs a) 
   src.scale = a.sl2;
   const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
   const size_t rows_wg = 32 * NW;
-  attend_wg_rows<NW>(smem, src,
+  attend_wg_rows<NW, V>(smem, src,
                      [&](int r) {
                        const int qr = row0 + r, i = qr / a.G, gg = qr % a.G;
                        return a.q + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128;
@@ -149,7 +151,9 @@ __global__ __launch_bounds__(64 * NW) void spec_partial_rows_kernel(SpecArgs a) 
                      a.part_ml + (size_t)item * rows_wg * 2);
 }
 
-// LSE merge of the nsplit partials of every query row; one workgroup (128 threads = head-dims) per row.
+// LSE merge of the nsplit partials of every query row; one workgroup (128 threads = head-dims) per row.  E is the
+// output element type.
+template <class E>
 __global__ __launch_bounds__(128) void spec_combine_kernel(SpecArgs a) {
   const int R = a.kd * a.G;
   const int rowg = blockIdx.x;                 // grp * R + row
@@ -165,7 +169,7 @@ __global__ __launch_bounds__(128) void spec_combine_kernel(SpecArgs a) {
                         ml = a.part_ml + base * 2;
                         o = a.part_o + base * 128;
                       },
-                      a.out + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128);
+                      reinterpret_cast<E*>(a.out) + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128);
 }
 
 struct SpecPlan {
@@ -208,7 +212,9 @@ extern "C" size_t vmk_spec_workspace_size(int64_t B, int64_t kd, int64_t Hq, int
   return kWsHead + (p.po_floats + p.pml_floats) * sizeof(float) + 256;
 }
 
-// Partial launch (key split or row split by the plan) and LSE-combine launch of one spec/decode call.
+// Partial launch (key split or row split by the plan) and LSE-combine launch of one spec/decode call; V is the
+// operand type of the inputs (half8: fp16, bf16x8: bf16).
+template <class V>
 static int spec_launch(SpecArgs& a, const SpecPlan& p, void* workspace, hipStream_t s) {
   a.part_o = (float*)align_up((char*)workspace + kWsHead, 256);
   a.part_ml = a.part_o + p.po_floats;
@@ -217,23 +223,25 @@ static int spec_launch(SpecArgs& a, const SpecPlan& p, void* workspace, hipStrea
   const unsigned items = (unsigned)(a.B * a.Hkv * p.nrb * p.nsplit);
   prof_before(kKSpecPartial, s);
   if (!p.rows_mode)
-    hipLaunchKernelGGL(spec_partial_kernel, dim3(items), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(spec_partial_kernel<V>, dim3(items), dim3(256), 0, s, a);
   else if (p.WR == 4)
-    hipLaunchKernelGGL(spec_partial_rows_kernel<4>, dim3(items), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((spec_partial_rows_kernel<4, V>), dim3(items), dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL(spec_partial_rows_kernel<8>, dim3(items), dim3(512), 0, s, a);
+    hipLaunchKernelGGL((spec_partial_rows_kernel<8, V>), dim3(items), dim3(512), 0, s, a);
   prof_after(kKSpecPartial, s);
   VMK_CHECK_HIP(hipGetLastError());
   prof_before(kKSpecCombine, s);
-  hipLaunchKernelGGL(spec_combine_kernel, dim3((unsigned)(a.B * a.Hkv * a.kd * a.G)), dim3(128), 0, s, a);
+  hipLaunchKernelGGL(spec_combine_kernel<elem_t<V>>, dim3((unsigned)(a.B * a.Hkv * a.kd * a.G)), dim3(128), 0, s,
+                     a);
   prof_after(kKSpecCombine, s);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
 }
 
-extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out,
-                               int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W,
-                               void* workspace, size_t ws_bytes, void* stream) {
+template <class V>
+static int spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
+                       int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, void* workspace,
+                       size_t ws_bytes, void* stream) {
   VMK_CHECK(q && k && v && mask_words && out, "null pointer argument");
   VMK_CHECK(B > 0 && kd > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/batch sizes");
   VMK_CHECK(D == 128, "only head_dim 128 is supported");
@@ -250,7 +258,7 @@ extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, cons
   a.lens = nullptr;
   a.out = (f16*)out;
   a.B = (int)B; a.kd = (int)kd; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = (int)W;
-  return spec_launch(a, p, workspace, (hipStream_t)stream);
+  return spec_launch<V>(a, p, workspace, (hipStream_t)stream);
 }
 
 // Plain single-token decode: the verify path with one query row per request and no mask (the row's own position is
@@ -259,9 +267,9 @@ extern "C" size_t vmk_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, 
   return vmk_spec_workspace_size(B, 1, Hq, Hkv, D, L);
 }
 
-extern "C" int vmk_decode(const void* q, const void* k, const void* v, const void* lens, void* out, int64_t B,
-                          int64_t Hq, int64_t Hkv, int64_t D, int64_t L, void* workspace, size_t ws_bytes,
-                          void* stream) {
+template <class V>
+static int decode(const void* q, const void* k, const void* v, const void* lens, void* out, int64_t B, int64_t Hq,
+                  int64_t Hkv, int64_t D, int64_t L, void* workspace, size_t ws_bytes, void* stream) {
   VMK_CHECK(q && k && v && out, "null pointer argument");
   VMK_CHECK(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/batch sizes");
   VMK_CHECK(D == 128, "only head_dim 128 is supported");
@@ -276,5 +284,29 @@ extern "C" int vmk_decode(const void* q, const void* k, const void* v, const voi
   a.lens = (const int*)lens;
   a.out = (f16*)out;
   a.B = (int)B; a.kd = 1; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = 1;
-  return spec_launch(a, p, workspace, (hipStream_t)stream);
+  return spec_launch<V>(a, p, workspace, (hipStream_t)stream);
+}
+
+extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out,
+                               int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W,
+                               void* workspace, size_t ws_bytes, void* stream) {
+  return spec_verify<half8>(q, k, v, mask_words, out, B, kd, Hq, Hkv, D, L, W, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_spec_verify_bf16(const void* q, const void* k, const void* v, const void* mask_words, void* out,
+                                    int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W,
+                                    void* workspace, size_t ws_bytes, void* stream) {
+  return spec_verify<bf16x8>(q, k, v, mask_words, out, B, kd, Hq, Hkv, D, L, W, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_decode(const void* q, const void* k, const void* v, const void* lens, void* out, int64_t B,
+                          int64_t Hq, int64_t Hkv, int64_t D, int64_t L, void* workspace, size_t ws_bytes,
+                          void* stream) {
+  return decode<half8>(q, k, v, lens, out, B, Hq, Hkv, D, L, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_decode_bf16(const void* q, const void* k, const void* v, const void* lens, void* out, int64_t B,
+                               int64_t Hq, int64_t Hkv, int64_t D, int64_t L, void* workspace, size_t ws_bytes,
+                               void* stream) {
+  return decode<bf16x8>(q, k, v, lens, out, B, Hq, Hkv, D, L, workspace, ws_bytes, stream);
 }

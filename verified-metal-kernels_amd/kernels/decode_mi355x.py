@@ -8,9 +8,8 @@ import vmk
 
 
 def kernel(q, k, v, lens=None):
-    if q.dtype == torch.bfloat16 or k.dtype == torch.bfloat16 or v.dtype == torch.bfloat16:
-        raise TypeError("decode kernel reads fp16 inputs; bf16 is not supported")
-    q, k, v = (x.to(torch.float16).contiguous() for x in (q, k, v))
+    dt = torch.bfloat16 if torch.bfloat16 in (q.dtype, k.dtype, v.dtype) else torch.float16
+    q, k, v = (x.to(dt).contiguous() for x in (q, k, v))
     if lens is not None:
         lens = lens.to(device=q.device, dtype=torch.int32).contiguous()
     return vmk.decode(q, k, v, lens)

@@ -9,9 +9,8 @@ import vmk
 
 
 def kernel(q, kp, vp, ks, vs, slens=None):
-    if any(x.dtype == torch.bfloat16 for x in (q, kp, vp, ks, vs)):
-        raise TypeError("prefix kernel reads fp16 inputs; bf16 is not supported")
-    q, kp, vp, ks, vs = (x.to(torch.float16).contiguous() for x in (q, kp, vp, ks, vs))
+    dt = torch.bfloat16 if any(x.dtype == torch.bfloat16 for x in (q, kp, vp, ks, vs)) else torch.float16
+    q, kp, vp, ks, vs = (x.to(dt).contiguous() for x in (q, kp, vp, ks, vs))
     if slens is not None:
         slens = slens.to(device=q.device, dtype=torch.int32).contiguous()
     return vmk.prefix_decode(q, kp, vp, ks, vs, slens)

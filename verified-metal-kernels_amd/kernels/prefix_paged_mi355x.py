@@ -8,9 +8,8 @@ import vmk
 
 
 def kernel(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None):
-    if q.dtype == torch.bfloat16 or k_pages.dtype == torch.bfloat16 or v_pages.dtype == torch.bfloat16:
-        raise TypeError("prefix_paged kernel reads fp16 inputs; bf16 is not supported")
-    q, k_pages, v_pages = (x.to(torch.float16).contiguous() for x in (q, k_pages, v_pages))
+    dt = torch.bfloat16 if torch.bfloat16 in (q.dtype, k_pages.dtype, v_pages.dtype) else torch.float16
+    q, k_pages, v_pages = (x.to(dt).contiguous() for x in (q, k_pages, v_pages))
     prefix_pages = prefix_pages.to(device=q.device, dtype=torch.int32).contiguous()
     suffix_pages = suffix_pages.to(device=q.device, dtype=torch.int32).contiguous()
     if slens is not None:

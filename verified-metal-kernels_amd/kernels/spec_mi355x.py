@@ -9,9 +9,8 @@ import vmk
 
 
 def kernel(q, k, v, bits):
-    if q.dtype == torch.bfloat16 or k.dtype == torch.bfloat16 or v.dtype == torch.bfloat16:
-        raise TypeError("spec kernel reads fp16 inputs; bf16 is not supported")
-    q, k, v = (x.to(torch.float16).contiguous() for x in (q, k, v))
+    dt = torch.bfloat16 if torch.bfloat16 in (q.dtype, k.dtype, v.dtype) else torch.float16
+    q, k, v = (x.to(dt).contiguous() for x in (q, k, v))
     B, kd = q.shape[0], q.shape[1]
     words = bits.to(device=q.device, dtype=torch.int32)
     if words.dim() == 2:

@@ -60,12 +60,25 @@ def _need(t, name, dtype, ndim):
         raise ValueError(f"{name} must be contiguous")
 
 
+_SUFFIX = {torch.float16: "", torch.bfloat16: "_bf16"}
+
+
+def _elem(q):
+    """Entry-point suffix for q's dtype: fp16 or bf16 (q, keys and values share it; the output gets it too)."""
+    if not isinstance(q, torch.Tensor):
+        raise TypeError("q must be a torch.Tensor")
+    if q.dtype not in _SUFFIX:
+        raise TypeError(f"q must be float16 or bfloat16, got {q.dtype}")
+    return q.dtype, _SUFFIX[q.dtype]
+
+
 def spec_verify(q, k, v, words, out=None):
-    """q (B, kd, Hq, 128) fp16, k/v (B, Hkv, L, 128) fp16, words (B, kd, W) int32 with W = ceil(kd/32).
-    Returns out (B, kd, Hq, 128) fp16."""
-    _need(q, "q", torch.float16, 4)
-    _need(k, "k", torch.float16, 4)
-    _need(v, "v", torch.float16, 4)
+    """q (B, kd, Hq, 128), k/v (B, Hkv, L, 128), all fp16 or all bf16; words (B, kd, W) int32 with W = ceil(kd/32).
+    Returns out (B, kd, Hq, 128) of q's dtype."""
+    dt, sfx = _elem(q)
+    _need(q, "q", dt, 4)
+    _need(k, "k", dt, 4)
+    _need(v, "v", dt, 4)
     _need(words, "bits", torch.int32, 3)
     B, kd, Hq, D = q.shape
     Hkv, L = k.shape[1], k.shape[2]
@@ -80,17 +93,18 @@ def spec_verify(q, k, v, words, out=None):
     if ws_n == 0:
         raise lib.VmkError(f"unsupported spec shape B={B} kd={kd} Hq={Hq} Hkv={Hkv} D={D} L={L}")
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_spec_verify", q.data_ptr(), k.data_ptr(), v.data_ptr(), words.data_ptr(), out.data_ptr(),
+    lib.call("vmk_spec_verify" + sfx, q.data_ptr(), k.data_ptr(), v.data_ptr(), words.data_ptr(), out.data_ptr(),
              B, kd, Hq, Hkv, D, L, words.shape[2], ws.data_ptr(), ws.numel(), _stream(q))
     return out
 
 
 def decode(q, k, v, lens=None, out=None):
-    """Single-token decode: q (B, Hq, 128) fp16, k/v (B, Hkv, L, 128) fp16, lens (B,) int32 or None (all L in use).
-    Returns out (B, Hq, 128) fp16."""
-    _need(q, "q", torch.float16, 3)
-    _need(k, "k", torch.float16, 4)
-    _need(v, "v", torch.float16, 4)
+    """Single-token decode: q (B, Hq, 128), k/v (B, Hkv, L, 128), all fp16 or all bf16; lens (B,) int32 or None (all
+    L in use).  Returns out (B, Hq, 128) of q's dtype."""
+    dt, sfx = _elem(q)
+    _need(q, "q", dt, 3)
+    _need(k, "k", dt, 4)
+    _need(v, "v", dt, 4)
     B, Hq, D = q.shape
     Hkv, L = k.shape[1], k.shape[2]
     if tuple(k.shape) != (B, Hkv, L, D) or tuple(v.shape) != tuple(k.shape):
@@ -106,19 +120,20 @@ def decode(q, k, v, lens=None, out=None):
     if ws_n == 0:
         raise lib.VmkError(f"unsupported decode shape B={B} Hq={Hq} Hkv={Hkv} D={D} L={L}")
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), 0 if lens is None else lens.data_ptr(),
+    lib.call("vmk_decode" + sfx, q.data_ptr(), k.data_ptr(), v.data_ptr(), 0 if lens is None else lens.data_ptr(),
              out.data_ptr(), B, Hq, Hkv, D, L, ws.data_ptr(), ws.numel(), _stream(q))
     return out
 
 
 def prefix_decode(q, kp, vp, ks, vs, slens=None, out=None):
-    """q (N, Hq, 128), kp/vp (Hkv, P, 128), ks/vs (N, Hkv, S, 128) fp16, slens (N,) int32 or None.
-    Returns out (N, Hq, 128) fp16."""
-    _need(q, "q", torch.float16, 3)
+    """q (N, Hq, 128), kp/vp (Hkv, P, 128), ks/vs (N, Hkv, S, 128), all fp16 or all bf16; slens (N,) int32 or
+    None.  Returns out (N, Hq, 128) of q's dtype."""
+    dt, sfx = _elem(q)
+    _need(q, "q", dt, 3)
     for t, n in ((kp, "kp"), (vp, "vp")):
-        _need(t, n, torch.float16, 3)
+        _need(t, n, dt, 3)
     for t, n in ((ks, "ks"), (vs, "vs")):
-        _need(t, n, torch.float16, 4)
+        _need(t, n, dt, 4)
     N, Hq, D = q.shape
     Hkv, P = kp.shape[0], kp.shape[1]
     S = ks.shape[2]
@@ -137,20 +152,21 @@ def prefix_decode(q, kp, vp, ks, vs, slens=None, out=None):
     if ws_n == 0:
         raise lib.VmkError(f"unsupported prefix shape N={N} Hq={Hq} Hkv={Hkv} D={D} P={P} S={S}")
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_prefix_decode", q.data_ptr(), kp.data_ptr(), vp.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+    lib.call("vmk_prefix_decode" + sfx, q.data_ptr(), kp.data_ptr(), vp.data_ptr(), ks.data_ptr(), vs.data_ptr(),
              0 if slens is None else slens.data_ptr(), out.data_ptr(), N, Hq, Hkv, D, P, S,
              0 if slens is None else 1, ws.data_ptr(), ws.numel(), _stream(q))
     return out
 
 
 def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None, out=None):
-    """Shared-prefix decode over a paged cache.  q (N, Hq, 128) fp16; k_pages/v_pages (num_pages, Hkv, page_size,
-    128) fp16 with page_size a multiple of 32; prefix_pages (P / page_size,) int32; suffix_pages (N, max_sp) int32;
-    slens (N,) int32 or None (full suffixes).  Page ids outside [0, num_pages) are absent pages (left out).
-    Returns out (N, Hq, 128) fp16."""
-    _need(q, "q", torch.float16, 3)
+    """Shared-prefix decode over a paged cache.  q (N, Hq, 128); k_pages/v_pages (num_pages, Hkv, page_size, 128)
+    with page_size a multiple of 32, all fp16 or all bf16; prefix_pages (P / page_size,) int32; suffix_pages
+    (N, max_sp) int32; slens (N,) int32 or None (full suffixes).  Page ids outside [0, num_pages) are absent pages
+    (left out).  Returns out (N, Hq, 128) of q's dtype."""
+    dt, sfx = _elem(q)
+    _need(q, "q", dt, 3)
     for t, n in ((k_pages, "k_pages"), (v_pages, "v_pages")):
-        _need(t, n, torch.float16, 4)
+        _need(t, n, dt, 4)
     _need(prefix_pages, "prefix_pages", torch.int32, 1)
     _need(suffix_pages, "suffix_pages", torch.int32, 2)
     N, Hq, D = q.shape
@@ -172,7 +188,7 @@ def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=N
         raise lib.VmkError(f"unsupported paged prefix shape N={N} Hq={Hq} Hkv={Hkv} D={D} P={P} page_size={ps} "
                            f"max_suffix_pages={max_sp}")
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_prefix_decode_paged", q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
+    lib.call("vmk_prefix_decode_paged" + sfx, q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
              prefix_pages.data_ptr() if P else 0, suffix_pages.data_ptr() if max_sp else 0,
              0 if slens is None else slens.data_ptr(), out.data_ptr(), N, Hq, Hkv, D, num_pages, ps, P, max_sp,
              ws.data_ptr(), ws.numel(), _stream(q))

@@ -10,6 +10,8 @@ import math
 import numpy as np
 import torch
 
+from .elem import cast16
+
 NAME = "decode"
 HQ, HKV, D = 32, 8, 128                                       # test-backend-ops.patch:79 (32 q heads, 8 kv, D 128)
 L1_SHAPE = dict(B=2, L=4096)
@@ -25,7 +27,7 @@ L3_CASES = [(dict(B=2, L=8192), "randn"), (dict(B=1, L=32768), "randn"), (dict(B
             (dict(B=2, L=8192), "needle"), (dict(B=8, L=2048), "randn")]
 # This build's ragged extension: lens ~ U[L_min, L].
 EXTRA = [(dict(B=6, L=5000, L_min=1), "randn"), (dict(B=8, L=2048, L_min=1), "needle"),
-         (dict(B=3, L=40000, L_min=30000), "randn")]
+         (dict(B=3, L=40000, L_min=30000), "randn"), (dict(B=4, L=5000, L_min=1, dtype="bf16"), "randn")]
 # Row invariance (L4): every request decoded alone (B = 1) must give the same bits as in the batch.
 L4_CASES = [(dict(B=8, L=8192), "randn"), (dict(B=6, L=5000, L_min=1), "randn"), (dict(B=4, L=16384), "needle")]
 
@@ -62,7 +64,7 @@ def make_inputs(shape, seed=0, dist="randn", device="cpu"):
         q, k, v = q * 1e-4, k * 1e-4, v * 1e-6
     elif dist != "randn":
         raise ValueError(f"unknown dist {dist!r}")
-    f = lambda a: torch.from_numpy(a.astype(np.float16)).to(device)
+    f = lambda a: cast16(a, shape.get("dtype", "fp16"), device)
     return dict(q=f(q), k=f(k), v=f(v), lens=None if lens is None else torch.from_numpy(lens).to(device))
 
 

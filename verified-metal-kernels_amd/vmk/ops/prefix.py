@@ -13,13 +13,16 @@ import math
 import numpy as np
 import torch
 
+from .elem import cast16
+
 NAME = "prefix"
 HQ, HKV, D = 32, 8, 128                                  # ops/prefix.py:10
 L1_SHAPE = dict(N=4, P=2048, S=256)                      # ops/prefix.py:11
 BENCH_SHAPES = [dict(N=8, P=8192, S=512), dict(N=16, P=16384, S=1024), dict(N=32, P=4096, S=256)]  # :12
 # Headline configurations of this build (BASELINE C1, C2).  S_min turns on ragged suffixes U[S_min, S].
 CONFIGS = {"C1": (dict(N=8, P=2048, S=256), "randn"),
-           "C2": (dict(N=64, P=16384, S=2048, S_min=128), "outlier")}
+           "C2": (dict(N=64, P=16384, S=2048, S_min=128), "outlier"),
+           "C2b": (dict(N=64, P=16384, S=2048, S_min=128, dtype="bf16"), "outlier")}   # C2 with bf16 inputs
 
 
 def make_inputs(shape, seed=0, dist="randn", with_ref_layouts=False, device="cpu"):
@@ -62,7 +65,7 @@ def make_inputs(shape, seed=0, dist="randn", with_ref_layouts=False, device="cpu
         ks[rng.random(ks.shape) < 0.01] *= 20.0
     elif dist != "randn":
         raise ValueError(f"unknown dist {dist!r}")
-    f = lambda a: torch.from_numpy(a.astype(np.float16)).to(device)
+    f = lambda a: cast16(a, shape.get("dtype", "fp16"), device)
     out = dict(q=f(q), kp=f(kp), vp=f(vp), ks=f(ks), vs=f(vs),
                slens=None if slens is None else torch.from_numpy(slens).to(device))
     if with_ref_layouts:
@@ -136,7 +139,8 @@ L3_CASES = [(dict(N=8, P=1024, S=128), "randn"), (dict(N=8, P=32768, S=1024), "r
             (dict(N=4, P=8192, S=512), "needle_suffix")]                                # ops/prefix.py:152-153
 # Cases this build adds for its own extensions (ragged suffixes, K outliers); judged like L2.
 EXTRA = [(dict(N=5, P=700, S=300, S_min=1), "randn"), (dict(N=16, P=2048, S=512, S_min=128), "outlier"),
-         (dict(N=3, P=1, S=64, S_min=1), "randn")]
+         (dict(N=3, P=1, S=64, S_min=1), "randn"), (dict(N=8, P=2048, S=256, S_min=1, dtype="bf16"), "randn"),
+         (dict(N=64, P=4096, S=512, S_min=128, dtype="bf16"), "outlier")]
 # Row invariance (L4, ONE-PAGER.md:13-14): every request computed alone (N = 1) must give the same bits as in the
 # batch.  The C2 and C1 shapes, a prefix of many chunks with suffixes split over two chunks, and odd sizes.
 L4_CASES = [(dict(N=64, P=16384, S=2048, S_min=128), "outlier"), (dict(N=8, P=2048, S=256), "randn"),

@@ -4,7 +4,7 @@ The reference leaves the paged variant of its shared-prefix kernel out of the pa
 measurement is cases/README.md:13).  This op is ops/prefix.py's attention with the keys and values held in a page
 pool, in the layout FlashInfer calls HND:
     q: (N, Hq, D)                                   one decode token per request
-    k_pages, v_pages: (num_pages, Hkv, ps, D) fp16  the page pool, ps (page size) a multiple of 32
+    k_pages, v_pages: (num_pages, Hkv, ps, D)       the page pool (fp16 or bf16), ps (page size) a multiple of 32
     prefix_pages: (P / ps,) int32                   the shared prefix's pages, in order
     suffix_pages: (N, max_sp) int32                 each request's suffix pages, in order
     slens: (N,) int32 or None                       suffix rows in use (None: all max_sp * ps)
@@ -32,7 +32,8 @@ FUZZ = [(dict(N=1, P=32, S=1, ps=32), "randn"), (dict(N=3, P=1024, S=77, ps=64),
 L3_CASES = [(dict(N=8, P=1024, S=128, ps=64), "randn"), (dict(N=8, P=32768, S=1024, ps=128), "randn"),
             (dict(N=16, P=4096, S=512, S_min=1, ps=32), "randn"), (dict(N=4, P=8192, S=512, ps=64), "needle_suffix"),
             (dict(N=64, P=16384, S=2048, S_min=128, ps=64), "outlier")]
-EXTRA = [(dict(N=33, P=640, S=40, ps=32, absent=2), "randn"), (dict(N=20, P=40960, S=3000, S_min=1, ps=256), "randn")]
+EXTRA = [(dict(N=33, P=640, S=40, ps=32, absent=2), "randn"), (dict(N=20, P=40960, S=3000, S_min=1, ps=256), "randn"),
+         (dict(N=6, P=1024, S=300, ps=64, dtype="bf16"), "randn")]
 L4_CASES = [(dict(N=64, P=16384, S=2048, S_min=128, ps=64), "outlier"), (dict(N=8, P=2048, S=256, ps=32), "randn"),
             (dict(N=12, P=3072, S=2500, S_min=1, ps=128, absent=2), "randn")]
 
@@ -52,7 +53,7 @@ def make_inputs(shape, seed=0, dist="randn", device="cpu"):
         raise ValueError(f"P={P} is not a whole number of pages of {ps}")
     base = {k: v for k, v in shape.items() if k not in ("ps", "absent")}
     c = prefix.make_inputs(base, seed=seed, dist=dist)
-    kp, vp, ks, vs = (c[k].numpy() for k in ("kp", "vp", "ks", "vs"))
+    kp, vp, ks, vs = (c[k] for k in ("kp", "vp", "ks", "vs"))          # CPU tensors of the op's dtype
     slens = None if c["slens"] is None else c["slens"].numpy()
     Hkv, d = kp.shape[0], kp.shape[2]
     npp, nsp = P // ps, -(-S // ps)
@@ -62,20 +63,20 @@ def make_inputs(shape, seed=0, dist="randn", device="cpu"):
     num_pages = used + used // 8 + 1
     rng = np.random.default_rng([seed, 1])
     ids = rng.permutation(num_pages).astype(np.int32)
-    kpool = np.full((num_pages, Hkv, ps, d), np.nan, np.float16)
-    vpool = np.full((num_pages, Hkv, ps, d), np.nan, np.float16)
+    kpool = torch.full((num_pages, Hkv, ps, d), float("nan"), dtype=kp.dtype)
+    vpool = torch.full((num_pages, Hkv, ps, d), float("nan"), dtype=kp.dtype)
     pp = ids[:npp].copy()
     for i in range(npp):
-        kpool[pp[i]] = kp[:, i * ps:(i + 1) * ps]
-        vpool[pp[i]] = vp[:, i * ps:(i + 1) * ps]
+        kpool[int(pp[i])] = kp[:, i * ps:(i + 1) * ps]
+        vpool[int(pp[i])] = vp[:, i * ps:(i + 1) * ps]
     sp = ids[npp:used].reshape(N, nsp).copy()
     for n in range(N):
         for j in range(nsp):
-            rows = min(ps, S - j * ps)
-            kpool[sp[n, j], :, :rows] = ks[n, :, j * ps:j * ps + rows]
-            vpool[sp[n, j], :, :rows] = vs[n, :, j * ps:j * ps + rows]
-            kpool[sp[n, j], :, rows:] = 0
-            vpool[sp[n, j], :, rows:] = 0
+            rows, page = min(ps, S - j * ps), int(sp[n, j])
+            kpool[page, :, :rows] = ks[n, :, j * ps:j * ps + rows]
+            vpool[page, :, :rows] = vs[n, :, j * ps:j * ps + rows]
+            kpool[page, :, rows:] = 0
+            vpool[page, :, rows:] = 0
         sn = S if slens is None else int(slens[n])
         sp[n, -(-sn // ps):] = -1                          # entries past the rows in use
     na = shape.get("absent", 0)
@@ -88,8 +89,8 @@ def make_inputs(shape, seed=0, dist="randn", device="cpu"):
             if live.size:
                 sp[n, int(rng.choice(live))] = -1
     t = lambda a: torch.from_numpy(a).to(device)
-    return dict(q=c["q"].to(device), k_pages=t(kpool), v_pages=t(vpool), prefix_pages=t(pp), suffix_pages=t(sp),
-                slens=None if slens is None else t(slens))
+    return dict(q=c["q"].to(device), k_pages=kpool.to(device), v_pages=vpool.to(device), prefix_pages=t(pp),
+                suffix_pages=t(sp), slens=None if slens is None else t(slens))
 
 
 def gather(k_pages, v_pages, prefix_pages, suffix_pages, slens=None):

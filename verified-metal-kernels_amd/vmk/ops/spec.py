@@ -11,6 +11,8 @@ import math
 import numpy as np
 import torch
 
+from .elem import cast16
+
 NAME = "spec"
 HQ, HKV, D = 32, 8, 128                                                   # ops/spec.py:8
 L1_SHAPE = dict(B=2, L=4096, k=8)                                         # ops/spec.py:9
@@ -105,7 +107,7 @@ def make_inputs(shape, seed=0, dist="randn", device="cpu"):
         q, k, v = q * 1e-4, k * 1e-4, v * 1e-6
     elif dist not in ("randn", "chain", "tree_bd"):
         raise ValueError(f"unknown dist {dist!r}")
-    f = lambda a: torch.from_numpy(a.astype(np.float16)).to(device)
+    f = lambda a: cast16(a, shape.get("dtype", "fp16"), device)
     return dict(q=f(q), k=f(k), v=f(v), bits=torch.from_numpy(words_to_int32(words, kd)).to(device))
 
 
@@ -157,7 +159,8 @@ L3_CASES = [(dict(B=1, L=1024, k=8), "randn"), (dict(B=1, L=32768, k=8), "randn"
             (dict(B=2, L=8192, k=8), "large"), (dict(B=2, L=8192, k=8), "needle_boundary")]  # ops/spec.py:158-159
 # Cases this build adds for kd > 32 (multi-word masks) and the bounded tree; judged like L2.
 EXTRA = [(dict(B=2, L=4096, k=64), "tree_bd"), (dict(B=1, L=70, k=64), "needle_masked"),
-         (dict(B=1, L=5000, k=33), "randn"), (dict(B=2, L=3000, k=64), "chain")]
+         (dict(B=1, L=5000, k=33), "randn"), (dict(B=2, L=3000, k=64), "chain"),
+         (dict(B=2, L=4096, k=8, dtype="bf16"), "chain"), (dict(B=1, L=3000, k=64, dtype="bf16"), "tree_bd")]
 # Row invariance (L4): every batch entry verified alone (B = 1) must give the same bits as in the batch.
 L4_CASES = [(dict(B=4, L=32768, k=8), "chain"), (dict(B=2, L=65536, k=64), "tree_bd"),
             (dict(B=3, L=5000, k=5), "randn"), (dict(B=5, L=777, k=33), "randn")]
