@@ -1,18 +1,21 @@
-"""Benchmark of the three attention ops on one MI355X, in the driver's contract.
+"""Benchmark of the attention ops on one MI355X, in the driver's contract.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs C1,C2,...] [--no-cpu]
 
 Prints human-readable progress on stderr and ONE JSON line on stdout.  A "step" is one call of the op on one batch
 of the headline configuration (BASELINE configs[1] = C2, shared-prefix decode at scale); `value` is its achieved
 HBM throughput (algorithmic bytes / time per call, inputs resident in HBM), `ops` holds the same figures for every
-configuration C1..C5.  Method (a counterpart of the reference's bench.py:44-140 timing):
+configuration (C1..C5, and this build's D1-D3 decode, P2 paged prefix, C2b bf16).  Method (a counterpart of the
+reference's bench.py:44-140 timing):
   * the kernel's output on the timed inputs is checked against the PyTorch standard op first
     (allclose atol=rtol=1e-2, bench.py:180-192 of the reference), and the inputs are checked for modification;
   * every call reads a different input set, rotating over enough distinct sets (>= 1 GiB in total) that the
     256 MB Infinity Cache cannot serve a repeat;
-  * W untimed warm-up calls, then K calls between two HIP events (synchronised before and after);
-  * the dominant kernel of each op is bracketed by its own pair of HIP events on its launch stream inside the same
-    timed loop (libvmk's vmk_profile_next hook), which gives the roofline figure.
+  * W untimed warm-up calls, then the per-call time: the K calls captured once in a HIP graph and replayed between
+    two HIP events (synchronised before and after), after 3 replays checked bit for bit against an eager call;
+    `eager` gives the same K calls launched one by one from Python, which adds the host's per-call overhead;
+  * the dominant kernel of each op is bracketed by its own pair of HIP events on its launch stream inside the eager
+    loop (libvmk's vmk_profile_next hook), which gives the roofline figure.
 The CPU baseline is the float64 NumPy oracle (oracle/) on the host, on a bounded sample of the same workload.
 """
 import argparse
@@ -249,19 +252,21 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
         call_op(opname, sets[i % len(sets)])
     e1.record()
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / steps
+    eager_us = e0.elapsed_time(e1) * 1e3 / steps
     dom_us = sum(hev.elapsed_ms(i) for i in range(steps)) * 1e3 / steps
     hev.close()
+    us = graph_us_per_call(opname, sets, steps)
     gbs = total_bytes / us / 1e3
     dom_gbs = dom_bytes / dom_us / 1e3
     row = dict(op=opname, shape=shape, dist=dist, us_per_call=round(us, 2), gbs=round(gbs, 1),
                pct_peak=round(100 * gbs / PEAK_HBM_GBS, 2), algorithmic_bytes=int(total_bytes),
                tflops=round(flops / us / 1e6, 2), mfma_pct=round(100 * flops / us / 1e6 / PEAK_FP16_TFLOPS, 2),
+               eager=dict(us_per_call=round(eager_us, 2), gbs=round(total_bytes / eager_us / 1e3, 1)),
                dominant=dict(kernel=DOMINANT[opname], us=round(dom_us, 2), bytes=int(dom_bytes),
                              gbs=round(dom_gbs, 1), frac=round(dom_gbs / PEAK_HBM_GBS, 4)),
                output_check="ok", distinct_input_sets=len(sets))
-    log(f"[{name}] {us:9.2f} us/call  {gbs:7.1f} GB/s ({row['pct_peak']:.1f}% of 8 TB/s)   "
-        f"dominant {DOMINANT[opname]} {dom_us:.2f} us = {dom_gbs:.0f} GB/s")
+    log(f"[{name}] {us:9.2f} us/call  {gbs:7.1f} GB/s ({row['pct_peak']:.1f}% of 8 TB/s)  [HIP graph of {steps} calls; "
+        f"eager loop {eager_us:.2f} us/call]   dominant {DOMINANT[opname]} {dom_us:.2f} us = {dom_gbs:.0f} GB/s")
     if do_cpu:
         row["cpu_baseline"] = cpu_baseline(opname, shape, dist, host, total_bytes)
         log(f"[{name}] CPU float64 oracle: {row['cpu_baseline']['us_per_call']:.0f} us/call "
@@ -269,6 +274,42 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     del sets, inp0, host
     torch.cuda.empty_cache()
     return row
+
+
+def graph_us_per_call(opname, sets, steps):
+    """µs per call of the K calls captured once in a HIP graph (torch.cuda.CUDAGraph over the calls' launches on the
+    capture stream, rotating over the same input sets) and replayed once between two events, synchronised before and
+    after: the GPU time of K steps without the Python and launch overhead of an eager loop, which dominates ops of a
+    few µs.  Before timing, the output of the last captured call after each of 3 replays (with eager work and
+    synchronisation in between) must equal an eager call on the same inputs bit for bit."""
+    import torch
+    n = steps
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(3):
+            call_op(opname, sets[i % len(sets)])
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [call_op(opname, sets[i % len(sets)]) for i in range(n)]
+    last = outs[-1]
+    ref = call_op(opname, sets[(n - 1) % len(sets)]).clone()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(last.view(torch.int16), ref.view(torch.int16)):
+            raise SystemExit(f"{opname}: a graph replay differs from the eager call")
+        call_op(opname, sets[0])                          # eager work between replays
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g, outs
+    return e0.elapsed_time(e1) * 1e3 / n
 
 
 def measured_traffic(name, dom):
@@ -326,7 +367,9 @@ def main():
         ms_per_step=round(head["us_per_call"] / 1e3, 5), higher_is_better=True, scaling="weak", vs_baseline=None,
         dtype="fp16 (fp32 accumulate)", data="synthetic (seeded N(0,1) inputs of the BASELINE configuration)",
         config=dict(workload=f"{head_name}: {head['op']} {head['shape']} dist={head['dist']}",
-                    us_per_call=head["us_per_call"], pct_peak=head["pct_peak"]),
+                    us_per_call=head["us_per_call"], pct_peak=head["pct_peak"],
+                    timing=f"{a.steps} calls replayed from one HIP graph; eager loop {head['eager']['us_per_call']} "
+                           f"us/call"),
         roofline=dict(bound="hbm", achieved=dom["gbs"], peak=PEAK_HBM_GBS, unit="GB/s", frac=dom["frac"],
                       kernel=dom["kernel"], kernel_us=dom["us"], traffic=measured_traffic(head_name, dom)),
         cpu_baseline={k: v for k, v in head.get("cpu_baseline", {}).items()} or None,

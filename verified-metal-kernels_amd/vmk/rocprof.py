@@ -13,11 +13,46 @@ import sqlite3
 import sys
 from collections import defaultdict
 
-KERNEL_PREFIX = "vmk::"
+KERNEL_PREFIX = "vmk"          # matches "vmk::name" and the mangled "_ZN3vmk..." that rocprofv3 leaves for some
+                               # template kernels (those with vector-type arguments)
+
+_MANGLED_ARGS = [("Dv8_DF16_", "half8"), ("Dv8_DF16b", "bf16x8"), ("DF16_", "_Float16"), ("DF16b", "__bf16"),
+                 ("Lb0E", "false"), ("Lb1E", "true")]
+
+
+def _demangle_vmk(name):
+    """'_ZN3vmk18prefix_rows_kernelILi8ELb1EDv8_DF16_EEvNS_10PrefixArgsE' -> 'prefix_rows_kernel<8, true, half8>'
+    (only the argument forms libvmk's kernels use; anything else is returned unchanged)."""
+    rest = name[len("_ZN3vmk"):]
+    digits = ""
+    while rest and rest[0].isdigit():
+        digits, rest = digits + rest[0], rest[1:]
+    if not digits:
+        return name
+    base, rest = rest[:int(digits)], rest[int(digits):]
+    if not rest.startswith("I"):
+        return base
+    rest, args = rest[1:], []
+    while rest and not rest.startswith("E"):
+        if rest.startswith("Li"):
+            end = rest.index("E")
+            args.append(rest[2:end])
+            rest = rest[end + 1:]
+            continue
+        for code, text in _MANGLED_ARGS:
+            if rest.startswith(code):
+                args.append(text)
+                rest = rest[len(code):]
+                break
+        else:
+            return name
+    return f"{base}<{', '.join(args)}>"
 
 
 def _short(name):
-    return name.split("(")[0].replace("void ", "").replace(KERNEL_PREFIX, "")
+    if name.startswith("_ZN3vmk"):
+        return _demangle_vmk(name)
+    return name.split("(")[0].replace("void ", "").replace("vmk::", "")
 
 
 def kernels(path, like=KERNEL_PREFIX):
