@@ -101,7 +101,7 @@ int vmk_prefix_decode_paged(const void* q, const void* k_pages, const void* v_pa
  * The reference kernels read fp16 only (README.md:140: on bf16 inputs they produce invalid values).  These entry points
  * take bf16 q, keys and values (and write a bf16 output) with the same arguments, workspace sizes, plans and
  * semantics as their fp16 counterparts above: the MFMAs run in bf16 with fp32 accumulation, and P is rounded to bf16
- * before the P.V product.  DSA decode stays fp16 only. */
+ * before the P.V product.  DSA takes bf16 q, kv, iq and ik (w stays fp32; its scores are fp32 either way). */
 int vmk_spec_verify_bf16(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
                          int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, void* workspace,
                          size_t ws_bytes, void* stream);
@@ -114,6 +114,13 @@ int vmk_prefix_decode_paged_bf16(const void* q, const void* k_pages, const void*
                                  const void* suffix_pages, const void* slens, void* out, int64_t N, int64_t Hq,
                                  int64_t Hkv, int64_t D, int64_t num_pages, int64_t page_size, int64_t P,
                                  int64_t max_suffix_pages, void* workspace, size_t ws_bytes, void* stream);
+int vmk_dsa_indexer_select_bf16(const void* iq, const void* ik, const void* w, const void* lens, void* idx, void* cnt,
+                                int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream);
+int vmk_dsa_sparse_mla_bf16(const void* q, const void* kv, const void* idx, const void* cnt, void* out, int64_t B,
+                            int64_t L, void* workspace, size_t ws_bytes, void* stream);
+int vmk_dsa_decode_bf16(const void* q, const void* kv, const void* iq, const void* ik, const void* w, const void* lens,
+                        void* out, void* idx, void* cnt, int64_t B, int64_t L, void* workspace, size_t ws_bytes,
+                        void* stream);
 
 /* ---------------------------------------------------------------------------------------------- DSA decode
  * Replaces kernel(q, kv, iq, ik, w, lens) of kernels/dsa_opus55_v7.py:946-977 (op contract ops/dsa.py:1-9, 53-83).

@@ -98,9 +98,9 @@ def test_python_wrappers_validate_shapes_without_gpu():
         vmk.spec_verify(q.float(), q, q, q)
 
 
-def test_bf16_reaches_the_bf16_entry_points_and_dsa_rejects_it():
+def test_bf16_reaches_the_bf16_entry_points():
     """bf16 inputs pass through the kernel modules to the _bf16 entry points (here: rejected as CPU tensors, after the
-    dtype dispatch); float32 q is rejected; DSA stays fp16 only."""
+    dtype dispatch, DSA included); float32 q is rejected."""
     import torch
     import vmk
     import dsa_mi355x
@@ -111,6 +111,6 @@ def test_bf16_reaches_the_bf16_entry_points_and_dsa_rejects_it():
     with pytest.raises(TypeError):
         vmk.decode(x[:, 0].float(), x, x)
     y = torch.zeros(1, 2100, 576, dtype=torch.bfloat16)
-    with pytest.raises(TypeError):
-        dsa_mi355x.kernel(y[:, :128], y, torch.zeros(1, 64, 128, dtype=torch.bfloat16),
-                          torch.zeros(1, 2100, 128, dtype=torch.bfloat16), torch.zeros(1, 64), None)
+    iq, ik = torch.zeros(1, 64, 128, dtype=torch.bfloat16), torch.zeros(1, 2100, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ROCm device"):
+        dsa_mi355x.kernel(y[:, :128], y, iq, ik, torch.zeros(1, 64), None)

@@ -133,6 +133,7 @@ struct IkSrc {
 // score = sum_h w[h] * max(S[h], 0) in fp32, and histograms of fkey(score) >> 19 (fine) and >> 24 (coarse) per
 // request.  Each of the 8 waves streams its 4 tiles through a private 2-stage ring of direct-to-LDS loads; the B
 // operand (ik^T) is read from the stage with the attention core's K-operand offsets.
+template <class V>
 __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) {
   __shared__ __attribute__((aligned(16))) char ring[kIdxWaves * kIdxStages * kIdxStageBytes];
   __shared__ uint32_t hist2[kBins / 2];                     // two 16-bit bin counts per word (<= 1024 per bin)
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
   const int r = lane & 31, g = lane >> 5;
   // Issue order: iq and w loads, then the ring's first tiles, so that the first wait for tile 0 covers both and
   // their latencies overlap; the histogram is cleared meanwhile behind a barrier that waits for LDS only.
-  half8 qa[2][8];
+  V qa[2][8];
   float wv[2][16];
   const f16* iqb = a.iq + (size_t)b * kHI * kDI;
 #pragma unroll
@@ -177,8 +178,8 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
     floatx16 s0 = floatx16{}, s1 = floatx16{};
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      s0 = mfma32(qa[0][t], as_h8(kk[t]), s0);
-      s1 = mfma32(qa[1][t], as_h8(kk[t]), s1);
+      s0 = mfma32(qa[0][t], as_v8<V>(kk[t]), s0);
+      s1 = mfma32(qa[1][t], as_v8<V>(kk[t]), s1);
     }
     float part = 0.f;
 #pragma unroll
@@ -451,12 +452,13 @@ __device__ __forceinline__ void dsa_issue_rows(char* __restrict__ stage, const f
 }
 
 // S^T of the tile in stage over all 576 QK dims (36 MFMAs; the same order in every wave).
-__device__ __forceinline__ floatx16 dsa_qk(const char* __restrict__ stage, const half8 (&qb)[36], int r, int g) {
+template <class V>
+__device__ __forceinline__ floatx16 dsa_qk(const char* __restrict__ stage, const V (&qb)[36], int r, int g) {
   floatx16 s = floatx16{};
 #pragma unroll
   for (int c = 0; c < 36; ++c) {
     const u32x4 k = *reinterpret_cast<const u32x4*>(stage + r * kLatStride + (2 * c + g) * 16);
-    s = mfma32(as_h8(k), qb[c], s);
+    s = mfma32(as_v8<V>(k), qb[c], s);
   }
   return s;
 }
@@ -465,7 +467,8 @@ __device__ __forceinline__ floatx16 dsa_qk(const char* __restrict__ stage, const
 // key 16tt + 8rr + 4g + ((l & 15) >> 2) at value dim 128w + 32dt + 16((l >> 4) & 1) + 4(l & 3); the transposed read
 // gives lane l the dim 128w + 32dt + (l & 31) of the four keys 16tt + 8rr + 4g + e, e = 0..3, the keys of P^T's
 // elements 4rr..4rr+3.
-__device__ __forceinline__ void dsa_pv(RowState& st, const char* __restrict__ stage, const half8 (&pb)[2], int lane,
+template <class V>
+__device__ __forceinline__ void dsa_pv(RowState& st, const char* __restrict__ stage, const V (&pb)[2], int lane,
                                        int w) {
   const int g = lane >> 5, e = (lane & 15) >> 2, hc = (lane >> 4) & 1, a4 = lane & 3;
 #pragma unroll
@@ -479,7 +482,7 @@ __device__ __forceinline__ void dsa_pv(RowState& st, const char* __restrict__ st
         const int col = 128 * w + 32 * dt + 16 * hc + 4 * a4;         // halfs
         part[rr] = lds_read_tr16(stage + row * kLatStride + (col >> 3) * 16 + (col & 7) * 2);
       }
-      const half8 va = as_h8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});
+      const V va = as_v8<V>(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});
       st.o[dt] = mfma32(va, pb[tt], st.o[dt]);
     }
 }
@@ -502,7 +505,8 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // One tile: S^T over all QK dims, masked online softmax, PV over this wave's value dims.
-__device__ __forceinline__ void dsa_tile(RowState& st, const half8 (&qb)[36], const char* __restrict__ stage,
+template <class V>
+__device__ __forceinline__ void dsa_tile(RowState& st, const V (&qb)[36], const char* __restrict__ stage,
                                          int key0, int kend, float sl2, int lane, int w) {
   const int r = lane & 31, g = lane >> 5;
   floatx16 s = dsa_qk(stage, qb, r, g);
@@ -512,7 +516,7 @@ __device__ __forceinline__ void dsa_tile(RowState& st, const half8 (&qb)[36], co
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         if (key0 + 8 * blk + 4 * g + c >= kend) s[4 * blk + c] = kNegInf;
-  half8 pb[2];
+  V pb[2];
   softmax_update(st, s, sl2, pb);
   dsa_pv(st, stage, pb, lane, w);
 }
@@ -523,8 +527,9 @@ __device__ __forceinline__ void dsa_tile(RowState& st, const half8 (&qb)[36], co
 // would otherwise wait for every load in flight before each read); the explicit vmcnt wait and the barrier order
 // them.  Every LDS array the walk touches is a restrict-qualified parameter, so every LDS access in it carries
 // alias information (the compiler waits for all direct-to-LDS loads before any LDS access that lacks it).
+template <class V>
 __device__ __forceinline__ void dsa_ring_walk(char* __restrict__ st0, char* __restrict__ st1, char* __restrict__ st2,
-                                              RowState& st, const half8 (&qb)[36], const f16* kvb,
+                                              RowState& st, const V (&qb)[36], const f16* kvb,
                                               const int* __restrict__ sidx, int kbeg, int kend, int ntiles,
                                               const int (&drow)[10], const int (&dchk)[10], float sl2, int lane,
                                               int w) {
@@ -552,6 +557,7 @@ __device__ __forceinline__ void dsa_ring_walk(char* __restrict__ st0, char* __re
   }
 }
 
+template <class V>
 __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   __shared__ __attribute__((aligned(16))) char st0[kLatStageBytes], st1[kLatStageBytes], st2[kLatStageBytes];
   __shared__ int sidx[kChunk];
@@ -573,9 +579,9 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
 
   // Q^T operand of k-step c: head r's dims 16c + 8g .. 16c + 8g + 7 (chunk 2c + g of the query row).
   const f16* qrow = a.q + ((size_t)b * kH + hb * 32 + r) * kDK;
-  half8 qb[36];
+  V qb[36];
 #pragma unroll
-  for (int c = 0; c < 36; ++c) qb[c] = as_h8(ld16(qrow + 16 * c + 8 * g));
+  for (int c = 0; c < 36; ++c) qb[c] = as_v8<V>(ld16(qrow + 16 * c + 8 * g));
 
   // This wave's DMA instructions j = w + 4q: the (row, chunk) its lane fetches for each.
   int drow[10], dchk[10];
@@ -607,7 +613,8 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   }
 }
 
-// One workgroup (256 threads, 2 value dims each) per (b, head): LSE merge over the chunks.
+// One workgroup (256 threads, 2 value dims each) per (b, head): LSE merge over the chunks; E is the output type.
+template <class E>
 __global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
   const int bh = blockIdx.x;
   const int b = bh / kH, head = bh % kH, hb = head / 32, hr = head % 32;
@@ -620,7 +627,7 @@ __global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
                         ml = a.pml + base * 2;
                         o = a.po + base * kDC;
                       },
-                      a.out + (size_t)bh * kDC);
+                      reinterpret_cast<E*>(a.out) + (size_t)bh * kDC);
 }
 
 struct DsaLayout {
@@ -678,6 +685,8 @@ static int dsa_fill_args(DsaArgs& a, const void* q, const void* kv, const void* 
   return 0;
 }
 
+// V: operand type of iq/ik (half8: fp16, bf16x8: bf16); the select works on fp32 scores.
+template <class V>
 static int launch_index_select(const DsaArgs& a, hipStream_t s) {
   if (a.L > kTopK) {
     if (!a.hist_in_head) {
@@ -685,7 +694,7 @@ static int launch_index_select(const DsaArgs& a, hipStream_t s) {
       VMK_CHECK_HIP(hipGetLastError());
     }
     prof_before(kKDsaIndexer, s);
-    hipLaunchKernelGGL(dsa_indexer_kernel, dim3((unsigned)((a.L + kIdxWG - 1) / kIdxWG), (unsigned)a.B),
+    hipLaunchKernelGGL(dsa_indexer_kernel<V>, dim3((unsigned)((a.L + kIdxWG - 1) / kIdxWG), (unsigned)a.B),
                        dim3(64 * kIdxWaves), 0, s, a);
     prof_after(kKDsaIndexer, s);
     VMK_CHECK_HIP(hipGetLastError());
@@ -701,13 +710,15 @@ static int launch_index_select(const DsaArgs& a, hipStream_t s) {
   return 0;
 }
 
+// V: operand type of q/kv; the output has its element type.
+template <class V>
 static int launch_attention(const DsaArgs& a, hipStream_t s) {
   prof_before(kKDsaAttn, s);
-  hipLaunchKernelGGL(dsa_attn_kernel, dim3((unsigned)(a.B * 4 * kNChunk)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(dsa_attn_kernel<V>, dim3((unsigned)(a.B * 4 * kNChunk)), dim3(256), 0, s, a);
   prof_after(kKDsaAttn, s);
   VMK_CHECK_HIP(hipGetLastError());
   prof_before(kKDsaCombine, s);
-  hipLaunchKernelGGL(dsa_combine_kernel, dim3((unsigned)(a.B * kH)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(dsa_combine_kernel<elem_t<V>>, dim3((unsigned)(a.B * kH)), dim3(256), 0, s, a);
   prof_after(kKDsaCombine, s);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
@@ -727,36 +738,72 @@ extern "C" size_t vmk_dsa_workspace_size(int64_t B, int64_t L) {
   VMK_CHECK(workspace && ws_bytes >= vmk_dsa_workspace_size(B, L),                             \
             "workspace too small (query vmk_dsa_workspace_size)")
 
-extern "C" int vmk_dsa_indexer_select(const void* iq, const void* ik, const void* w, const void* lens, void* idx,
-                                      void* cnt, int64_t B, int64_t L, void* workspace, size_t ws_bytes,
-                                      void* stream) {
+template <class V>
+static int dsa_indexer_select(const void* iq, const void* ik, const void* w, const void* lens, void* idx, void* cnt,
+                              int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream) {
   VMK_CHECK(iq && ik && w && idx && cnt, "null pointer argument");
   DSA_COMMON_CHECKS();
   VMK_CHECK(aligned16(iq) && aligned16(ik), "iq/ik must be 16-byte aligned");
   DsaArgs a;
   dsa_fill_args(a, nullptr, nullptr, iq, ik, w, lens, nullptr, idx, cnt, B, L, workspace);
-  return launch_index_select(a, (hipStream_t)stream);
+  return launch_index_select<V>(a, (hipStream_t)stream);
 }
 
-extern "C" int vmk_dsa_sparse_mla(const void* q, const void* kv, const void* idx, const void* cnt, void* out,
-                                  int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream) {
+template <class V>
+static int dsa_sparse_mla(const void* q, const void* kv, const void* idx, const void* cnt, void* out, int64_t B,
+                          int64_t L, void* workspace, size_t ws_bytes, void* stream) {
   VMK_CHECK(q && kv && idx && cnt && out, "null pointer argument");
   DSA_COMMON_CHECKS();
   VMK_CHECK(aligned16(q) && aligned16(kv), "q/kv must be 16-byte aligned");
   DsaArgs a;
   dsa_fill_args(a, q, kv, nullptr, nullptr, nullptr, nullptr, out, (void*)idx, (void*)cnt, B, L, workspace);
-  return launch_attention(a, (hipStream_t)stream);
+  return launch_attention<V>(a, (hipStream_t)stream);
 }
 
-extern "C" int vmk_dsa_decode(const void* q, const void* kv, const void* iq, const void* ik, const void* w,
-                              const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L,
-                              void* workspace, size_t ws_bytes, void* stream) {
+template <class V>
+static int dsa_decode(const void* q, const void* kv, const void* iq, const void* ik, const void* w, const void* lens,
+                      void* out, void* idx, void* cnt, int64_t B, int64_t L, void* workspace, size_t ws_bytes,
+                      void* stream) {
   VMK_CHECK(q && kv && iq && ik && w && out && idx && cnt, "null pointer argument");
   DSA_COMMON_CHECKS();
   VMK_CHECK(aligned16(q) && aligned16(kv) && aligned16(iq) && aligned16(ik), "tensors must be 16-byte aligned");
   DsaArgs a;
   dsa_fill_args(a, q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace);
   hipStream_t s = (hipStream_t)stream;
-  if (int rc = launch_index_select(a, s)) return rc;
-  return launch_attention(a, s);
+  if (int rc = launch_index_select<V>(a, s)) return rc;
+  return launch_attention<V>(a, s);
+}
+
+extern "C" int vmk_dsa_indexer_select(const void* iq, const void* ik, const void* w, const void* lens, void* idx,
+                                      void* cnt, int64_t B, int64_t L, void* workspace, size_t ws_bytes,
+                                      void* stream) {
+  return dsa_indexer_select<half8>(iq, ik, w, lens, idx, cnt, B, L, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_dsa_indexer_select_bf16(const void* iq, const void* ik, const void* w, const void* lens, void* idx,
+                                           void* cnt, int64_t B, int64_t L, void* workspace, size_t ws_bytes,
+                                           void* stream) {
+  return dsa_indexer_select<bf16x8>(iq, ik, w, lens, idx, cnt, B, L, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_dsa_sparse_mla(const void* q, const void* kv, const void* idx, const void* cnt, void* out,
+                                  int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream) {
+  return dsa_sparse_mla<half8>(q, kv, idx, cnt, out, B, L, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_dsa_sparse_mla_bf16(const void* q, const void* kv, const void* idx, const void* cnt, void* out,
+                                       int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream) {
+  return dsa_sparse_mla<bf16x8>(q, kv, idx, cnt, out, B, L, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_dsa_decode(const void* q, const void* kv, const void* iq, const void* ik, const void* w,
+                              const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L,
+                              void* workspace, size_t ws_bytes, void* stream) {
+  return dsa_decode<half8>(q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_dsa_decode_bf16(const void* q, const void* kv, const void* iq, const void* ik, const void* w,
+                                   const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L,
+                                   void* workspace, size_t ws_bytes, void* stream) {
+  return dsa_decode<bf16x8>(q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace, ws_bytes, stream);
 }

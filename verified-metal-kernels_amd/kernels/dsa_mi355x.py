@@ -9,9 +9,8 @@ import vmk
 
 
 def kernel(q, kv, iq, ik, w, lens=None):
-    if any(x.dtype == torch.bfloat16 for x in (q, kv, iq, ik)):
-        raise TypeError("dsa kernel reads fp16 inputs; bf16 is not supported")
-    q, kv, iq, ik = (x.to(torch.float16).contiguous() for x in (q, kv, iq, ik))
+    dt = torch.bfloat16 if any(x.dtype == torch.bfloat16 for x in (q, kv, iq, ik)) else torch.float16
+    q, kv, iq, ik = (x.to(dt).contiguous() for x in (q, kv, iq, ik))
     w = w.to(device=q.device, dtype=torch.float32).contiguous()
     if lens is not None:
         lens = lens.to(device=q.device, dtype=torch.int32).contiguous()
@@ -20,7 +19,8 @@ def kernel(q, kv, iq, ik, w, lens=None):
 
 def select(iq, ik, w, lens=None):
     """The indexer + exact top-2048 stage alone: returns idx (B, 2048) int32 and cnt (B,) int32."""
-    iq, ik = (x.to(torch.float16).contiguous() for x in (iq, ik))
+    dt = torch.bfloat16 if torch.bfloat16 in (iq.dtype, ik.dtype) else torch.float16
+    iq, ik = (x.to(dt).contiguous() for x in (iq, ik))
     w = w.to(device=iq.device, dtype=torch.float32).contiguous()
     if lens is not None:
         lens = lens.to(device=iq.device, dtype=torch.int32).contiguous()

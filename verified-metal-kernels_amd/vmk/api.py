@@ -199,10 +199,11 @@ DSA_H, DSA_DK, DSA_DC, DSA_HI, DSA_DI, DSA_TOPK = 128, 576, 512, 64, 128, 2048
 
 
 def _dsa_shapes(q, kv, iq, ik, w, lens):
-    _need(q, "q", torch.float16, 3)
-    _need(kv, "kv", torch.float16, 3)
-    _need(iq, "iq", torch.float16, 3)
-    _need(ik, "ik", torch.float16, 3)
+    dt, _ = _elem(q)
+    _need(q, "q", dt, 3)
+    _need(kv, "kv", dt, 3)
+    _need(iq, "iq", dt, 3)
+    _need(ik, "ik", dt, 3)
     _need(w, "w", torch.float32, 2)
     B, L = kv.shape[0], kv.shape[1]
     if tuple(q.shape) != (B, DSA_H, DSA_DK) or kv.shape[2] != DSA_DK:
@@ -217,10 +218,11 @@ def _dsa_shapes(q, kv, iq, ik, w, lens):
 
 
 def dsa_indexer_select(iq, ik, w, lens=None, idx=None, cnt=None):
-    """Indexer scores + exact top-2048 per request.  Returns idx (B, 2048) int32 (unordered, first cnt[b] valid)
-    and cnt (B,) int32."""
-    _need(iq, "iq", torch.float16, 3)
-    _need(ik, "ik", torch.float16, 3)
+    """Indexer scores + exact top-2048 per request; iq/ik both fp16 or both bf16, w fp32.  Returns idx (B, 2048)
+    int32 (unordered, first cnt[b] valid) and cnt (B,) int32."""
+    dt, sfx = _elem(iq)
+    _need(iq, "iq", dt, 3)
+    _need(ik, "ik", dt, 3)
     _need(w, "w", torch.float32, 2)
     B, L = ik.shape[0], ik.shape[1]
     if tuple(iq.shape) != (B, DSA_HI, DSA_DI) or tuple(ik.shape) != (B, L, DSA_DI) or tuple(w.shape) != (B, DSA_HI):
@@ -234,43 +236,46 @@ def dsa_indexer_select(iq, ik, w, lens=None, idx=None, cnt=None):
         cnt = torch.empty(B, dtype=torch.int32, device=ik.device)
     ws_n = lib.load().vmk_dsa_workspace_size(B, L)
     ws = workspace(ws_n, ik.device)
-    lib.call("vmk_dsa_indexer_select", iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
+    lib.call("vmk_dsa_indexer_select" + sfx, iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
              0 if lens is None else lens.data_ptr(), idx.data_ptr(), cnt.data_ptr(), B, L, ws.data_ptr(),
              ws.numel(), _stream(ik))
     return idx, cnt
 
 
 def dsa_sparse_mla(q, kv, idx, cnt, out=None):
-    """Sparse absorbed-MLA attention of q (B,128,576) over rows kv[b, idx[b, :cnt[b]]].  Returns (B,128,512) fp16."""
-    _need(q, "q", torch.float16, 3)
-    _need(kv, "kv", torch.float16, 3)
+    """Sparse absorbed-MLA attention of q (B,128,576) over rows kv[b, idx[b, :cnt[b]]], q/kv both fp16 or both bf16.
+    Returns (B,128,512) of q's dtype."""
+    dt, sfx = _elem(q)
+    _need(q, "q", dt, 3)
+    _need(kv, "kv", dt, 3)
     _need(idx, "idx", torch.int32, 2)
     _need(cnt, "cnt", torch.int32, 1)
     B, L = kv.shape[0], kv.shape[1]
     device_ok(q.device)
     if out is None:
-        out = torch.empty(B, DSA_H, DSA_DC, dtype=torch.float16, device=q.device)
+        out = torch.empty(B, DSA_H, DSA_DC, dtype=dt, device=q.device)
     ws_n = lib.load().vmk_dsa_workspace_size(B, L)
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_dsa_sparse_mla", q.data_ptr(), kv.data_ptr(), idx.data_ptr(), cnt.data_ptr(), out.data_ptr(),
+    lib.call("vmk_dsa_sparse_mla" + sfx, q.data_ptr(), kv.data_ptr(), idx.data_ptr(), cnt.data_ptr(), out.data_ptr(),
              B, L, ws.data_ptr(), ws.numel(), _stream(q))
     return out
 
 
 def dsa_decode(q, kv, iq, ik, w, lens=None, out=None, idx=None, cnt=None):
-    """Full DSA decode step (indexer -> top-2048 -> sparse MLA).  Returns out (B,128,512) fp16; the selected
-    indices land in `idx`/`cnt` when given."""
+    """Full DSA decode step (indexer -> top-2048 -> sparse MLA); q, kv, iq, ik all fp16 or all bf16, w fp32.
+    Returns out (B,128,512) of q's dtype; the selected indices land in `idx`/`cnt` when given."""
     B, L = _dsa_shapes(q, kv, iq, ik, w, lens)
+    dt, sfx = _elem(q)
     device_ok(q.device)
     if out is None:
-        out = torch.empty(B, DSA_H, DSA_DC, dtype=torch.float16, device=q.device)
+        out = torch.empty(B, DSA_H, DSA_DC, dtype=dt, device=q.device)
     if idx is None:
         idx = torch.empty(B, DSA_TOPK, dtype=torch.int32, device=q.device)
     if cnt is None:
         cnt = torch.empty(B, dtype=torch.int32, device=q.device)
     ws_n = lib.load().vmk_dsa_workspace_size(B, L)
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_dsa_decode", q.data_ptr(), kv.data_ptr(), iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
+    lib.call("vmk_dsa_decode" + sfx, q.data_ptr(), kv.data_ptr(), iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
              0 if lens is None else lens.data_ptr(), out.data_ptr(), idx.data_ptr(), cnt.data_ptr(), B, L,
              ws.data_ptr(), ws.numel(), _stream(q))
     return out

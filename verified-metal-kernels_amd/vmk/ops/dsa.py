@@ -6,12 +6,14 @@ Per request b (one new token), DeepSeek-V3.2 shapes (ops/dsa.py:1-9):
   attend : absorbed MLA, 128 query heads over 576-dim latent rows (512 latent + 64 rope):
            out = softmax(q . kv[idx]^T * scale) @ kv[idx][:, :512],  scale = 1/sqrt(192)
 Shapes: q (B,128,576) fp16, kv (B,L,576) fp16, iq (B,64,128) fp16, ik (B,L,128) fp16, w (B,64) fp32,
-lens (B,) int32 or None  ->  out (B,128,512) fp16.
+lens (B,) int32 or None  ->  out (B,128,512) fp16.  q, kv, iq, ik may all be bf16 instead (out is then bf16).
 """
 import math
 
 import numpy as np
 import torch
+
+from .elem import cast16
 
 NAME = "dsa"
 H, DC, DR, HI, DI, TOPK = 128, 512, 64, 64, 128, 2048          # ops/dsa.py:15
@@ -24,7 +26,7 @@ CONFIGS = {"C5": (dict(B=4, L=65536), "randn")}                # BASELINE C5
 
 def make_inputs(shape, seed=0, dist="randn", device="cpu"):
     """Seeded inputs with the reference's draw order (ops/dsa.py:22-50): q, kv, iq, ik, w (scaled by
-    HI^-1/2 * DI^-1/2), then the dist recipe; fp16 cast on the host, w stays float32, lens int32 or None."""
+    HI^-1/2 * DI^-1/2), then the dist recipe; fp16 (or shape["dtype"] = "bf16") cast on the host, w stays float32, lens int32 or None."""
     rng = np.random.default_rng(seed)
     B, L = shape["B"], shape["L"]
     q = rng.standard_normal((B, H, DK), dtype=np.float32)
@@ -52,7 +54,7 @@ def make_inputs(shape, seed=0, dist="randn", device="cpu"):
         q, kv = q * 1e-3, kv * 1e-3
     elif dist != "randn":
         raise ValueError(f"unknown dist {dist!r}")
-    f = lambda a: torch.from_numpy(a.astype(np.float16)).to(device)
+    f = lambda a: cast16(a, shape.get("dtype", "fp16"), device)
     return dict(q=f(q), kv=f(kv), iq=f(iq), ik=f(ik), w=torch.from_numpy(w).to(device),
                 lens=None if lens is None else torch.from_numpy(lens).to(device))
 
@@ -81,9 +83,9 @@ def torch_ref(q, kv, iq, ik, w, lens=None):
 
 
 def torch_fp32_ref(q, kv, iq, ik, w, lens=None):
-    """The same algorithm computed in float32, output cast to fp16 (the L1 standard op, ops/dsa.py:150-153)."""
+    """The same algorithm computed in float32, output cast to q's dtype (the L1 standard op, ops/dsa.py:150-153)."""
     f = lambda a: a.float()
-    return torch_ref(f(q), f(kv), f(iq), f(ik), w, lens).half()
+    return torch_ref(f(q), f(kv), f(iq), f(ik), w, lens).to(q.dtype)
 
 
 def chain_torch(out, kw):
@@ -101,7 +103,7 @@ FUZZ = [(dict(B=1, L=1), "randn"), (dict(B=1, L=2048), "randn"), (dict(B=1, L=20
         (dict(B=2, L=6000), "tiny"), (dict(B=4, L=3000), "ragged")]                       # ops/dsa.py:158-161
 L3_CASES = [(dict(B=1, L=1500), "randn"), (dict(B=1, L=8192), "randn"), (dict(B=1, L=65536), "randn"),
             (dict(B=2, L=8192), "large"), (dict(B=2, L=8192), "needle")]                  # ops/dsa.py:162-163
-EXTRA = [(dict(B=4, L=65536), "randn"), (dict(B=5, L=4100), "ragged")]
+EXTRA = [(dict(B=4, L=65536), "randn"), (dict(B=5, L=4100), "ragged"), (dict(B=2, L=6000, dtype="bf16"), "randn")]
 # Row invariance (L4): every request decoded alone (B = 1) must give the same bits as in the batch.
 L4_CASES = [(dict(B=4, L=65536), "randn"), (dict(B=5, L=4100), "ragged"), (dict(B=3, L=2049), "randn")]
 
