@@ -182,6 +182,14 @@ __device__ __forceinline__ void wait_vmem_dyn(int n) {
 #undef VMK_WAIT_CASE
 }
 
+// Workgroup barrier that waits for this wave's LDS operations only (s_waitcnt lgkmcnt(0), then s_barrier).  The
+// compiler's __syncthreads would also wait for every direct-to-LDS load in flight (s_waitcnt vmcnt(0)), i.e. drain
+// the ring each tile; the walks wait for their own tiles explicitly before barriers that publish them.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // Runs f(integral_constant<int, I>) for I = 0 .. N-1 in order while it returns true; false if one returned false.
 template <int I, int N, class F>
@@ -346,7 +354,7 @@ __device__ __forceinline__ void ring_walk(char* ring, const Src& src, int kbeg, 
       const int t = t0 + S;
       if (t >= ntiles) return false;
       wait_vmem_dyn(DPW * min(NS - 2, ntiles - 1 - t));
-      __syncthreads();
+      lds_barrier();
       if (t + NS - 1 < ntiles) issue(ring + ((S + NS - 1) % NS) * kStageBytes, t + NS - 1);
       compute(S, t);
       return true;
@@ -556,8 +564,8 @@ __device__ __forceinline__ void combine_row(int nparts, Part part, E* out) {
 // ---- one workgroup of NW waves sharing a ring of kRowsStages stages: wave w owns rows [32w, 32w+32) and every wave
 // consumes every tile of [kbeg, kbeg + 32*ntiles).  Writes the WG's partial (32*NW rows) like attend_wg.
 // Eight stages (128 KB): seven tiles in flight, and one workgroup per CU (two would not fit).  LDS reads address
-// stages 0-3 from the per-lane offsets of tl and stages 4-7 from those of tl_hi (64 KB further), so every stage offset
-// fits the 16-bit immediate field.
+// stages 0-3 from the per-lane offsets of tl and stages 4-7 from those of tl_hi (64 KB further), so every stage
+// offset fits the 16-bit immediate field.
 constexpr int kRowsStages = 8;
 constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
 

@@ -495,15 +495,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup barrier that waits for this wave's LDS operations only (s_waitcnt lgkmcnt(0), then s_barrier).  The
-// compiler's __syncthreads would also wait for every direct-to-LDS load in flight, i.e. drain the ring; the walks
-// wait for their own tiles explicitly before barriers that publish them.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // One tile: S^T over all QK dims, masked online softmax, PV over this wave's value dims.
 template <class V>
 __device__ __forceinline__ void dsa_tile(RowState& st, const V (&qb)[36], const char* __restrict__ stage,
