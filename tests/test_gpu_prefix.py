@@ -40,6 +40,8 @@ ROWS_CASES = [
     (dict(N=32, P=16384, S=40, S_min=0), "randn", 111),                    # long prefix, short or empty suffixes
     (dict(N=100, P=3000, S=500, S_min=1, Hq=24, Hkv=8), "randn", 112),     # G = 3: requests straddle row blocks
     (dict(N=24, P=5000, S=700), "randn", 113),                             # equal suffix lengths
+    (dict(N=40, P=4096, S=300, S_min=1, Hq=64, Hkv=8), "randn", 115),      # G = 8: the general merge
+    (dict(N=40, P=65536, S=100, S_min=1), "randn", 116),                   # 64 prefix chunks: the general merge
 ]
 
 

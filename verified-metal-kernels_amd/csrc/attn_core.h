@@ -205,26 +205,30 @@ __device__ __forceinline__ bool unroll_while(F& f) {
 // Per-lane byte offsets that are the same for every tile, computed once per walk, so that a tile costs no address
 // arithmetic: the stage is a compile-time index in the unrolled walks and lands in the instructions' immediate
 // offset fields.
-//   dma[j]: this lane's 16 B of DMA instruction j (rows 4j..4j+3) within a tile's 32 rows of 256 B: logical chunk
-//           (l & 15) ^ swz(row) of row 4j + (l >> 4), which lands at chunk position l & 15 of LDS block j;
+//   dma[j & 3]: this lane's 16 B of DMA instruction j (rows 4j..4j+3) within a tile's 32 rows of 256 B, less 1024 j:
+//           logical chunk (l & 15) ^ swz(row) of row 4j + (l >> 4), which lands at chunk position l & 15 of LDS block
+//           j.  swz(4j + s) = (s << 2) | (j & 3) for s < 4, so the lane part depends on j & 3 only (dma_lane);
 //   k[t]:   K operand of step t: row l % 32, logical chunk 8g + t (g = l / 32), from the ring base;
 //   v[2dt + rr]: V^T half rr of d-tile dt at step 0 (step 1 is 16 rows = 4096 bytes further): source row
 //           8rr + 4g + ((l & 15) >> 2), head-dim 32dt + 16((l >> 4) & 1) + 4(l & 3), from the ring base.  swz of
 //           row + 16 equals swz of row, so step 1 really is a constant 4096 further.
 struct TileLanes {
-  uint32_t dma[8];
+  uint32_t dma[4];
   uint32_t k[8];
   uint32_t v[8];
 };
 
+// Lane part of DMA instruction j's source offset within a tile (the whole offset is 1024 j + dma_lane(lane, j)).
+__device__ __forceinline__ uint32_t dma_lane(int lane, int j) {
+  const int sub = lane >> 4, row = 4 * (j & 3) + sub;
+  return sub * 256 + (((lane & 15) ^ swz(row)) << 4);
+}
+
 __device__ __forceinline__ TileLanes tile_lanes(int lane, uint32_t ring_off) {
   TileLanes tl;
-  const int sub = lane >> 4, cl = lane & 15, r = lane & 31, g = lane >> 5;
+  const int r = lane & 31, g = lane >> 5;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = 4 * j + sub;
-    tl.dma[j] = row * 256 + ((cl ^ swz(row)) << 4);
-  }
+  for (int j = 0; j < 4; ++j) tl.dma[j] = dma_lane(lane, j);
 #pragma unroll
   for (int t = 0; t < 8; ++t) tl.k[t] = ring_off + r * 256 + (((8 * g + t) ^ swz(r)) << 4);
   const int e = (lane & 15) >> 2, hc = (lane >> 4) & 1, a4 = lane & 3;
@@ -240,32 +244,50 @@ __device__ __forceinline__ TileLanes tile_lanes(int lane, uint32_t ring_off) {
   return tl;
 }
 
+// Buffer resource of one 8 KB tile half (32 rows of 256 B) at a uniform address: base, 8192 bytes in range (an
+// offset outside the half would read zeros, never foreign memory), raw 32-bit dword format (word 3 = 0x00020000).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const f16* tile) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(tile), 0, 8192, 0x00020000);
+}
+
 // DMA instruction i (0..15) of a tile: i < 8 loads K rows 4i..4i+3 into LDS block i, i >= 8 the V rows of block
-// i - 8 into the V half.  A whole tile inside the sequence takes the rows at uniform base + per-lane offset; the last,
-// partial tile of a walk takes keys past src.kend from g_zero_row.
+// i - 8 into the V half.  A whole tile inside the sequence (issue_dma_full) takes the rows at uniform base + per-lane
+// offset; the last, partial tile of a walk (issue_dma_part) takes keys past src.kend from g_zero_row.  Whether a tile
+// is whole is the same for the whole wave, and the callers take the two cases in separate branches so that the
+// whole-tile path carries none of the partial tile's per-lane pointers.
+// lp = dma_lane(lane, i & 7): the rows of block j = i & 7 start 1024 j bytes into the tile half, which the load takes
+// as its scalar offset: a buffer load with the half's resource in scalar registers and lp as the only per-lane
+// operand, so a whole tile costs no per-lane address arithmetic.
 template <class Src>
-__device__ __forceinline__ void issue_dma(char* __restrict__ stage, const Src& src, int key0, bool full, int i,
-                                          uint32_t off, int lane) {
+__device__ __forceinline__ void issue_dma_full(char* __restrict__ stage, const Src& src, int key0, int i,
+                                               uint32_t lp) {
   const int j = i & 7;
-  char* dst = stage + (i < 8 ? 0 : 8192) + j * 1024;
-  const char* gp;
+  const __amdgpu_buffer_rsrc_t r = tile_rsrc(i < 8 ? src.ktile(key0) : src.vtile(key0));
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, VMK_LPTR(stage + (i < 8 ? 0 : 8192) + j * 1024), 16, lp, 1024 * j, 0,
+                                           0);
+}
+
+template <class Src>
+__device__ __forceinline__ void issue_dma_part(char* __restrict__ stage, const Src& src, int key0, int i,
+                                               uint32_t lp, int lane) {
+  const int j = i & 7;
   const f16* tile = i < 8 ? src.ktile(key0) : src.vtile(key0);
-  if (full) {
-    gp = reinterpret_cast<const char*>(tile) + off;
-  } else {
-    const int row = 4 * j + (lane >> 4);
-    gp = reinterpret_cast<const char*>(key0 + row < src.kend ? tile + row * 128 : g_zero_row) + (off & 255);
-  }
-  __builtin_amdgcn_global_load_lds(VMK_GPTR(gp), VMK_LPTR(dst), 16, 0, 0);
+  const int row = 4 * j + (lane >> 4);
+  const char* gp = reinterpret_cast<const char*>(key0 + row < src.kend ? tile + row * 128 : g_zero_row) + (lp & 255);
+  __builtin_amdgcn_global_load_lds(VMK_GPTR(gp), VMK_LPTR(stage + (i < 8 ? 0 : 8192) + j * 1024), 16, 0, 0);
 }
 
 // All 16 DMA instructions of one tile from one wave.
 template <class Src>
 __device__ __forceinline__ void issue_tile_dma(char* __restrict__ stage, const Src& src, int key0,
                                                const TileLanes& tl, int lane) {
-  const bool full = key0 + kTile <= src.kend;
+  if (key0 + kTile <= src.kend) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) issue_dma(stage, src, key0, full, i, tl.dma[i & 7], lane);
+    for (int i = 0; i < 16; ++i) issue_dma_full(stage, src, key0, i, tl.dma[i & 3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) issue_dma_part(stage, src, key0, i, tl.dma[i & 3], lane);
+  }
 }
 
 typedef short short4v __attribute__((ext_vector_type(4)));
@@ -331,17 +353,18 @@ template <int NS, int NW, class Src, class Compute>
 __device__ __forceinline__ void ring_walk(char* ring, const Src& src, int kbeg, int ntiles, int wave, int lane,
                                           Compute compute) {
   constexpr int DPW = 16 / NW;
-  uint32_t dmaw[DPW];                                       // this wave's instructions' lane offsets
+  uint32_t dmaw[DPW];                                       // lane parts of this wave's instructions
 #pragma unroll
-  for (int q = 0; q < DPW; ++q) {
-    const int row = 4 * ((wave + q * NW) & 7) + (lane >> 4);
-    dmaw[q] = row * 256 + (((lane & 15) ^ swz(row)) << 4);
-  }
+  for (int q = 0; q < DPW; ++q) dmaw[q] = dma_lane(lane, (wave + q * NW) & 7);
   auto issue = [&](char* stage, int t) {
     const int key0 = kbeg + t * kTile;
-    const bool full = key0 + kTile <= src.kend;
+    if (key0 + kTile <= src.kend) {
 #pragma unroll
-    for (int q = 0; q < DPW; ++q) issue_dma(stage, src, key0, full, wave + q * NW, dmaw[q], lane);
+      for (int q = 0; q < DPW; ++q) issue_dma_full(stage, src, key0, wave + q * NW, dmaw[q]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < DPW; ++q) issue_dma_part(stage, src, key0, wave + q * NW, dmaw[q], lane);
+    }
   };
   auto pre = [&](auto S) {
     if (S >= ntiles) return false;
@@ -569,6 +592,33 @@ __device__ __forceinline__ void combine_row(int nparts, Part part, E* out) {
 constexpr int kRowsStages = 8;
 constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
 
+// The row-split workgroup's partial (NW waves x 32 rows), written through LDS so that every store instruction
+// writes two whole rows (1 KB contiguous) instead of 32-byte pieces of 32 rows.  Each wave parks its O^T registers
+// in its own 16 KB of LDS as 32 rows of 128 floats, the 16-byte chunk c of row r at chunk position (c + r) mod 32
+// (at most two lanes per bank group on the writes, none on the row reads), then stores rows 2i, 2i + 1 per
+// instruction.  Called by every wave of the workgroup (it contains a barrier); rows >= nvalid are not written.
+__device__ __forceinline__ void store_partial_rows(char* smem, float* po, float* pml, const RowState& st, int wave,
+                                                   int lane, int nvalid) {
+  __syncthreads();                                          // every wave is done with the ring
+  float* lds = reinterpret_cast<float*>(smem) + wave * 32 * 128;
+  const int r = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+      *reinterpret_cast<floatx4*>(lds + r * 128 + (((dt * 8 + 2 * blk + g) + r) & 31) * 4) =
+          floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]};
+  const float ltot = st.l + xor32(st.l);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");       // the wave reads back only its own rows
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = 2 * i + g;
+    const floatx4 v = *reinterpret_cast<const floatx4*>(lds + row * 128 + ((r + row) & 31) * 4);
+    if (row < nvalid) *reinterpret_cast<floatx4*>(po + row * 128 + r * 4) = v;
+  }
+  if (g == 0 && r < nvalid) *reinterpret_cast<float2*>(pml + 2 * r) = float2{st.m, ltot};
+}
+
 template <int NW, class V = half8, class Src, class QRow>
 __device__ __forceinline__ void attend_wg_rows(char* smem, const Src& src, QRow qrow, int nrows, int kbeg,
                                                int ntiles, float* po, float* pml) {
@@ -585,7 +635,9 @@ __device__ __forceinline__ void attend_wg_rows(char* smem, const Src& src, QRow 
     if (has_rows)
       compute_tile_lds(st, qb, smem + (S & 3) * kStageBytes, S < 4 ? tl : tl_hi, src, kbeg + t * kTile, lane);
   });
-  if (has_rows) store_partial(po + (size_t)wave * 32 * 128, pml + wave * 32 * 2, st, lane, nrows - wave * 32);
+  static_assert(NW * 32 * 128 * 4 <= kRowsSmemBytes, "the partial's transpose fits in the ring");
+  store_partial_rows(smem, po + (size_t)wave * 32 * 128, pml + wave * 32 * 2, st, wave, lane,
+                                nrows - wave * 32);
 }
 
 }  // namespace vmk

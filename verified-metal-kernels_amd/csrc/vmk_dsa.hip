@@ -167,9 +167,13 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
   float* sc = a.scores + (size_t)b * a.Ls;
   auto issue = [&](char* stage, int j) {
     const int key0 = (t0 + j) * kTile;
-    const bool full = key0 + kTile <= n;
+    if (key0 + kTile <= n) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) issue_dma(stage, src, key0, full, i, tl.dma[i], lane);
+      for (int i = 0; i < 8; ++i) issue_dma_full(stage, src, key0, i, tl.dma[i & 3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) issue_dma_part(stage, src, key0, i, tl.dma[i & 3], lane);
+    }
   };
   auto compute = [&](const char* stage, int j) {
     u32x4 kk[8];
