@@ -62,29 +62,28 @@ struct RangeSrc {
 };
 
 // Keys [kbeg, kend) of one KV head of a sequence in a paged cache: pages of ps rows (ps a multiple of 32, so a tile
-// never straddles two pages) laid out (num_pages, Hkv, ps, 128), the sequence's pages listed in `table`.  Lane i
-// holds the id of the range's i-th page (a range of at most 2048 keys spans at most 64 pages), so a tile finds its
-// page with one readlane.  An id outside [0, num_pages) is an absent page: its tiles read a zero tile and its keys
-// are masked out.
+// never straddles two pages) laid out (num_pages, Hkv, ps, 128), the sequence's pages listed in `table`.  Lane t
+// holds the K and V row addresses of the range's tile t (keys kbeg + 32 t ..; kbeg is a multiple of 32 and a range
+// has at most 2048 keys, i.e. 64 tiles), worked out once per lane, so a tile finds its rows with readlanes only (no
+// division or multiply per tile).  An id outside [0, num_pages) is an absent page: its tiles read a zero tile and
+// its keys are masked out.
 struct PagedSrc {
-  const f16* kpool;        // page 0 of this KV head
-  const f16* vpool;
-  size_t page_stride;      // elements from one page to the next (Hkv * ps * 128)
-  int ps, first, npages, kend;
-  int pid;                 // this lane's page id: table[first + lane]
+  const f16* kt;           // this lane's tile: K rows, or g_zero_tile when its page is absent
+  const f16* vt;           //                   V rows
+  int here;                // 1 when this lane's tile has a page
+  int kbeg, kend;
   float scale;
-  __device__ int page(int key0) const { return __builtin_amdgcn_readlane(pid, key0 / ps - first); }
-  __device__ bool present(int p) const { return (unsigned)p < (unsigned)npages; }
-  __device__ const f16* ktile(int key0) const {
-    const int p = page(key0);
-    return present(p) ? kpool + (size_t)p * page_stride + (size_t)(key0 % ps) * 128 : g_zero_tile;
+  __device__ int tile(int key0) const { return (key0 - kbeg) >> 5; }
+  __device__ static const f16* lane_ptr(const f16* p, int t) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, t), hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), t);
+    return reinterpret_cast<const f16*>(((uint64_t)hi << 32) | lo);
   }
-  __device__ const f16* vtile(int key0) const {
-    const int p = page(key0);
-    return present(p) ? vpool + (size_t)p * page_stride + (size_t)(key0 % ps) * 128 : g_zero_tile;
-  }
+  __device__ bool present(int key0) const { return __builtin_amdgcn_readlane(here, tile(key0)) != 0; }
+  __device__ const f16* ktile(int key0) const { return lane_ptr(kt, tile(key0)); }
+  __device__ const f16* vtile(int key0) const { return lane_ptr(vt, tile(key0)); }
   __device__ void mask(floatx16& s, int key0, int g) const {
-    const bool here = present(page(key0));
+    const bool here = present(key0);
     if (here && key0 + kTile <= kend) return;              // whole tile inside (same for the whole wave)
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
@@ -99,17 +98,16 @@ struct PagedSrc {
 __device__ __forceinline__ PagedSrc paged_src(const PrefixArgs& a, const int* table, int ntable, int h, int kbeg,
                                               int kend) {
   PagedSrc s;
-  s.kpool = a.kp + (size_t)h * a.ps * 128;
-  s.vpool = a.vp + (size_t)h * a.ps * 128;
-  s.page_stride = (size_t)a.Hkv * a.ps * 128;
-  s.ps = a.ps;
-  s.first = kbeg / a.ps;
-  s.npages = a.num_pages;
+  s.kbeg = kbeg;
   s.kend = kend;
   s.scale = a.sl2;
-  const int idx = s.first + (int)(threadIdx.x & 63);
-  const int last = kend > kbeg ? (kend - 1) / a.ps : -1;
-  s.pid = idx <= last && idx < ntable ? table[idx] : -1;
+  const int key = kbeg + kTile * (int)(threadIdx.x & 63);     // this lane's tile
+  const int slot = key / a.ps;
+  const int page = key < kend && slot < ntable ? table[slot] : -1;
+  s.here = (unsigned)page < (unsigned)a.num_pages;
+  const size_t off = (((size_t)page * a.Hkv + h) * a.ps + (key - slot * a.ps)) * 128;
+  s.kt = s.here ? a.kp + off : g_zero_tile;
+  s.vt = s.here ? a.vp + off : g_zero_tile;
   return s;
 }
 
