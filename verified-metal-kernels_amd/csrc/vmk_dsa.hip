@@ -426,31 +426,38 @@ __global__ __launch_bounds__(1024) void dsa_hist_zero_kernel(DsaArgs a) {
 // Workgroup = (request b, block of 32 heads, chunk of 128 selected keys); 4 waves.  Every wave computes the full
 // S^T tile (all 576 QK dims, in the same order, so all four hold bit-identical scores, softmax state and P) and owns
 // the value dims [128w, 128w+128) of O.
-// The selected latent rows of a 32-key tile are gathered by direct-to-LDS loads into a 3-stage ring (two tiles in
-// flight while one is computed).  In a stage, row r starts at byte r * kLatStride: 1152 bytes of the row plus 16 of
-// padding, so the 73-chunk stride is odd and 16 consecutive rows at one chunk fall on 16 distinct bank groups
-// (conflict-free K-operand reads).  DMA instruction j fills stage bytes [1024j, 1024j + 1024): lane i's 16 bytes go
-// to slot 64j + i, which is chunk (slot % 73) of row (slot / 73); padding slots and slots past the 32 rows take
-// copies of real chunks.  V^T is read from the same rows with the transposing LDS read.
+// The selected latent rows of the chunk's four 32-key tiles are gathered by direct-to-LDS loads into four stages,
+// all issued before the first tile is computed, so the chunk waits for one gather round trip.  In a stage, row r
+// starts at byte r * kLatStride: 1152 bytes of the row plus 16 of padding, so the 73-chunk stride is odd and 16
+// consecutive rows at one chunk fall on 16 distinct bank groups (conflict-free K-operand reads).  DMA instruction j
+// (0 <= j < 37, wave j % 4 issues it) fills stage bytes [1024j, 1024j + 1024): lane i's 16 bytes go to slot 64j + i,
+// which is chunk (slot % 73) of row (slot / 73); padding slots and slots past the 32 rows take copies of real chunks.
+// V^T is read from the same rows with the transposing LDS read.
 constexpr int kSSlot = 16 * 64;          // floats of one wave's partial S^T tile
 constexpr int kLatChunks = kDK / 8;      // 72 chunks of 16 bytes per latent row
 constexpr int kLatStride = (kLatChunks + 1) * 16;           // 1168 bytes
-constexpr int kLatInstr = 40;            // DMA instructions per tile: 10 per wave, >= 32 * 73 / 64 slots
+constexpr int kLatInstr = 37;            // DMA instructions per tile (>= 32 * 73 / 64 slots): 10 for wave 0, 9 others
+constexpr int kLatInstrMin = kLatInstr / 4;                 // the fewest any wave issues per tile
 constexpr int kLatStageBytes = kLatInstr * 1024;
-constexpr int kLatStages = 3;
+constexpr int kLatStages = kChunk / kTile;                  // one stage per tile of the chunk
 static_assert(kLatInstr * 64 >= kTile * (kLatChunks + 1), "a stage holds 32 padded rows");
 
 // Zero latent row: the source of every key past the selected count.
 __device__ const f16 g_zero_latent[kDK] = {};
 
-// The 10 DMA instructions of wave w for the tile at key0.
-__device__ __forceinline__ void dsa_issue_rows(char* __restrict__ stage, const f16* kvb, const int* sidx, int kbeg,
-                                               int kend, int key0, const int (&drow)[10], const int (&dchk)[10],
-                                               int w) {
+// The DMA instructions j = w + 4q < kLatInstr of wave w for the tile at key0.  The selected positions are read
+// from LDS first, all ten together, so the instructions issue back to back.
+__device__ __forceinline__ void dsa_issue_rows(char* __restrict__ stage, const f16* kvb, const int* __restrict__ sidx,
+                                               int kbeg, int kend, int key0, const int (&drow)[10],
+                                               const int (&dchk)[10], int w) {
+  int pos[10];
+#pragma unroll
+  for (int q = 0; q < 10; ++q) pos[q] = sidx[key0 - kbeg + drow[q]];     // < kChunk: key0 - kbeg <= 96, drow <= 31
 #pragma unroll
   for (int q = 0; q < 10; ++q) {
+    if (w + 4 * q >= kLatInstr) break;                      // wave-uniform
     const int key = key0 + drow[q];
-    const f16* row = key < kend ? kvb + (size_t)sidx[key - kbeg] * kDK : g_zero_latent;
+    const f16* row = key < kend ? kvb + (size_t)pos[q] * kDK : g_zero_latent;
     __builtin_amdgcn_global_load_lds(VMK_GPTR(row + 8 * dchk[q]), VMK_LPTR(stage + (w + 4 * q) * 1024), 16, 0, 0);
   }
 }
@@ -516,67 +523,77 @@ __device__ __forceinline__ void dsa_tile(RowState& st, const V (&qb)[36], const 
   dsa_pv(st, stage, pb, lane, w);
 }
 
-// Ring walk over the chunk's tiles: tile t lives in stage t % 3, two tiles are in flight while one is computed, and
-// the stage refilled at step t held tile t - 1, which every wave finished before the step's barrier.  The three
-// stages are separate LDS arrays, so the compiler can tell the stage being filled from the stage being read (it
-// would otherwise wait for every load in flight before each read); the explicit vmcnt wait and the barrier order
-// them.  Every LDS array the walk touches is a restrict-qualified parameter, so every LDS access in it carries
-// alias information (the compiler waits for all direct-to-LDS loads before any LDS access that lacks it).
+// Walk over the chunk's tiles: every tile has its own stage and all four are requested up front (rows past kend
+// read the zero row).  Before tile t a wave waits until at most kLatInstrMin * (3 - t) of its DMA instructions are
+// in flight, i.e. its part of tile t has landed (wave 0, with one more instruction per tile, waits slightly longer
+// than needed), and the barrier makes every wave's part visible.  The stages are separate LDS arrays and every LDS
+// array the walk touches is a restrict-qualified parameter, so the compiler can tell the stages apart (it would
+// otherwise wait for every load in flight before each LDS read).  The last wait drains every load, so no DMA is
+// still writing LDS when the workgroup ends.
 template <class V>
-__device__ __forceinline__ void dsa_ring_walk(char* __restrict__ st0, char* __restrict__ st1, char* __restrict__ st2,
-                                              RowState& st, const V (&qb)[36], const f16* kvb,
-                                              const int* __restrict__ sidx, int kbeg, int kend, int ntiles,
-                                              const int (&drow)[10], const int (&dchk)[10], float sl2, int lane,
-                                              int w) {
-  auto stage = [&](auto S) -> char* {
-    if constexpr (S % kLatStages == 0) return st0;
-    else if constexpr (S % kLatStages == 1) return st1;
-    else return st2;
-  };
+__device__ __forceinline__ void dsa_chunk_walk(char* __restrict__ st0, char* __restrict__ st1, char* __restrict__ st2,
+                                               char* __restrict__ st3, RowState& st, const V (&qb)[36],
+                                               const f16* kvb, const int* __restrict__ sidx, int kbeg, int kend,
+                                               int ntiles, const int (&drow)[10], const int (&dchk)[10], float sl2,
+                                               int lane, int w) {
+  static_assert(kLatStages == 4 && 3 * kLatInstrMin < 64, "four stages, vmcnt range");
   dsa_issue_rows(st0, kvb, sidx, kbeg, kend, kbeg, drow, dchk, w);
-  if (ntiles > 1) dsa_issue_rows(st1, kvb, sidx, kbeg, kend, kbeg + kTile, drow, dchk, w);
-  for (int t0 = 0; t0 < ntiles; t0 += kLatStages) {
-    auto step = [&](auto S) {
-      const int t = t0 + S;
-      if (t >= ntiles) return false;
-      if (t + 1 < ntiles) wait_vmcnt<10>();
-      else wait_vmcnt<0>();
-      lds_barrier();
-      if (t + 2 < ntiles)
-        dsa_issue_rows(stage(std::integral_constant<int, S + 2>()), kvb, sidx, kbeg, kend, kbeg + (t + 2) * kTile,
-                       drow, dchk, w);
-      dsa_tile(st, qb, stage(S), kbeg + t * kTile, kend, sl2, lane, w);
-      return true;
-    };
-    if (!unroll_while<0, kLatStages>(step)) break;
+  dsa_issue_rows(st1, kvb, sidx, kbeg, kend, kbeg + kTile, drow, dchk, w);
+  dsa_issue_rows(st2, kvb, sidx, kbeg, kend, kbeg + 2 * kTile, drow, dchk, w);
+  dsa_issue_rows(st3, kvb, sidx, kbeg, kend, kbeg + 3 * kTile, drow, dchk, w);
+  if (ntiles > 0) {
+    wait_vmcnt<3 * kLatInstrMin>();
+    lds_barrier();
+    dsa_tile(st, qb, st0, kbeg, kend, sl2, lane, w);
+  }
+  if (ntiles > 1) {
+    wait_vmcnt<2 * kLatInstrMin>();
+    lds_barrier();
+    dsa_tile(st, qb, st1, kbeg + kTile, kend, sl2, lane, w);
+  }
+  if (ntiles > 2) {
+    wait_vmcnt<kLatInstrMin>();
+    lds_barrier();
+    dsa_tile(st, qb, st2, kbeg + 2 * kTile, kend, sl2, lane, w);
+  }
+  wait_vmcnt<0>();
+  if (ntiles > 3) {
+    lds_barrier();
+    dsa_tile(st, qb, st3, kbeg + 3 * kTile, kend, sl2, lane, w);
   }
 }
 
 template <class V>
 __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
-  __shared__ __attribute__((aligned(16))) char st0[kLatStageBytes], st1[kLatStageBytes], st2[kLatStageBytes];
+  __shared__ __attribute__((aligned(16))) char st0[kLatStageBytes], st1[kLatStageBytes], st2[kLatStageBytes],
+      st3[kLatStageBytes];
   __shared__ int sidx[kChunk];
   const int item = blockIdx.x;                  // (b * 4 + hb) * kNChunk + chunk
   const int chunk = item % kNChunk;
   const int hb = (item / kNChunk) % 4;
   const int b = item / (kNChunk * 4);
-  const int cnt = min(a.cnt[b], kTopK);
   const int kbeg = chunk * kChunk;
-  if (kbeg >= cnt) return;                      // whole workgroup
-  const int kend = min(cnt, kbeg + kChunk);
+  // The chunk's selected positions: idx holds kTopK entries per request, so every thread loads one without waiting
+  // for the count (entries past it are masked below), and the Q loads are issued before the positions are used.
+  // No branch depends on the count before the loads are issued: a chunk past it (lens, or L < kTopK) runs with no
+  // tiles and writes an empty partial, which the combine does not read.
+  const int* ip = a.idx + (size_t)b * kTopK;
+  const int sel = ip[kbeg + (int)(threadIdx.x & (kChunk - 1))];
+  const int cnt = min(a.cnt[b], kTopK);
+  const int kend = max(kbeg, min(cnt, kbeg + kChunk));
   const int ntiles = (kend - kbeg + kTile - 1) / kTile;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 31, g = lane >> 5;
-
-  // The chunk's selected positions, clamped into the cache.
-  const int* ip = a.idx + (size_t)b * kTopK;
-  if (threadIdx.x < kChunk) sidx[threadIdx.x] = min(max(ip[min(kbeg + (int)threadIdx.x, kend - 1)], 0), a.L - 1);
 
   // Q^T operand of k-step c: head r's dims 16c + 8g .. 16c + 8g + 7 (chunk 2c + g of the query row).
   const f16* qrow = a.q + ((size_t)b * kH + hb * 32 + r) * kDK;
   V qb[36];
 #pragma unroll
   for (int c = 0; c < 36; ++c) qb[c] = as_v8<V>(ld16(qrow + 16 * c + 8 * g));
+
+  // Clamped into the cache; keys past kend read the zero row whatever their entry holds.
+  // Threads t and t + kChunk store the same value.
+  sidx[threadIdx.x & (kChunk - 1)] = min(max(sel, 0), a.L - 1);
 
   // This wave's DMA instructions j = w + 4q: the (row, chunk) its lane fetches for each.
   int drow[10], dchk[10];
@@ -587,11 +604,11 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
     drow[q] = rr < kTile ? rr : kTile - 1;
     dchk[q] = (rr < kTile && cc < kLatChunks) ? cc : 0;
   }
-  __syncthreads();                              // sidx
+  lds_barrier();                                // sidx; waits for LDS only, the Q loads stay in flight
   const f16* kvb = a.kv + (size_t)b * a.L * kDK;
   RowState st;
   row_state_init(st);
-  dsa_ring_walk(st0, st1, st2, st, qb, kvb, sidx, kbeg, kend, ntiles, drow, dchk, a.sl2, lane, w);
+  dsa_chunk_walk(st0, st1, st2, st3, st, qb, kvb, sidx, kbeg, kend, ntiles, drow, dchk, a.sl2, lane, w);
   // Partial: O[head][128w + d'] for this wave's value dims; m and l are identical in all waves.
   float* po = a.po + (size_t)item * 32 * kDC;
   const float ltot = st.l + xor32(st.l);
