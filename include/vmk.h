@@ -136,7 +136,9 @@ int vmk_dsa_decode_bf16(const void* q, const void* kv, const void* iq, const voi
  *                                increasing position order.  With n <= 2048 valid positions, idx = 0..n-1.
  *   cnt   (B,)           int32   min(n, 2048)
  *   out   (B, 128, 512)  fp16
- * score[l] = sum_h w[h] * max(iq[h] . ik[l], 0) in fp32; attention scale 1/sqrt(192). */
+ * score[l] = sum_h w[h] * max(iq[h] . ik[l], 0) in fp32; attention scale 1/sqrt(192).
+ * Limits: L <= 4194304 (indexer/select); the attention entries also need L * 1152 bytes < 2 GiB per request
+ * (L <= 1864134), since the row gather addresses a request's cache by 32-bit offsets. */
 size_t vmk_dsa_workspace_size(int64_t B, int64_t L);
 /* Indexer + exact top-2048 only (the reference's indexer_mpp/indexer_float + select, dsa_opus55_v7.py:963-973). */
 int vmk_dsa_indexer_select(const void* iq, const void* ik, const void* w, const void* lens, void* idx, void* cnt,

@@ -426,50 +426,67 @@ __global__ __launch_bounds__(1024) void dsa_hist_zero_kernel(DsaArgs a) {
 // Workgroup = (request b, block of 32 heads, chunk of 128 selected keys); 4 waves.  Every wave computes the full
 // S^T tile (all 576 QK dims, in the same order, so all four hold bit-identical scores, softmax state and P) and owns
 // the value dims [128w, 128w+128) of O.
-// The selected latent rows of the chunk's four 32-key tiles are gathered by direct-to-LDS loads into four stages,
-// all issued before the first tile is computed, so the chunk waits for one gather round trip.  In a stage, row r
-// starts at byte r * kLatStride: 1152 bytes of the row plus 16 of padding, so the 73-chunk stride is odd and 16
-// consecutive rows at one chunk fall on 16 distinct bank groups (conflict-free K-operand reads).  DMA instruction j
-// (0 <= j < 37, wave j % 4 issues it) fills stage bytes [1024j, 1024j + 1024): lane i's 16 bytes go to slot 64j + i,
-// which is chunk (slot % 73) of row (slot / 73); padding slots and slots past the 32 rows take copies of real chunks.
-// V^T is read from the same rows with the transposing LDS read.
+// The selected latent rows of the chunk's four 32-key tiles are gathered by direct-to-LDS buffer loads into four
+// stages, all issued before the first tile is computed, so the chunk waits for one gather round trip.  In a stage,
+// row r starts at byte r * kLatStride: 1152 bytes of the row plus 16 of padding, so the 73-chunk stride is odd and
+// 16 consecutive rows at one chunk fall on 16 distinct bank groups (conflict-free K-operand reads).  DMA block j
+// (0 <= j < 37) fills stage bytes [1024j, 1024j + 1024): lane i's 16 bytes go to slot 64j + i, which is chunk
+// (slot % 73) of row (slot / 73); padding slots and slots past the 32 rows take copies of real chunks.  Wave w
+// fills blocks w + 4q (q < 9) and all four waves fill block 36 with the same bytes, so every wave issues exactly
+// kLatPerWave loads per tile.  V^T is read from the same rows with the transposing LDS read.
 constexpr int kSSlot = 16 * 64;          // floats of one wave's partial S^T tile
 constexpr int kLatChunks = kDK / 8;      // 72 chunks of 16 bytes per latent row
 constexpr int kLatStride = (kLatChunks + 1) * 16;           // 1168 bytes
-constexpr int kLatInstr = 37;            // DMA instructions per tile (>= 32 * 73 / 64 slots): 10 for wave 0, 9 others
-constexpr int kLatInstrMin = kLatInstr / 4;                 // the fewest any wave issues per tile
+constexpr int kLatInstr = 37;            // DMA blocks per tile (>= 32 * 73 / 64 slots)
+constexpr int kLatPerWave = 10;          // DMA loads per wave and tile
 constexpr int kLatStageBytes = kLatInstr * 1024;
 constexpr int kLatStages = kChunk / kTile;                  // one stage per tile of the chunk
-static_assert(kLatInstr * 64 >= kTile * (kLatChunks + 1), "a stage holds 32 padded rows");
+static_assert(kLatInstr * 64 >= kTile * (kLatChunks + 1) && kLatInstr == 4 * (kLatPerWave - 1) + 1,
+              "a stage holds 32 padded rows; block 36 is shared");
+// The gather addresses a request's rows by 32-bit offsets from one buffer resource, and an offset of 2^31 (past
+// every row) reads zeros: the source of every key past the selected count.
+constexpr int64_t kMaxAttnL = ((int64_t)1 << 31) / (kDK * 2) - 1;
+constexpr uint32_t kZeroOffset = 0x80000000u;
 
-// Zero latent row: the source of every key past the selected count.
-__device__ const f16 g_zero_latent[kDK] = {};
+__device__ __forceinline__ int lat_block(int w, int q) { return q < kLatPerWave - 1 ? w + 4 * q : kLatInstr - 1; }
 
-// The DMA instructions j = w + 4q < kLatInstr of wave w for the tile at key0.  The selected positions are read
-// from LDS first, all ten together, so the instructions issue back to back.
-__device__ __forceinline__ void dsa_issue_rows(char* __restrict__ stage, const f16* kvb, const int* __restrict__ sidx,
-                                               int kbeg, int kend, int key0, const int (&drow)[10],
-                                               const int (&dchk)[10], int w) {
-  int pos[10];
+// The kLatPerWave DMA loads of wave w for the tile at key0.  The selected positions are read from LDS first, all
+// ten together, so the loads issue back to back.
+__device__ __forceinline__ void dsa_issue_rows(char* __restrict__ stage, __amdgpu_buffer_rsrc_t rows,
+                                               const int* __restrict__ sidx, int kbeg, int kend, int key0,
+                                               const int (&drow)[10], const int (&dchk)[10], int w) {
+  int pos[kLatPerWave];
 #pragma unroll
-  for (int q = 0; q < 10; ++q) pos[q] = sidx[key0 - kbeg + drow[q]];     // < kChunk: key0 - kbeg <= 96, drow <= 31
+  for (int q = 0; q < kLatPerWave; ++q) pos[q] = sidx[key0 - kbeg + drow[q]];   // < kChunk: key0 - kbeg <= 96
 #pragma unroll
-  for (int q = 0; q < 10; ++q) {
-    if (w + 4 * q >= kLatInstr) break;                      // wave-uniform
-    const int key = key0 + drow[q];
-    const f16* row = key < kend ? kvb + (size_t)pos[q] * kDK : g_zero_latent;
-    __builtin_amdgcn_global_load_lds(VMK_GPTR(row + 8 * dchk[q]), VMK_LPTR(stage + (w + 4 * q) * 1024), 16, 0, 0);
+  for (int q = 0; q < kLatPerWave; ++q) {
+    const uint32_t off = key0 + drow[q] < kend ? (uint32_t)pos[q] * (kDK * 2) + 16 * dchk[q] : kZeroOffset;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rows, VMK_LPTR(stage + lat_block(w, q) * 1024), 16, off, 0, 0, 0);
   }
 }
 
 // S^T of the tile in stage over all 576 QK dims (36 MFMAs; the same order in every wave).
 template <class V>
 __device__ __forceinline__ floatx16 dsa_qk(const char* __restrict__ stage, const V (&qb)[36], int r, int g) {
+  // K operands are read from LDS one group of six ahead of their MFMAs (the scheduling barriers keep that order): a
+  // wave is alone on its SIMD, so nothing else hides the LDS latency.
   floatx16 s = floatx16{};
+  const char* kb = stage + r * kLatStride + g * 16;
+  u32x4 k[2][6];
 #pragma unroll
-  for (int c = 0; c < 36; ++c) {
-    const u32x4 k = *reinterpret_cast<const u32x4*>(stage + r * kLatStride + (2 * c + g) * 16);
-    s = mfma32(as_v8<V>(k), qb[c], s);
+  for (int j = 0; j < 6; ++j) k[0][j] = *reinterpret_cast<const u32x4*>(kb + 2 * j * 16);
+  __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+  for (int c0 = 0; c0 < 36; c0 += 6) {
+    const int cur = (c0 / 6) & 1;
+    if (c0 + 6 < 36) {
+#pragma unroll
+      for (int j = 0; j < 6; ++j) k[cur ^ 1][j] = *reinterpret_cast<const u32x4*>(kb + 2 * (c0 + 6 + j) * 16);
+      __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 6; ++j) s = mfma32(as_v8<V>(k[cur][j]), qb[c0 + j], s);
+    __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
   }
   return s;
 }
@@ -524,35 +541,36 @@ __device__ __forceinline__ void dsa_tile(RowState& st, const V (&qb)[36], const 
 }
 
 // Walk over the chunk's tiles: every tile has its own stage and all four are requested up front (rows past kend
-// read the zero row).  Before tile t a wave waits until at most kLatInstrMin * (3 - t) of its DMA instructions are
-// in flight, i.e. its part of tile t has landed (wave 0, with one more instruction per tile, waits slightly longer
-// than needed), and the barrier makes every wave's part visible.  The stages are separate LDS arrays and every LDS
+// read zeros).  Before tile t a wave waits until at most kLatPerWave * (3 - t) of its loads are in flight, i.e. its
+// part of tile t (and every older load, such as the Q operands) has landed, and the barrier makes every wave's part
+// visible.  The stages are separate LDS arrays and every LDS
 // array the walk touches is a restrict-qualified parameter, so the compiler can tell the stages apart (it would
 // otherwise wait for every load in flight before each LDS read).  The last wait drains every load, so no DMA is
 // still writing LDS when the workgroup ends.
 template <class V>
 __device__ __forceinline__ void dsa_chunk_walk(char* __restrict__ st0, char* __restrict__ st1, char* __restrict__ st2,
                                                char* __restrict__ st3, RowState& st, const V (&qb)[36],
-                                               const f16* kvb, const int* __restrict__ sidx, int kbeg, int kend,
+                                               __amdgpu_buffer_rsrc_t rows, const int* __restrict__ sidx, int kbeg,
+                                               int kend,
                                                int ntiles, const int (&drow)[10], const int (&dchk)[10], float sl2,
                                                int lane, int w) {
-  static_assert(kLatStages == 4 && 3 * kLatInstrMin < 64, "four stages, vmcnt range");
-  dsa_issue_rows(st0, kvb, sidx, kbeg, kend, kbeg, drow, dchk, w);
-  dsa_issue_rows(st1, kvb, sidx, kbeg, kend, kbeg + kTile, drow, dchk, w);
-  dsa_issue_rows(st2, kvb, sidx, kbeg, kend, kbeg + 2 * kTile, drow, dchk, w);
-  dsa_issue_rows(st3, kvb, sidx, kbeg, kend, kbeg + 3 * kTile, drow, dchk, w);
+  static_assert(kLatStages == 4 && 3 * kLatPerWave < 64, "four stages, vmcnt range");
+  dsa_issue_rows(st0, rows, sidx, kbeg, kend, kbeg, drow, dchk, w);
+  dsa_issue_rows(st1, rows, sidx, kbeg, kend, kbeg + kTile, drow, dchk, w);
+  dsa_issue_rows(st2, rows, sidx, kbeg, kend, kbeg + 2 * kTile, drow, dchk, w);
+  dsa_issue_rows(st3, rows, sidx, kbeg, kend, kbeg + 3 * kTile, drow, dchk, w);
   if (ntiles > 0) {
-    wait_vmcnt<3 * kLatInstrMin>();
+    wait_vmcnt<3 * kLatPerWave>();
     lds_barrier();
     dsa_tile(st, qb, st0, kbeg, kend, sl2, lane, w);
   }
   if (ntiles > 1) {
-    wait_vmcnt<2 * kLatInstrMin>();
+    wait_vmcnt<2 * kLatPerWave>();
     lds_barrier();
     dsa_tile(st, qb, st1, kbeg + kTile, kend, sl2, lane, w);
   }
   if (ntiles > 2) {
-    wait_vmcnt<kLatInstrMin>();
+    wait_vmcnt<kLatPerWave>();
     lds_barrier();
     dsa_tile(st, qb, st2, kbeg + 2 * kTile, kend, sl2, lane, w);
   }
@@ -574,9 +592,9 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   const int b = item / (kNChunk * 4);
   const int kbeg = chunk * kChunk;
   // The chunk's selected positions: idx holds kTopK entries per request, so every thread loads one without waiting
-  // for the count (entries past it are masked below), and the Q loads are issued before the positions are used.
-  // No branch depends on the count before the loads are issued: a chunk past it (lens, or L < kTopK) runs with no
-  // tiles and writes an empty partial, which the combine does not read.
+  // for the count (entries past it are masked below), and the Q loads are issued before the positions are used.  No
+  // branch depends on the count: a chunk past it (lens, or L < kTopK) runs no tiles and writes an empty partial,
+  // which the combine does not read.
   const int* ip = a.idx + (size_t)b * kTopK;
   const int sel = ip[kbeg + (int)(threadIdx.x & (kChunk - 1))];
   const int cnt = min(a.cnt[b], kTopK);
@@ -595,20 +613,21 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   // Threads t and t + kChunk store the same value.
   sidx[threadIdx.x & (kChunk - 1)] = min(max(sel, 0), a.L - 1);
 
-  // This wave's DMA instructions j = w + 4q: the (row, chunk) its lane fetches for each.
-  int drow[10], dchk[10];
+  // This wave's DMA loads q (block lat_block(w, q)): the (row, chunk) its lane fetches for each.
+  int drow[kLatPerWave], dchk[kLatPerWave];
 #pragma unroll
-  for (int q = 0; q < 10; ++q) {
-    const int slot = 64 * (w + 4 * q) + lane;
+  for (int q = 0; q < kLatPerWave; ++q) {
+    const int slot = 64 * lat_block(w, q) + lane;
     const int rr = slot / (kLatChunks + 1), cc = slot % (kLatChunks + 1);
     drow[q] = rr < kTile ? rr : kTile - 1;
     dchk[q] = (rr < kTile && cc < kLatChunks) ? cc : 0;
   }
   lds_barrier();                                // sidx; waits for LDS only, the Q loads stay in flight
-  const f16* kvb = a.kv + (size_t)b * a.L * kDK;
+  const __amdgpu_buffer_rsrc_t rows =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(a.kv + (size_t)b * a.L * kDK), 0, a.L * kDK * 2, 0x00020000);
   RowState st;
   row_state_init(st);
-  dsa_chunk_walk(st0, st1, st2, st3, st, qb, kvb, sidx, kbeg, kend, ntiles, drow, dchk, a.sl2, lane, w);
+  dsa_chunk_walk(st0, st1, st2, st3, st, qb, rows, sidx, kbeg, kend, ntiles, drow, dchk, a.sl2, lane, w);
   // Partial: O[head][128w + d'] for this wave's value dims; m and l are identical in all waves.
   float* po = a.po + (size_t)item * 32 * kDC;
   const float ltot = st.l + xor32(st.l);
@@ -767,6 +786,7 @@ static int dsa_sparse_mla(const void* q, const void* kv, const void* idx, const 
   VMK_CHECK(q && kv && idx && cnt && out, "null pointer argument");
   DSA_COMMON_CHECKS();
   VMK_CHECK(aligned16(q) && aligned16(kv), "q/kv must be 16-byte aligned");
+  VMK_CHECK(L <= kMaxAttnL, "sparse attention needs L * 1152 bytes < 2 GiB per request (L <= 1864134)");
   DsaArgs a;
   dsa_fill_args(a, q, kv, nullptr, nullptr, nullptr, nullptr, out, (void*)idx, (void*)cnt, B, L, workspace);
   return launch_attention<V>(a, (hipStream_t)stream);
@@ -779,6 +799,7 @@ static int dsa_decode(const void* q, const void* kv, const void* iq, const void*
   VMK_CHECK(q && kv && iq && ik && w && out && idx && cnt, "null pointer argument");
   DSA_COMMON_CHECKS();
   VMK_CHECK(aligned16(q) && aligned16(kv) && aligned16(iq) && aligned16(ik), "tensors must be 16-byte aligned");
+  VMK_CHECK(L <= kMaxAttnL, "sparse attention needs L * 1152 bytes < 2 GiB per request (L <= 1864134)");
   DsaArgs a;
   dsa_fill_args(a, q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace);
   hipStream_t s = (hipStream_t)stream;
