@@ -533,8 +533,69 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
 // part(i, ml, o) sets ml -> (m, l) and o -> the partial's O row of partial i (0 <= i < nparts).  The m/l of a batch
 // of NT partials are fetched in parallel and their weights shared through LDS, so that the O loads of the
 // accumulation loop are independent of each other and can all be in flight together.
+//
+// Up to 32 partials (every bench shape: 8-32), the O rows are loaded into registers together with the m/l, before
+// the maximum is known, so the merge waits for one round of loads instead of three.  The H loads are unconditional
+// (slots past nparts reload the last partial, never used) so that they issue back to back.  Both forms add the same
+// terms in the same order (partial 0 first), so they give the same bits.
+template <int NT, int PER, int H, class Part, class E>
+__device__ __forceinline__ void combine_row_held(int nparts, Part part, E* out) {
+  __shared__ float sw[H], sl[H], red[NT / 64];
+  const int tid = threadIdx.x;
+  float ov[H][PER];
+#pragma unroll
+  for (int j = 0; j < H; ++j) {
+    const float* ml;
+    const float* o;
+    part(min(j, nparts - 1), ml, o);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) ov[j][k] = o[tid + k * NT];
+  }
+  float m0 = kNegInf, l0 = 0.f;
+  if (tid < nparts) {
+    const float* ml;
+    const float* o;
+    part(tid, ml, o);
+    m0 = ml[0];
+    l0 = ml[1];
+  }
+  float M = m0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = M;
+  __syncthreads();
+  M = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) M = fmaxf(M, red[w]);
+  const float Muse = (M == kNegInf) ? 0.f : M;
+  if (tid < nparts) {
+    const float w = fast_exp2(m0 - Muse);
+    sw[tid] = w;
+    sl[tid] = w * l0;
+  }
+  __syncthreads();
+  float num[PER], den = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) num[k] = 0.f;
+#pragma unroll
+  for (int j = 0; j < H; ++j) {
+    if (j < nparts) {                                  // uniform
+      const float w = sw[j];
+      den += sl[j];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) num[k] += w * ov[j][k];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) out[tid + k * NT] = (E)(num[k] / den);
+}
+
 template <int NT, int PER, class Part, class E>
 __device__ __forceinline__ void combine_row(int nparts, Part part, E* out) {
+  static_assert(NT >= 32, "one thread per held partial's m/l");
+  if (nparts <= 8) return combine_row_held<NT, PER, 8>(nparts, part, out);
+  if (nparts <= 16) return combine_row_held<NT, PER, 16>(nparts, part, out);
+  if (nparts <= 32) return combine_row_held<NT, PER, 32>(nparts, part, out);
   __shared__ float sw[NT], sl[NT], red[NT / 64];
   const int tid = threadIdx.x;
   float M = kNegInf;
