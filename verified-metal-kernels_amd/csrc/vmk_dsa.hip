@@ -322,19 +322,86 @@ __device__ __forceinline__ int slice_of(const uint32_t* off, int ns, uint32_t e)
   return lo;
 }
 
+// Requests with n <= kTopK valid positions select all of them (idx = 0..n-1).  When the indexer ran, its histograms
+// are left zero for the next call.
+__device__ __forceinline__ void select_all(const DsaArgs& a, int b, int n, int* idx, uint32_t* gh) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kTopK; i += 1024) idx[i] = i < n ? i : 0;
+  if (a.L > kTopK) {
+    for (int i = tid; i < kBins; i += 1024) gh[i] = 0;
+    if (tid < kCBins) a.chist[(size_t)b * kCBins + tid] = 0;
+  }
+  if (tid == 0) a.cnt[b] = n;
+}
+
+// The common tail of both select forms.  The n_gt positions above the threshold bucket b1 are in idx[0, n_gt); the
+// bucket's ncand candidates are in position order, in LDS (in_lds) or read by gcand(c, key, pos).  Refines the bucket
+// to the exact threshold key T by the second and third radix digits, then writes the keys above T and the first
+// need_eq keys equal to T (position order) after the n_gt, and leaves the histograms zero for the next call.
+template <class GCand>
+__device__ __forceinline__ void select_refine(const DsaArgs& a, SelectShared& sh, int b, int* idx, uint32_t n_gt,
+                                              uint32_t ncand, bool in_lds, uint32_t b1, GCand gcand) {
+  const int tid = threadIdx.x;
+  uint32_t need = kTopK - n_gt;                      // picks still to make from the bucket (>= 1)
+  // Candidate walk over thread-contiguous ranges of the ordered candidate list.
+  const int cper = (int)((ncand + 1023) / 1024);
+  const int c_lo = min((int)ncand, tid * cper), c_hi = min((int)ncand, c_lo + cper);
+  auto for_each = [&](auto&& f) {
+    for (int c = c_lo; c < c_hi; ++c) {
+      if (in_lds) {
+        f(sh.cand_key[c], sh.cand_pos[c]);
+      } else {
+        uint32_t key;
+        int pos;
+        gcand(c, key, pos);
+        f(key, pos);
+      }
+    }
+  };
+  for (int i = tid; i < 2048; i += 1024) sh.hist[i] = 0;
+  __syncthreads();
+  for_each([&](uint32_t key, int) { atomicAdd(&sh.hist[(key >> 8) & 0x7FF], 1u); });
+  __syncthreads();
+  find_threshold<1024>(sh.hist, 2048, need, sh.red, sh.thr);
+  const uint32_t b2 = sh.thr[0];
+  need = sh.thr[1];
+  sh.hist[tid] = 0;
+  __syncthreads();
+  for_each([&](uint32_t key, int) {
+    if (((key >> 8) & 0x7FF) == b2) atomicAdd(&sh.hist[key & 0xFF], 1u);
+  });
+  __syncthreads();
+  find_threshold<1024>(sh.hist, 1024, need, sh.red, sh.thr);
+  const uint32_t T = (b1 << 19) | (b2 << 8) | sh.thr[0];
+  const uint32_t need_eq = sh.thr[1];
+  // Bucket picks: keys above T, then the first need_eq keys equal to T in position order.
+  uint32_t c_above = 0, c_tie = 0, above_total, tie_total;
+  for_each([&](uint32_t key, int) { c_above += key > T; c_tie += key == T; });
+  uint32_t o_above = block_excl_scan<1024>(c_above, sh.red, &above_total);
+  uint32_t o_tie = block_excl_scan<1024>(c_tie, sh.red, &tie_total);
+  for_each([&](uint32_t key, int p) {
+    if (key > T) {
+      const uint32_t slot = n_gt + o_above++;
+      if (slot < (uint32_t)kTopK) idx[slot] = p;
+    } else if (key == T) {
+      const uint32_t slot = n_gt + above_total + o_tie;
+      if (o_tie < need_eq && slot < (uint32_t)kTopK) idx[slot] = p;
+      ++o_tie;
+    }
+  });
+  uint32_t* gh = a.hist + (size_t)b * kBins;
+  for (int i = tid; i < kBins; i += 1024) gh[i] = 0;               // leave the histograms zero for the next call
+  if (tid < kCBins) a.chist[(size_t)b * kCBins + tid] = 0;
+  if (tid == 0) a.cnt[b] = kTopK;
+}
+
 __global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
   __shared__ SelectShared sh;
   const int b = blockIdx.x, tid = threadIdx.x;
   const int n = valid_len(a, b);
   int* idx = a.idx + (size_t)b * kTopK;
-  uint32_t* gh = a.hist + (size_t)b * kBins;
   if (n <= kTopK) {
-    for (int i = tid; i < kTopK; i += 1024) idx[i] = i < n ? i : 0;
-    if (a.L > kTopK) {                                      // the indexer ran: leave the histograms zero
-      for (int i = tid; i < kBins; i += 1024) gh[i] = 0;
-      if (tid < kCBins) a.chist[(size_t)b * kCBins + tid] = 0;
-    }
-    if (tid == 0) a.cnt[b] = n;
+    select_all(a, b, n, idx, a.hist + (size_t)b * kBins);
     return;
   }
   const int ns = (n + kScanWG - 1) / kScanWG;
@@ -353,7 +420,6 @@ __global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
     const int sl = slice_of(sh.goff, ns, s);
     idx[s] = glb[sl * kScanWG + (s - sh.goff[sl])];
   }
-  uint32_t need = kTopK - n_gt;                      // picks still to make from the bucket (>= 1)
   const uint32_t* ekb = a.ekey + (size_t)b * a.Ls;
   const int* epb = a.epos + (size_t)b * a.Ls;
   const bool in_lds = ncand <= (uint32_t)kCand;
@@ -363,56 +429,19 @@ __global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
       sh.cand_key[c] = ekb[sl * kScanWG + (c - sh.eoff[sl])];
       sh.cand_pos[c] = epb[sl * kScanWG + (c - sh.eoff[sl])];
     }
-  // Candidate walk over thread-contiguous ranges of the ordered candidate list (LDS, or global when too many ties).
-  const int cper = (int)((ncand + 1023) / 1024);
-  const int c_lo = min((int)ncand, tid * cper), c_hi = min((int)ncand, c_lo + cper);
-  auto for_each = [&](auto&& f) {
-    for (int c = c_lo; c < c_hi; ++c) {
-      if (in_lds) {
-        f(sh.cand_key[c], sh.cand_pos[c]);
-      } else {
-        const int sl = slice_of(sh.eoff, ns, (uint32_t)c);
-        const size_t o = (size_t)sl * kScanWG + (c - sh.eoff[sl]);
-        f(ekb[o], epb[o]);
-      }
-    }
+  auto gcand = [&](int c, uint32_t& key, int& pos) {
+    const int sl = slice_of(sh.eoff, ns, (uint32_t)c);
+    const size_t o = (size_t)sl * kScanWG + (c - sh.eoff[sl]);
+    key = ekb[o];
+    pos = epb[o];
   };
-  for (int i = tid; i < 2048; i += 1024) sh.hist[i] = 0;
-  __syncthreads();
-  for_each([&](uint32_t key, int) { atomicAdd(&sh.hist[(key >> 8) & 0x7FF], 1u); });
-  __syncthreads();
-  find_threshold<1024>(sh.hist, 2048, need, sh.red, sh.thr);
-  const uint32_t b2 = sh.thr[0];
-  need = sh.thr[1];
-  sh.hist[tid] = 0;
-  __syncthreads();
-  for_each([&](uint32_t key, int) {
-    if (((key >> 8) & 0x7FF) == b2) atomicAdd(&sh.hist[key & 0xFF], 1u);
-  });
-  __syncthreads();
-  find_threshold<1024>(sh.hist, 1024, need, sh.red, sh.thr);
-  const int sl0 = slice_of(sh.eoff, ns, 0);                        // the bucket is non-empty: need >= 1 of it
-  const uint32_t b1 = ekb[(size_t)sl0 * kScanWG] >> 19;
-  const uint32_t T = (b1 << 19) | (b2 << 8) | sh.thr[0];
-  const uint32_t need_eq = sh.thr[1];
-  // Bucket picks: keys above T, then the first need_eq keys equal to T in position order.
-  uint32_t c_above = 0, c_tie = 0, above_total, tie_total;
-  for_each([&](uint32_t key, int) { c_above += key > T; c_tie += key == T; });
-  uint32_t o_above = block_excl_scan<1024>(c_above, sh.red, &above_total);
-  uint32_t o_tie = block_excl_scan<1024>(c_tie, sh.red, &tie_total);
-  for_each([&](uint32_t key, int p) {
-    if (key > T) {
-      const uint32_t slot = n_gt + o_above++;
-      if (slot < (uint32_t)kTopK) idx[slot] = p;
-    } else if (key == T) {
-      const uint32_t slot = n_gt + above_total + o_tie;
-      if (o_tie < need_eq && slot < (uint32_t)kTopK) idx[slot] = p;
-      ++o_tie;
-    }
-  });
-  for (int i = tid; i < kBins; i += 1024) gh[i] = 0;               // leave the histograms zero for the next call
-  if (tid < kCBins) a.chist[(size_t)b * kCBins + tid] = 0;
-  if (tid == 0) a.cnt[b] = kTopK;
+  __syncthreads();                                   // the candidates in LDS
+  // b1 from the first candidate (the bucket is non-empty: need >= 1 of it).
+  uint32_t key0;
+  int pos0;
+  if (in_lds) key0 = sh.cand_key[0];
+  else gcand(0, key0, pos0);
+  select_refine(a, sh, b, idx, n_gt, ncand, in_lds, key0 >> 19, gcand);
 }
 
 // Zero-fills the per-request histograms before the indexer accumulates into them (when they are not in the head).
