@@ -85,6 +85,14 @@ def test_entry_points_reject_before_launch(lib):
     assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
     rc = lib.vmk_dsa_decode(fake, fake, fake, fake, None, None, fake, fake, fake, 2, 5000, fake, 1 << 30, None)
     assert rc == 1 and b"null pointer" in lib.vmk_last_error()
+    # The sparse attention addresses a request's latent rows by 32-bit offsets: L * 1152 bytes must stay < 2 GiB.
+    big = 1864135
+    ws = lib.vmk_dsa_workspace_size(1, big)
+    assert ws > 0
+    rc = lib.vmk_dsa_sparse_mla(fake, fake, fake, fake, fake, 1, big, fake, ws, None)
+    assert rc == 1 and b"L <= 1864134" in lib.vmk_last_error()
+    rc = lib.vmk_dsa_decode(fake, fake, fake, fake, fake, None, fake, fake, fake, 1, big, fake, ws, None)
+    assert rc == 1 and b"L <= 1864134" in lib.vmk_last_error()
 
 
 def test_python_wrappers_validate_shapes_without_gpu():
