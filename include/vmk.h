@@ -164,6 +164,10 @@ int vmk_profile_next(void* before_event, void* after_event, int kernel_id);
 int vmk_debug_mfma32(const void* a, const void* b, void* d, void* stream);
 int vmk_debug_tile(const void* q, const void* k, const void* v, void* s, void* vt, void* o, void* ml, float sl2,
                    void* stream);
+/* Host-only replay (no GPU work) of the DSA select's threshold-bucket search, with the kernels' own bin arithmetic:
+ * coarse_hist (256) and fine_hist (8192) counts in host memory, need = picks (2048) -> out[0] coarse bin, out[1]
+ * picks left in it, out[2] fine bucket.  Every bin it returns is inside the histograms, whatever the counts. */
+int vmk_debug_select_threshold(const uint32_t* coarse_hist, const uint32_t* fine_hist, uint32_t need, uint32_t* out);
 
 #ifdef __cplusplus
 }

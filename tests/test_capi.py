@@ -5,6 +5,7 @@ import os
 import re
 import subprocess
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -122,3 +123,95 @@ def test_bf16_reaches_the_bf16_entry_points():
     iq, ik = torch.zeros(1, 64, 128, dtype=torch.bfloat16), torch.zeros(1, 2100, 128, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="ROCm device"):
         dsa_mi355x.kernel(y[:, :128], y, iq, ik, torch.zeros(1, 64), None)
+
+
+def test_dsa_wrappers_check_every_shape_before_the_device():
+    """Wrongly shaped DSA arguments are refused on the host (here CPU tensors, so nothing reaches a GPU): the
+    attention's q/kv/idx/cnt and the indexer's lens length."""
+    import torch
+    import vmk
+    B, L = 2, 3000
+    f16 = dict(dtype=torch.float16)
+    q, kv = torch.zeros(B, 128, 576, **f16), torch.zeros(B, L, 576, **f16)
+    iq, ik, w = torch.zeros(B, 64, 128, **f16), torch.zeros(B, L, 128, **f16), torch.zeros(B, 64)
+    idx, cnt = torch.zeros(B, 2048, dtype=torch.int32), torch.zeros(B, dtype=torch.int32)
+    bad = [
+        (vmk.dsa_sparse_mla, (torch.zeros(B, 128, 512, **f16), kv, idx, cnt), "q"),
+        (vmk.dsa_sparse_mla, (q, torch.zeros(B, L, 512, **f16), idx, cnt), "kv"),
+        (vmk.dsa_sparse_mla, (q, torch.zeros(B + 1, L, 576, **f16), idx, cnt), "kv"),
+        (vmk.dsa_sparse_mla, (q, kv, torch.zeros(B, 1024, dtype=torch.int32), cnt), "idx"),
+        (vmk.dsa_sparse_mla, (q, kv, idx, torch.zeros(B + 1, dtype=torch.int32)), "cnt"),
+        (vmk.dsa_indexer_select, (iq, ik, w, torch.ones(B + 1, dtype=torch.int32)), "lens"),
+        (vmk.dsa_indexer_select, (iq, torch.zeros(B, L, 64, **f16), w), "ik"),
+        (vmk.dsa_decode, (q, torch.zeros(B, L + 1, 576, **f16), iq, ik, w), "positions"),
+        (vmk.dsa_decode, (q, kv, iq, ik, w, torch.ones(1, dtype=torch.int32)), "lens"),
+    ]
+    for fn, args, needle in bad:
+        with pytest.raises(ValueError, match=needle):
+            fn(*args)
+    with pytest.raises(ValueError, match="ROCm device"):        # well-formed: only the device check is left
+        vmk.dsa_sparse_mla(q, kv, idx, cnt)
+    with pytest.raises(TypeError, match="share one dtype"):
+        vmk.dsa_decode(q, kv, iq.bfloat16(), ik.bfloat16(), w)
+
+
+def test_failed_call_sets_the_workspace_aside(monkeypatch):
+    """A call that fails leaves the cached workspace retired (kept alive, not reused): the next call gets a fresh,
+    zeroed one.  Forced on the CPU by a failing stand-in for the library call."""
+    import torch
+    from vmk import api, lib
+    buf = torch.zeros(16, dtype=torch.uint8)
+    monkeypatch.setitem(api._ws, buf.device.index, buf)
+    monkeypatch.setattr(api, "_retired", [])
+
+    def fail(*a):
+        raise lib.VmkError("launch failed")
+    monkeypatch.setattr(lib, "call", fail)
+    with pytest.raises(lib.VmkError):
+        api._launch("vmk_spec_verify", buf)
+    assert buf.device.index not in api._ws and api._retired == [buf]
+
+
+def _select_threshold(coarse, fine, need=2048):
+    import ctypes
+    from vmk import lib
+    c = np.ascontiguousarray(coarse, dtype=np.uint32)
+    f = np.ascontiguousarray(fine, dtype=np.uint32)
+    out = np.zeros(3, dtype=np.uint32)
+    lib.call("vmk_debug_select_threshold", c.ctypes.data_as(ctypes.c_void_p), f.ctypes.data_as(ctypes.c_void_p),
+             need, out.ctypes.data_as(ctypes.c_void_p))
+    return [int(x) for x in out]
+
+
+def test_select_threshold_arithmetic_on_consistent_histograms():
+    """The select kernels' bin arithmetic, replayed on the host: for histograms of real score keys the fine bucket
+    holds the 2048th largest key, and the coarse result agrees with it."""
+    rng = np.random.default_rng(3)
+    for trial in range(40):
+        n = int(rng.integers(2049, 200000))
+        keys = rng.integers(0, 1 << 32, n, dtype=np.uint64) if trial % 2 else \
+            (0x80000000 + rng.normal(0, 2 ** 24 * (1 + trial), n).astype(np.int64)).astype(np.uint64) % (1 << 32)
+        fine = np.bincount((keys >> 19).astype(np.int64), minlength=8192).astype(np.uint32)
+        coarse = fine.reshape(256, 32).sum(1).astype(np.uint32)
+        c, rest, b1 = _select_threshold(coarse, fine)
+        kth = np.sort(keys)[::-1][2047]
+        assert b1 == int(kth >> 19) and c == b1 >> 5
+        assert rest == 2048 - int(coarse[c + 1:].sum())
+
+
+def test_select_threshold_stays_in_range_on_inconsistent_histograms():
+    """An empty histogram, fewer than 2048 counts, coarse counts with no fine counts under them, and random garbage
+    (sums that wrap): every bin returned lies inside the histograms, so the kernels never address outside them."""
+    rng = np.random.default_rng(4)
+    cases = [(np.zeros(256), np.zeros(8192)),
+             (np.full(256, 7), np.zeros(8192)),
+             (np.eye(1, 256, 200).ravel() * 5000, np.zeros(8192)),
+             (np.zeros(256), np.full(8192, 9))]
+    cases += [(rng.integers(0, 1 << 32, 256, dtype=np.uint64), rng.integers(0, 1 << 32, 8192, dtype=np.uint64))
+              for _ in range(200)]
+    cases += [(rng.integers(0, 40, 256), rng.integers(0, 3, 8192)) for _ in range(200)]
+    for coarse, fine in cases:
+        for need in (1, 2048, 0xFFFFFFFF):
+            c, rest, b1 = _select_threshold(coarse, fine, need)
+            assert 0 <= c < 256 and 0 <= b1 < 8192
+    assert _select_threshold(np.zeros(256), np.zeros(8192)) == [0, 0, 0]

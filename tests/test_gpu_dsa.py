@@ -4,7 +4,7 @@ import pytest
 import torch
 
 import oracle
-from judge import nerr, same_pattern
+from judge import normalised_error as nerr, same_nonfinite as same_pattern
 from vmk.ops import dsa
 
 pytestmark = pytest.mark.gpu
@@ -51,3 +51,78 @@ def test_dsa_kernel_module_matches_entry_points():
     o2 = vmk.dsa_sparse_mla(inp["q"], inp["kv"], idx, cnt)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+def tied_inputs(L, n_high, n_tied, seed):
+    """DSA inputs whose indexer scores take three values: n_high positions at 2 s, n_tied at exactly s (identical
+    ik rows give identical fp32 scores), the rest at 0 (ik = 0).  With n_high < 2048 < n_high + n_tied, the
+    threshold bucket holds the n_tied exact ties, and the select must take the first 2048 - n_high of them in
+    position order.  Returns (inputs, expected index set)."""
+    B = 2
+    inp = dsa.make_inputs(dict(B=B, L=L), seed=seed, dist="randn")
+    rng = np.random.default_rng(seed + 1)
+    ik = np.zeros((B, L, dsa.DI), dtype=np.float32)
+    want = []
+    for b in range(B):
+        iq = inp["iq"][b].float().numpy()
+        w = inp["w"][b].numpy()
+        base = (iq * np.sign(w)[:, None]).mean(0) * 8.0
+        s = float((w * np.maximum(iq.astype(np.float64) @ base.astype(np.float16).astype(np.float64), 0)).sum())
+        assert s > 0
+        perm = rng.permutation(L)
+        high, tied = np.sort(perm[:n_high]), np.sort(perm[n_high:n_high + n_tied])
+        ik[b, tied] = base
+        ik[b, high] = 2.0 * base
+        want.append(np.concatenate([high, tied[:dsa.TOPK - n_high]]))
+    inp["ik"] = torch.from_numpy(ik).half()
+    return inp, want
+
+
+@pytest.mark.parametrize("L,n_high,n_tied", [(16384, 1000, 3000), (16384, 1000, 15384), (70000, 7, 50000)])
+def test_dsa_select_exact_ties_broken_by_position(L, n_high, n_tied):
+    """More than 4096 tied candidates take the select's global-memory walk; up to 4096 stay in LDS.  Either way the
+    picks among equal scores are the lowest positions, and the attention over them matches float64."""
+    import vmk
+    print(f"dsa ties L={L} high={n_high} tied={n_tied}", flush=True)
+    inp, want = tied_inputs(L, n_high, n_tied, seed=11)
+    inp = {k: (v.cuda() if v is not None else None) for k, v in inp.items()}
+    idx = torch.full((2, 2048), -1, dtype=torch.int32, device="cuda")
+    cnt = torch.full((2,), -1, dtype=torch.int32, device="cuda")
+    out = vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], None, idx=idx, cnt=cnt)
+    torch.cuda.synchronize()
+    idx, cnt = idx.cpu().numpy(), cnt.cpu().numpy()
+    s64, _ = oracle.dsa.ref_select64(inp["iq"], inp["ik"], inp["w"], None)
+    sel = []
+    for b in range(2):
+        assert cnt[b] == 2048
+        ok, det = oracle.dsa.topk_set_check(idx[b], 2048, s64[b], L)
+        assert ok and det["boundary"] == n_tied, det
+        assert np.array_equal(np.sort(idx[b]), np.sort(want[b]))
+        sel.append(idx[b].astype(np.int64))
+    r = oracle.dsa.ref64(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], sel=sel)
+    em, _ = nerr(out.float().cpu().numpy(), r)
+    assert em <= 1e-2
+    again = vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], None)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)                    # the histograms were left zero by the first call
+
+
+def test_dsa_batch_above_64_keeps_histograms_outside_the_head():
+    """B > 64 moves the per-request histograms out of the workspace head and zero-fills them first; two calls in a
+    row must both select exactly."""
+    import vmk
+    shape = dict(B=65, L=2500)
+    print(f"dsa {shape}", flush=True)
+    for seed in (21, 22):
+        inp = dsa.make_inputs(shape, seed=seed, dist="randn", device="cuda")
+        idx = torch.full((65, 2048), -1, dtype=torch.int32, device="cuda")
+        cnt = torch.full((65,), -1, dtype=torch.int32, device="cuda")
+        out = vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], None, idx=idx, cnt=cnt)
+        torch.cuda.synchronize()
+        s64, sel = oracle.dsa.ref_select64(inp["iq"], inp["ik"], inp["w"], None)
+        idx, cnt = idx.cpu().numpy(), cnt.cpu().numpy()
+        for b in range(65):
+            ok, det = oracle.dsa.topk_set_check(idx[b], int(cnt[b]), s64[b], 2500)
+            assert ok, (seed, b, det)
+        em, _ = nerr(out.float().cpu().numpy(), oracle.dsa.ref64(**inp, sel=sel))
+        assert em <= 1e-2

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle
-from judge import nerr, same_pattern
+from judge import normalised_error as nerr, same_nonfinite as same_pattern
 from vmk.ops import prefix, prefix_paged
 
 pytestmark = pytest.mark.gpu

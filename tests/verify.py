@@ -1,34 +1,44 @@
-"""Three-layer verifier for one kernel module (the counterpart of the reference's verify.py, with a PyTorch-ROCm
-adapter): the standard op of L1/L3 is a PyTorch SDPA composition on the GPU where the reference used MLX, and
-L2/L3 keep judging against the NumPy float64 oracle.
+"""Judge one kernel module of an op: is it CORRECT on every case of the op's case plan, or REJECTED?
 
-    python tests/verify.py verified-metal-kernels_amd/kernels/spec_mi355x.py          # op from the file name
+    python tests/verify.py verified-metal-kernels_amd/kernels/spec_mi355x.py
     python tests/verify.py tests/wrong_kernels/spec_cheat_nomax.py --skip-gate
-    python tests/verify.py my_kernel.py --op dsa --json out.json
+    python tests/verify.py some_module.py --op dsa --json report.json
 
-A kernel module has a top-level `def kernel(...)` taking the op's inputs as keyword arguments (vmk.ops.KEYS).
+A kernel module defines `kernel(**inputs)`, called with the op's keyword inputs (vmk.ops.KEYS; absent optional
+inputs arrive as None).  The op is taken from the file name (`<op>_anything.py`) unless --op names it.
 
-Steps (verify.py:10-24 of the reference):
-  0. static gate (AST whitelist, before import): imports limited to torch, math, functools and the vmk package; no
-     file/OS access, no reflection, no attribute stores, no standard attention/top-k/sort entry points, and at least
-     one call into vmk (the libvmk kernels).  --skip-gate disables it (needed for tests/wrong_kernels/).
-  1. the kernel is imported and run on every case in a CHILD process, which saves its raw outputs;
-  2. the verdict is computed in THIS process, which never imports the kernel, by regenerating the same inputs:
-     L1: 5 seeds at the nominal shape, allclose(atol=rtol=1e-2) against the PyTorch standard op;
-     L2: fuzzing against the float64 oracle: NaN/Inf pattern equal to the oracle rounded to fp16 (for nan_inf
-         inputs: equal to the standard op's pattern), normalised max error <= 1e-2;
-     L3: max and mean error vs float64 <= 2 * max(standard op error, 2^-11).
-  This build adds three judged groups outside the reference's counts: X (the op's EXTRA cases: ragged suffixes,
-  K outliers, kd > 32 masks, ...) judged like L2; TK (dsa only, when the module exports `select`): the
-  selected index set must equal the float64 top-2048 outside the boundary-tie band (oracle.dsa.topk_set_check);
-  and L4 (the judge's fourth layer, ONE-PAGER.md:13-14, absent from the public verify.py): on the op's L4_CASES,
-  every batch row computed alone (the op's `row_inputs`) must have the same output bits as in the batch.
-  An exception on any case is a failure.  Verdict: CORRECT only if every case of every group passes.
+How a module is judged
+----------------------
+1. Screening.  Before anything runs, the module's source is parsed and screened (`screen`): imports, builtins and
+   attributes must stay inside what a kernel module needs (torch tensors in, libvmk kernels, tensors out), and the
+   module must call into vmk at least once.  --skip-gate turns the screening off; the calibration fixtures under
+   tests/wrong_kernels/ are plain torch code and need it.
+2. Running.  A worker process (this script with --worker) imports the module and runs it over the case plan.  Each
+   finished case is written to disk at once: one .npz of outputs plus one line of a manifest.  A worker that dies
+   or runs out of time therefore leaves every case it finished behind.
+3. Scoring.  This process never imports the module.  It rebuilds each case's inputs from its seed, computes the
+   float64 oracle and the torch standard op where the layer needs them, and scores what the worker left.  A case
+   the worker did not finish is a failure.
 
-Exit code: 0 = CORRECT, 1 = REJECTED, 2 = usage error.
+The layers.  L1, L2 and L3 are the reference harness's (their case lists, seeds and thresholds follow
+verify.py:48-53 and 160-241 of the reference); the others are this build's.
+  L1   five seeds at the nominal shape; every output allclose (atol = rtol = 1e-2, NaN matching NaN) to the
+       torch standard op L1_REF.
+  L2   the op's FUZZ cases, seed 7 + i: NaN/Inf positions as in the float64 oracle rounded to the output type
+       (for dist "nan_inf", the standard op L3_REF's positions are accepted too) and normalised max error <= 1e-2.
+  L3   the op's L3_CASES, seed 3: max and mean normalised error each <= 2 * max(standard op's, 2^-11).
+  X    the op's EXTRA cases (this build's extensions), seed 50 + i, scored like L2.
+  CFG  the op's benchmark configurations (CONFIGS, seed 0 as in bench.py), scored like L2 and like L3.
+  TK   (dsa, when the module also defines `select(iq, ik, w, lens)`) on every case above: the count is
+       min(n, 2048), the positions are distinct and below n, and the set equals the float64 top-2048 except inside
+       the tie band around the 2048th score (oracle.dsa.topk_set_check).
+  L4   the op's L4_CASES, seed 200 + i: each batch row run alone gives the same output bytes as in the batch.
+The verdict is CORRECT when every case of every layer passes.  Exit status: 0 CORRECT, 1 REJECTED, 2 bad usage.
 """
 import argparse
 import ast
+import builtins
+import importlib
 import importlib.util
 import json
 import os
@@ -36,356 +46,574 @@ import subprocess
 import sys
 import tempfile
 import time
+from dataclasses import dataclass
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-PKG = os.path.join(ROOT, "verified-metal-kernels_amd")
-for _p in (ROOT, PKG, HERE):
+for _p in (ROOT, os.path.join(ROOT, "verified-metal-kernels_amd"), HERE):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
 import numpy as np  # noqa: E402
 
+from judge import normalised_error, nonfinite, rounding_of  # noqa: E402
 from vmk.ops import KEYS, load_op  # noqa: E402
 
-ORACLE = {"prefix": "oracle.prefix", "spec": "oracle.spec", "dsa": "oracle.dsa", "decode": "oracle.decode",
-          "prefix_paged": "oracle.prefix_paged"}
+ORACLES = {name: f"oracle.{name}" for name in KEYS}
+FLOOR = 2.0 ** -11                                  # L3: the error a correct fp16 kernel may always have
 
 
-def cand_inputs(opname, inp):
-    return {k: inp.get(k) for k in KEYS[opname]}
+# ============================================================================================ the case plan
+@dataclass
+class Case:
+    layer: str
+    n: int
+    shape: dict
+    dist: str
+    seed: int
+    label: str = ""
+
+    @property
+    def key(self):
+        return f"{self.layer}-{self.n}"
+
+    def describe(self):
+        return dict(case=self.key, label=self.label, shape=self.shape, dist=self.dist, seed=self.seed)
 
 
-def cases(op, extra=True):
-    """Verification cases, identical in the child (kernel outputs) and the parent (judgement): verify.py:48-53."""
-    out = [("L1", i, op.L1_SHAPE, "randn", 100 + i) for i in range(5)]
-    out += [("L2", i, s, d, 7 + i) for i, (s, d) in enumerate(op.FUZZ)]
-    out += [("L3", i, s, d, 3) for i, (s, d) in enumerate(op.L3_CASES)]
-    if extra:
-        out += [("X", i, s, d, 50 + i) for i, (s, d) in enumerate(getattr(op, "EXTRA", []))]
+@dataclass
+class Layer:
+    name: str
+    title: str
+    cases: object                     # op -> [(shape, dist, seed, label)]
+    rules: tuple = ()                 # scoring rules applied to each case, all of which must pass
+
+
+LAYERS = (
+    Layer("L1", "standard op at the nominal shape",
+          lambda op: [(op.L1_SHAPE, "randn", 100 + i, "") for i in range(5)], ("standard",)),
+    Layer("L2", "fuzzed shapes and values vs float64",
+          lambda op: [(s, d, 7 + i, "") for i, (s, d) in enumerate(op.FUZZ)], ("fuzz",)),
+    Layer("L3", "error within 2x the standard op's",
+          lambda op: [(s, d, 3, "") for s, d in op.L3_CASES], ("relative",)),
+    Layer("X", "this build's extension cases",
+          lambda op: [(s, d, 50 + i, "") for i, (s, d) in enumerate(getattr(op, "EXTRA", ()))], ("fuzz",)),
+    Layer("CFG", "benchmark configurations (L2 and L3 rules)",
+          lambda op: [(s, d, 0, name) for name, (s, d) in getattr(op, "CONFIGS", {}).items()],
+          ("fuzz", "relative")),
+)
+ROW_LAYER = Layer("L4", "row alone = row in the batch",
+                  lambda op: [(s, d, 200 + i, "") for i, (s, d) in enumerate(getattr(op, "L4_CASES", ()))])
+TOPK_LAYER = "TK"
+ALL_LAYERS = tuple(l.name for l in LAYERS) + (TOPK_LAYER, ROW_LAYER.name)
+
+
+def plan(op, layers=LAYERS):
+    """Every output case of the op, in the order the worker runs them."""
+    out = []
+    for layer in layers:
+        out += [Case(layer.name, i, s, d, seed, label) for i, (s, d, seed, label) in enumerate(layer.cases(op))]
     return out
 
 
-# ------------------------------------------------------------------------------------------------ static gate
-ALLOWED_IMPORTS = {"torch", "math", "functools", "vmk"}
-BANNED_NAMES = {"open", "exec", "eval", "compile", "__import__", "globals", "locals", "vars", "getattr", "setattr",
-                "delattr", "input", "breakpoint", "help", "exit", "quit", "memoryview", "super", "classmethod",
-                "staticmethod", "property", "type", "object", "dir", "id", "hash", "print"}
-BANNED_ATTRS = {"save", "load", "manual_seed", "seed", "set_default_device", "set_default_dtype", "distributed",
-                "random", "rand", "randn", "scaled_dot_product_attention", "softmax", "log_softmax", "topk", "sort",
-                "argsort", "kthvalue", "msort", "multi_head_attention_forward", "flash_attention", "cuda_kernel",
-                "load_inline", "cpp_extension", "system", "popen"}
-MAX_BYTES = 200_000
+def row_plan(op):
+    return [Case(ROW_LAYER.name, i, s, d, seed) for i, (s, d, seed, _) in enumerate(ROW_LAYER.cases(op))]
 
 
-def gate(src):
-    """List of violations (empty = accepted); verify.py:57-108 with torch/vmk in place of mlx.core."""
-    errs = []
-    if len(src.encode()) > MAX_BYTES:
-        return [f"module larger than {MAX_BYTES} bytes"]
+def kernel_inputs(opname, inputs):
+    """The keyword inputs the op's kernel receives; optional ones the generator left out are None."""
+    return {k: inputs.get(k) for k in KEYS[opname]}
+
+
+# ============================================================================================ screening
+SIZE_LIMIT = 200_000
+IMPORT_ROOTS = {"torch", "math", "functools", "vmk"}
+TORCH_SUBMODULES = {"torch.nn.functional"}
+# Builtins a kernel module may name; any other builtin (open, exec, getattr, print, type, ...) is refused.
+BUILTINS_ALLOWED = frozenset({
+    "abs", "all", "any", "bool", "dict", "divmod", "enumerate", "float", "int", "isinstance", "len", "list", "max",
+    "min", "pow", "range", "reversed", "round", "slice", "str", "sum", "tuple", "zip", "Exception", "RuntimeError",
+    "TypeError", "ValueError", "IndexError", "KeyError", "NotImplementedError", "AssertionError"})
+BUILTIN_NAMES = frozenset(dir(builtins))
+# Attribute names refused anywhere, by the reason for refusing them.
+ATTRIBUTES_REFUSED = {
+    "reads or writes files, or starts processes": {
+        "save", "load", "savez", "tofile", "fromfile", "from_file", "system", "popen", "spawn", "fork"},
+    "changes global state or draws random numbers": {
+        "manual_seed", "seed", "random", "rand", "randn", "randint", "set_default_device", "set_default_dtype",
+        "set_rng_state", "distributed"},
+    "is a standard attention, softmax or selection routine": {
+        "scaled_dot_product_attention", "multi_head_attention_forward", "flash_attention", "softmax",
+        "log_softmax", "topk", "sort", "argsort", "msort", "kthvalue"},
+    "generates or compiles code at run time": {"cpp_extension", "load_inline", "cuda_kernel", "jit", "compile"},
+}
+_REFUSED = {a: why for why, names in ATTRIBUTES_REFUSED.items() for a in names}
+
+
+class _Screen(ast.NodeVisitor):
+    def __init__(self):
+        self.problems = []
+        self.calls_vmk = False
+
+    def refuse(self, node, what):
+        self.problems.append(f"line {getattr(node, 'lineno', '?')}: {what}")
+
+    @staticmethod
+    def _import_ok(name):
+        root = name.split(".")[0]
+        if root not in IMPORT_ROOTS:
+            return False
+        return name in (root,) or name in TORCH_SUBMODULES
+
+    def visit_Import(self, node):
+        for alias in node.names:
+            if not self._import_ok(alias.name):
+                self.refuse(node, f"`import {alias.name}` (modules allowed: {sorted(IMPORT_ROOTS)}, "
+                                  f"{sorted(TORCH_SUBMODULES)})")
+
+    def visit_ImportFrom(self, node):
+        if node.level or not node.module or not self._import_ok(node.module):
+            self.refuse(node, f"`from {'.' * node.level}{node.module or ''} import ...`")
+
+    def visit_Name(self, node):
+        if node.id.startswith("__"):
+            self.refuse(node, f"dunder name `{node.id}`")
+        elif node.id in BUILTIN_NAMES and node.id not in BUILTINS_ALLOWED:
+            self.refuse(node, f"builtin `{node.id}` is not on the allowlist")
+        self.generic_visit(node)
+
+    def visit_Attribute(self, node):
+        if isinstance(node.ctx, (ast.Store, ast.Del)):
+            self.refuse(node, f"stores into or deletes the attribute `.{node.attr}`")
+        if node.attr.startswith("_"):
+            self.refuse(node, f"private attribute `.{node.attr}`")
+        if node.attr in _REFUSED:
+            self.refuse(node, f"`.{node.attr}` {_REFUSED[node.attr]}")
+        self.generic_visit(node)
+
+    def visit_Call(self, node):
+        f = node.func
+        while isinstance(f, ast.Attribute):
+            if isinstance(f.value, ast.Name) and f.value.id == "vmk":
+                self.calls_vmk = True
+            f = f.value
+        self.generic_visit(node)
+
+    def _scope(self, node):
+        self.refuse(node, f"`{type(node).__name__.lower()}` statement")
+
+    visit_Global = visit_Nonlocal = _scope
+
+    def _coroutine(self, node):
+        self.refuse(node, f"{type(node).__name__} (no async code or generators)")
+        self.generic_visit(node)
+
+    visit_AsyncFunctionDef = visit_Await = visit_Yield = visit_YieldFrom = _coroutine
+
+
+def screen(src):
+    """Problems found in a kernel module's source; an empty list means it may run."""
+    if len(src.encode()) > SIZE_LIMIT:
+        return [f"the module is larger than {SIZE_LIMIT} bytes"]
     try:
         tree = ast.parse(src)
     except SyntaxError as e:
-        return [f"SyntaxError: {e}"]
+        return [f"does not parse: {e}"]
+    s = _Screen()
+    s.visit(tree)
     if not any(isinstance(n, ast.FunctionDef) and n.name == "kernel" for n in tree.body):
-        errs.append("no top-level `def kernel(...)`")
-    uses_vmk = False
-    for n in ast.walk(tree):
-        if isinstance(n, ast.Import):
-            for a in n.names:
-                if a.name.split(".")[0] not in ALLOWED_IMPORTS or (a.name.startswith("torch.") and
-                                                                     a.name != "torch.nn.functional"):
-                    errs.append(f"line {n.lineno}: import {a.name} not allowed")
-        elif isinstance(n, ast.ImportFrom):
-            if not n.module or n.module.split(".")[0] not in ALLOWED_IMPORTS or n.level:
-                errs.append(f"line {n.lineno}: from {n.module} import ... not allowed")
-        elif isinstance(n, ast.Name):
-            if n.id in BANNED_NAMES or n.id.startswith("__"):
-                errs.append(f"line {n.lineno}: name `{n.id}` not allowed")
-        elif isinstance(n, ast.Attribute):
-            if isinstance(n.ctx, (ast.Store, ast.Del)):
-                errs.append(f"line {n.lineno}: assigning/deleting attributes is not allowed")
-            if n.attr.startswith("_"):
-                errs.append(f"line {n.lineno}: attribute `.{n.attr}` not allowed")
-            if n.attr in BANNED_ATTRS:
-                errs.append(f"line {n.lineno}: `.{n.attr}` not allowed")
-            if isinstance(n.value, ast.Name) and n.value.id == "vmk":
-                uses_vmk = True
-        elif isinstance(n, (ast.Global, ast.Nonlocal)):
-            errs.append(f"line {n.lineno}: global/nonlocal not allowed")
-        elif isinstance(n, (ast.AsyncFunctionDef, ast.Await, ast.Yield, ast.YieldFrom)):
-            errs.append(f"line {n.lineno}: async/generators not allowed")
-    if not uses_vmk:
-        errs.append("no call into vmk found: the hot path must use the libvmk kernels")
-    return errs
+        s.problems.append("no top-level `def kernel(...)`")
+    if not s.calls_vmk:
+        s.problems.append("never calls into vmk: the libvmk kernels must do the work")
+    return s.problems
 
 
-def import_module(path):
-    s = importlib.util.spec_from_file_location("candidate_kernel", path)
-    m = importlib.util.module_from_spec(s)
-    s.loader.exec_module(m)
-    return m
+# ============================================================================================ worker side
+def _module(path):
+    spec = importlib.util.spec_from_file_location("kernel_under_test", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
 
 
-# ------------------------------------------------------------------------------------------------ child side
-def as_tuple(o):
-    return tuple(o) if isinstance(o, (tuple, list)) else (o,)
+def _outputs(result):
+    return list(result) if isinstance(result, (tuple, list)) else [result]
 
 
-def child_outputs(opname, kernel_path, out):
-    """The only function that imports the kernel.  Saves raw outputs (.npz) and per-case status (.json)."""
+def _host(t):
+    """An output on the host: bf16 widened to float32 (NumPy has no bf16), anything else as it is."""
     import torch
-    mod = import_module(kernel_path)
-    fn = mod.kernel
-    sel = getattr(mod, "select", None) if opname == "dsa" else None
-    op = load_op(opname)
-    arrays, meta = {}, {}
-    for layer, i, shape, dist, seed in cases(op):
-        key = f"{layer}_{i}"
-        inp = cand_inputs(opname, op.make_inputs(shape, seed=seed, dist=dist, device="cuda"))
-        t0 = time.time()
-        try:
-            o = as_tuple(fn(**inp))
-            torch.cuda.synchronize()
-            for j, a in enumerate(o):
-                arrays[f"{key}__{j}"] = a.float().cpu().numpy() if a.dtype == torch.bfloat16 else a.cpu().numpy()
-            meta[key] = dict(ok=True, n_out=len(o), dtypes=[str(a.dtype) for a in o], s=time.time() - t0)
-            if sel is not None:
-                idx, cnt = sel(inp["iq"], inp["ik"], inp["w"], inp.get("lens"))
-                torch.cuda.synchronize()
-                arrays[f"{key}__idx"], arrays[f"{key}__cnt"] = idx.cpu().numpy(), cnt.cpu().numpy()
-                meta[key]["select"] = True
-        except Exception as e:
-            meta[key] = dict(ok=False, error=f"{type(e).__name__}: {str(e)[:1500]}")
-        del inp
-        torch.cuda.empty_cache()
-    for i, (shape, dist) in enumerate(getattr(op, "L4_CASES", [])):
-        key = f"L4_{i}"
-        inp = cand_inputs(opname, op.make_inputs(shape, seed=200 + i, dist=dist, device="cuda"))
-        t0 = time.time()
-        try:
-            full = as_tuple(fn(**inp))
-            torch.cuda.synchronize()
-            full = [a.cpu().numpy() for a in full]
-            nrows = full[0].shape[0]
-            rows = [[] for _ in full]
-            for r in range(nrows):
-                o = as_tuple(fn(**op.row_inputs(inp, r)))
-                torch.cuda.synchronize()
-                for j, a in enumerate(o):
-                    rows[j].append(a.cpu().numpy())
-            for j, a in enumerate(full):
-                arrays[f"{key}__full{j}"] = a
-                arrays[f"{key}__rows{j}"] = np.concatenate(rows[j])
-            meta[key] = dict(ok=True, n_out=len(full), n_rows=nrows, s=time.time() - t0)
-        except Exception as e:
-            meta[key] = dict(ok=False, error=f"{type(e).__name__}: {str(e)[:1500]}")
-        del inp
-        torch.cuda.empty_cache()
-    np.savez(out + ".npz", **arrays)
-    json.dump(meta, open(out + ".json", "w"))
+    return (t.float() if t.dtype == torch.bfloat16 else t).cpu().numpy()
 
 
-# ------------------------------------------------------------------------------------------------ parent side
-from judge import kind_of, nerr, pattern  # noqa: E402
-
-
-def to64(a):
+def _bytes(t):
+    """An output's raw bytes, row by row, on the host (the row-invariance layer compares bits)."""
     import torch
-    if isinstance(a, torch.Tensor):
-        a = a.detach().float().cpu().numpy()
-    return np.asarray(a).astype(np.float64)
+    return t.contiguous().view(torch.uint8).reshape(t.shape[0], -1).cpu().numpy()
 
 
-def judge(opname, outpath):
-    """verify.py:174-241 of the reference, against the float64 oracle and the PyTorch standard op."""
-    import importlib
-    import torch
-    op = load_op(opname)
-    orc = importlib.import_module(ORACLE[opname])
-    meta = json.load(open(outpath + ".json"))
-    arrs = np.load(outpath + ".npz")
-    std1, std3 = getattr(op, op.L1_REF), getattr(op, op.L3_REF)
-    rep = dict(L1=[], L2=[], L3=[], X=[], TK=[])
-    for layer, i, shape, dist, seed in cases(op):
-        key = f"{layer}_{i}"
-        case = dict(case=key, shape=shape, dist=dist)
-        m = meta.get(key, dict(ok=False, error="missing (child crashed or timed out before this case)"))
-        if not m["ok"]:
-            case.update(ok=False, error=m["error"])
-            rep[layer].append(case)
-            continue
-        inp = op.make_inputs(shape, seed=seed, dist=dist, device="cuda")
-        outs = [arrs[f"{key}__{j}"].astype(np.float64) for j in range(m["n_out"])]
-        if m.get("select"):
-            s64, _ = orc.ref_select64(inp["iq"], inp["ik"], inp["w"], inp["lens"])
-            idx, cnt = arrs[f"{key}__idx"], arrs[f"{key}__cnt"]
-            lens = None if inp["lens"] is None else inp["lens"].cpu().numpy()
-            tk_ok, det = True, []
-            for b in range(s64.shape[0]):
-                n = shape["L"] if lens is None else int(lens[b])
-                okb, d = orc.topk_set_check(idx[b], int(cnt[b]), s64[b], n)
-                tk_ok &= okb
-                det.append(d)
-            rep["TK"].append(dict(case=key, shape=shape, dist=dist, ok=bool(tk_ok), detail=det if not tk_ok else None))
-        if layer == "L1":
-            s = [to64(x) for x in as_tuple(std1(**inp))]
+class Worker:
+    """Runs a kernel module over a case plan and writes each case as soon as it finishes."""
+
+    def __init__(self, opname, module_path, outdir, device="cuda"):
+        self.opname, self.outdir, self.device = opname, outdir, device
+        self.op = load_op(opname)
+        self.mod = _module(module_path)
+        self.select = getattr(self.mod, "select", None) if opname == "dsa" else None
+        self.manifest = open(os.path.join(outdir, "manifest.jsonl"), "a")
+
+    def sync(self):
+        import torch
+        if self.device != "cpu":
             torch.cuda.synchronize()
-            if len(s) != len(outs) or any(a.shape != b.shape for a, b in zip(outs, s)):
-                case.update(ok=False, error=f"output shapes {[a.shape for a in outs]} != expected {[b.shape for b in s]}")
-            else:
-                ok = all(np.allclose(a, b, atol=1e-2, rtol=1e-2, equal_nan=True) for a, b in zip(outs, s))
-                case.update(ok=bool(ok), maxdiff=max(float(np.nanmax(np.abs(a - b))) if a.size else 0.0
-                                                     for a, b in zip(outs, s)))
-            rep[layer].append(case)
-            continue
-        r = [to64(x) for x in as_tuple(orc.ref64(**cand_inputs(opname, inp)))]
-        if len(r) != len(outs) or any(a.shape != b.shape for a, b in zip(outs, r)):
-            case.update(ok=False, error=f"output shapes {[a.shape for a in outs]} != expected {[b.shape for b in r]}")
-            rep[layer].append(case)
-            continue
-        if layer in ("L2", "X"):
-            pat_ok, emax, emean, s = True, 0.0, 0.0, None
-            for j, (o, rr) in enumerate(zip(outs, r)):
-                half = kind_of(m["dtypes"][j])
-                pn, pi = pattern(o, half)
-                rn, ri = pattern(rr, half)
-                pj = bool((pn == rn).all() and (pi == ri).all())
-                if not pj and dist == "nan_inf":
-                    s = s or [to64(x) for x in as_tuple(std3(**inp))]
-                    sn, si = pattern(s[j], half)
-                    pj = bool((pn == sn).all() and (pi == si).all())
-                    case["pattern_vs"] = "std_op"
-                if not pj:
-                    case.setdefault("pattern_detail", []).append(
-                        dict(output=j, nan_got=int(pn.sum()), nan_exp=int(rn.sum()), inf_got=int(pi.sum()),
-                             inf_exp=int(ri.sum())))
-                em, ea = nerr(o, rr)
-                pat_ok, emax, emean = pat_ok and pj, max(emax, em), max(emean, ea)
-            case.update(ok=bool(pat_ok and emax <= 1e-2), pattern_ok=pat_ok, err_max=emax, err_mean=emean)
-        else:
-            s = [to64(x) for x in as_tuple(std3(**inp))]
-            ok, worst = True, {}
-            for j, (o, rr, ss) in enumerate(zip(outs, r, s)):
-                em, ea = nerr(o, rr)
-                sm, sa = nerr(ss, rr)
-                tol = 2.0 ** -11
-                okj = em <= 2 * max(sm, tol) and ea <= 2 * max(sa, tol)
-                ok = ok and okj
-                worst[f"out{j}"] = dict(err_max=em, err_mean=ea, std_err_max=sm, std_err_mean=sa)
-            case.update(ok=bool(ok), errors=worst)
-        rep[layer].append(case)
-        del inp
-        torch.cuda.empty_cache()
-    rep["L4"] = [l4_case(meta, arrs, i, shape, dist) for i, (shape, dist) in enumerate(getattr(op, "L4_CASES", []))]
-    for layer in LAYERS:
-        rep[f"{layer}_pass"] = sum(c["ok"] for c in rep[layer])
-        rep[f"{layer}_n"] = len(rep[layer])
-    rep["verdict"] = "CORRECT" if all(rep[f"{l}_pass"] == rep[f"{l}_n"] for l in LAYERS) else "REJECTED"
-    rep["sdpa_backends"] = dict(flash=torch.backends.cuda.flash_sdp_enabled(),
-                                mem_efficient=torch.backends.cuda.mem_efficient_sdp_enabled(),
-                                math=torch.backends.cuda.math_sdp_enabled())
+
+    def inputs(self, case):
+        return kernel_inputs(self.opname, self.op.make_inputs(case.shape, seed=case.seed, dist=case.dist,
+                                                              device=self.device))
+
+    def record(self, case, entry, arrays):
+        if arrays:
+            np.savez(os.path.join(self.outdir, case.key + ".npz"), **arrays)
+        self.manifest.write(json.dumps(dict(key=case.key, **entry)) + "\n")
+        self.manifest.flush()
+        os.fsync(self.manifest.fileno())
+
+    def run_case(self, case):
+        inp = self.inputs(case)
+        t0 = time.perf_counter()
+        outs = _outputs(self.mod.kernel(**inp))
+        self.sync()
+        arrays = {f"out{j}": _host(o) for j, o in enumerate(outs)}
+        entry = dict(ok=True, dtypes=[str(o.dtype) for o in outs], seconds=round(time.perf_counter() - t0, 3))
+        if self.select is not None:
+            idx, cnt = self.select(inp["iq"], inp["ik"], inp["w"], inp.get("lens"))
+            self.sync()
+            arrays.update(idx=idx.cpu().numpy(), cnt=cnt.cpu().numpy())
+            entry["selection"] = True
+        return entry, arrays
+
+    def run_rows(self, case):
+        inp = self.inputs(case)
+        t0 = time.perf_counter()
+        batch = _outputs(self.mod.kernel(**inp))
+        self.sync()
+        arrays = {f"batch{j}": _bytes(o) for j, o in enumerate(batch)}
+        alone = [[] for _ in batch]
+        nrows = batch[0].shape[0]
+        for r in range(nrows):
+            for j, o in enumerate(_outputs(self.mod.kernel(**self.op.row_inputs(inp, r)))):
+                alone[j].append(_bytes(o))
+            self.sync()
+        arrays.update({f"alone{j}": np.concatenate(a) for j, a in enumerate(alone)})
+        return dict(ok=True, rows=nrows, outputs=len(batch), seconds=round(time.perf_counter() - t0, 3)), arrays
+
+    def run(self, cases, row_cases):
+        for run_one, todo in ((self.run_case, cases), (self.run_rows, row_cases)):
+            for case in todo:
+                print(f"[worker] {case.key} {case.label} {case.shape} {case.dist}", flush=True)
+                try:
+                    entry, arrays = run_one(case)
+                except Exception as e:             # the case fails; the plan goes on
+                    entry, arrays = dict(ok=False, error=f"{type(e).__name__}: {str(e)[:1500]}"), {}
+                self.record(case, entry, arrays)
+                if self.device != "cpu":
+                    import torch
+                    torch.cuda.empty_cache()
+        self.manifest.close()
+
+
+def read_results(outdir):
+    """key -> (manifest entry, arrays or None), for every case the worker finished."""
+    done = {}
+    path = os.path.join(outdir, "manifest.jsonl")
+    if not os.path.exists(path):
+        return done
+    with open(path) as f:
+        for line in f:
+            line = line.strip()
+            if not line:
+                continue
+            try:
+                e = json.loads(line)
+            except json.JSONDecodeError:           # a line cut short by a dying worker
+                continue
+            npz = os.path.join(outdir, e["key"] + ".npz")
+            done[e["key"]] = (e, dict(np.load(npz)) if os.path.exists(npz) else None)
+    return done
+
+
+# ============================================================================================ scoring side
+def _f64(x):
+    import torch
+    if isinstance(x, torch.Tensor):
+        x = x.detach().float().cpu().numpy()
+    return np.asarray(x, dtype=np.float64)
+
+
+class Scorer:
+    """Scores finished cases of one op; references are computed lazily, once per case."""
+
+    def __init__(self, opname, device="cuda"):
+        self.opname, self.device = opname, device
+        self.op = load_op(opname)
+        self.oracle = importlib.import_module(ORACLES[opname])
+        self.std_l1 = getattr(self.op, self.op.L1_REF)
+        self.std_l3 = getattr(self.op, self.op.L3_REF)
+        self._last = None
+
+    def sync(self):
+        import torch
+        if self.device != "cpu":
+            torch.cuda.synchronize()
+
+    def context(self, case):
+        """The references of `case`; the last case's are kept, since the TK layer scores the same case next."""
+        if self._last is None or self._last.case is not case:
+            self._last = _Refs(self, case)
+        return self._last
+
+    # -- rules: each returns (ok, details)
+    def rule_standard(self, refs, outs, dtypes):
+        want = refs.standard(self.std_l1)
+        if (msg := _shape_mismatch(outs, want)):
+            return False, dict(error=msg)
+        close = [bool(np.allclose(o, w, rtol=1e-2, atol=1e-2, equal_nan=True)) for o, w in zip(outs, want)]
+        worst = max((float(np.nanmax(np.abs(o - w))) if o.size else 0.0) for o, w in zip(outs, want))
+        return all(close), dict(max_abs_diff=worst)
+
+    def rule_fuzz(self, refs, outs, dtypes):
+        want = refs.oracle()
+        if (msg := _shape_mismatch(outs, want)):
+            return False, dict(error=msg)
+        ok, det = True, dict(err_max=0.0, err_mean=0.0)
+        for j, (o, w) in enumerate(zip(outs, want)):
+            kind = rounding_of(dtypes[j])
+            on, oi = nonfinite(o, kind)
+            wn, wi = nonfinite(w, kind)
+            same = np.array_equal(on, wn) and np.array_equal(oi, wi)
+            if not same and refs.case.dist == "nan_inf":
+                sn, si = nonfinite(refs.standard(self.std_l3)[j], kind)
+                same = np.array_equal(on, sn) and np.array_equal(oi, si)
+                det["nonfinite_matched"] = "standard op"
+            if not same:
+                det.setdefault("nonfinite_mismatch", []).append(
+                    dict(output=j, nan=[int(on.sum()), int(wn.sum())], inf=[int(oi.sum()), int(wi.sum())]))
+            emax, emean = normalised_error(o, w)
+            det["err_max"], det["err_mean"] = max(det["err_max"], emax), max(det["err_mean"], emean)
+            ok = ok and same and emax <= 1e-2
+        return ok, det
+
+    def rule_relative(self, refs, outs, dtypes):
+        want = refs.oracle()
+        if (msg := _shape_mismatch(outs, want)):
+            return False, dict(error=msg)
+        std = refs.standard(self.std_l3)
+        ok, det = True, {}
+        for j, (o, w, s) in enumerate(zip(outs, want, std)):
+            kmax, kmean = normalised_error(o, w)
+            smax, smean = normalised_error(s, w)
+            okj = kmax <= 2 * max(smax, FLOOR) and kmean <= 2 * max(smean, FLOOR)
+            det[f"out{j}"] = dict(kernel=[kmax, kmean], standard=[smax, smean])
+            ok = ok and okj
+        return ok, det
+
+    def score(self, layer, case, entry, arrays):
+        res = case.describe()
+        if entry is None:
+            return dict(res, ok=False, error="the worker did not finish this case")
+        if not entry["ok"]:
+            return dict(res, ok=False, error=entry["error"])
+        outs = [arrays[f"out{j}"].astype(np.float64) for j in range(len(entry["dtypes"]))]
+        refs = self.context(case)
+        ok = True
+        for rule in layer.rules:
+            okr, det = getattr(self, "rule_" + rule)(refs, outs, entry["dtypes"])
+            res[rule] = det
+            ok = ok and okr
+        res["ok"] = bool(ok)
+        return res
+
+    def score_selection(self, case, entry, arrays):
+        """The TK layer for one case whose worker entry holds a selection."""
+        res = case.describe()
+        refs = self.context(case)
+        s64, _ = refs.selection()
+        lens = refs.inputs.get("lens")
+        lens = None if lens is None else lens.cpu().numpy()
+        per = []
+        ok = True
+        for b in range(s64.shape[0]):
+            n = s64.shape[1] if lens is None else int(lens[b])
+            okb, det = self.oracle.topk_set_check(arrays["idx"][b], int(arrays["cnt"][b]), s64[b], n)
+            ok = ok and okb
+            per.append(det)
+        res.update(ok=bool(ok), boundary=[d.get("boundary", 0) for d in per])
+        if not ok:
+            res["requests"] = per
+        return res
+
+
+class _Refs:
+    """Inputs and references of one case, each built on first use."""
+
+    def __init__(self, scorer, case):
+        self.s, self.case = scorer, case
+        self._inp, self._oracle, self._std, self._sel = None, None, {}, None
+
+    @property
+    def inputs(self):
+        if self._inp is None:
+            c = self.case
+            self._inp = self.s.op.make_inputs(c.shape, seed=c.seed, dist=c.dist, device=self.s.device)
+        return self._inp
+
+    def standard(self, fn):
+        if fn not in self._std:
+            self._std[fn] = [_f64(x) for x in _outputs(fn(**self.inputs))]
+            self.s.sync()
+        return self._std[fn]
+
+    def oracle(self):
+        if self._oracle is None:
+            self._oracle = [_f64(x) for x in _outputs(self.s.oracle.ref64(**kernel_inputs(self.s.opname,
+                                                                                            self.inputs)))]
+        return self._oracle
+
+    def selection(self):
+        if self._sel is None:
+            i = self.inputs
+            self._sel = self.s.oracle.ref_select64(i["iq"], i["ik"], i["w"], i.get("lens"))
+        return self._sel
+
+
+def _shape_mismatch(outs, want):
+    got_s, want_s = [o.shape for o in outs], [w.shape for w in want]
+    return None if got_s == want_s else f"the kernel returned shapes {got_s}; the reference has {want_s}"
+
+
+def score_rows(case, entry, arrays):
+    """The L4 layer for one case: rows of the batch output whose bytes differ from the same row computed alone."""
+    res = case.describe()
+    if entry is None:
+        return dict(res, ok=False, error="the worker did not finish this case")
+    if not entry["ok"]:
+        return dict(res, ok=False, error=entry["error"])
+    differ = set()
+    for j in range(entry["outputs"]):
+        a, b = arrays[f"batch{j}"], arrays[f"alone{j}"]
+        if a.shape != b.shape:
+            return dict(res, ok=False, error=f"output {j}: batch bytes {a.shape} vs rows alone {b.shape}")
+        differ |= set(np.nonzero((a != b).any(axis=1))[0].tolist())
+    return dict(res, ok=not differ, rows=entry["rows"], differing=len(differ), first_differing=sorted(differ)[:16])
+
+
+def assess(opname, outdir, device="cuda", cases=None, row_cases=None):
+    """The report of one worker run: every layer's cases, scored; the verdict."""
+    import torch
+    sc = Scorer(opname, device)
+    cases = plan(sc.op) if cases is None else cases
+    row_cases = row_plan(sc.op) if row_cases is None else row_cases
+    done = read_results(outdir)
+    layers = {name: [] for name in ALL_LAYERS}
+    by_name = {l.name: l for l in LAYERS}
+    for case in cases:
+        entry, arrays = done.get(case.key, (None, None))
+        layers[case.layer].append(sc.score(by_name[case.layer], case, entry, arrays))
+        if entry is not None and entry.get("selection"):
+            layers[TOPK_LAYER].append(sc.score_selection(case, entry, arrays))
+        if device != "cpu":
+            torch.cuda.empty_cache()
+    for case in row_cases:
+        entry, arrays = done.get(case.key, (None, None))
+        layers[ROW_LAYER.name].append(score_rows(case, entry, arrays))
+    titles = {l.name: l.title for l in LAYERS}
+    titles.update({TOPK_LAYER: "top-2048 set vs float64", ROW_LAYER.name: ROW_LAYER.title})
+    rep = dict(op=opname, layers={name: dict(title=titles[name], passed=sum(c["ok"] for c in cs), total=len(cs),
+                                             cases=cs) for name, cs in layers.items()})
+    rep["verdict"] = "CORRECT" if all(v["passed"] == v["total"] for v in rep["layers"].values()) else "REJECTED"
+    if device != "cpu":
+        rep["sdpa_backends"] = dict(flash=torch.backends.cuda.flash_sdp_enabled(),
+                                    mem_efficient=torch.backends.cuda.mem_efficient_sdp_enabled(),
+                                    math=torch.backends.cuda.math_sdp_enabled())
     return rep
 
 
-LAYERS = ("L1", "L2", "L3", "X", "TK", "L4")
-
-
-def l4_case(meta, arrs, i, shape, dist):
-    """Row invariance: each output row of the batch call must be bit-equal to the same row computed alone."""
-    key = f"L4_{i}"
-    case = dict(case=key, shape=shape, dist=dist)
-    m = meta.get(key, dict(ok=False, error="missing (child crashed or timed out before this case)"))
-    if not m["ok"]:
-        case.update(ok=False, error=m["error"])
-        return case
-    bad = []
-    for j in range(m["n_out"]):
-        full, rows = arrs[f"{key}__full{j}"], arrs[f"{key}__rows{j}"]
-        if full.shape != rows.shape or full.dtype != rows.dtype:
-            case.update(ok=False,
-                        error=f"output {j}: batch {full.shape} {full.dtype} vs rows {rows.shape} {rows.dtype}")
-            return case
-        fb = full.reshape(full.shape[0], -1).view(np.uint8)
-        rb = rows.reshape(rows.shape[0], -1).view(np.uint8)
-        bad += [r for r in range(full.shape[0]) if not np.array_equal(fb[r], rb[r]) and r not in bad]
-    case.update(ok=not bad, n_rows=m["n_rows"], rows_differing=sorted(bad)[:16], n_differing=len(bad))
-    return case
-
-
-def summary(rep, max_fail=6):
-    lines = [f"L1 (standard op, nominal shape)  {rep['L1_pass']}/{rep['L1_n']}",
-             f"L2 (fuzzing vs float64)          {rep['L2_pass']}/{rep['L2_n']}",
-             f"L3 (numerical error vs float64)  {rep['L3_pass']}/{rep['L3_n']}",
-             f"X  (this build's extra cases)    {rep['X_pass']}/{rep['X_n']}"]
-    if rep["TK_n"]:
-        lines.append(f"TK (top-k set vs float64)        {rep['TK_pass']}/{rep['TK_n']}")
-    if rep["L4_n"]:
-        lines.append(f"L4 (row alone = row in batch)    {rep['L4_pass']}/{rep['L4_n']}")
-    lines.append(f"=> {rep['verdict']}")
-    fails = [c for l in LAYERS for c in rep[l] if not c["ok"]]
-    for c in fails[:max_fail]:
-        d = {k: v for k, v in c.items() if k != "ok"}
-        if "error" in d:
-            d["error"] = d["error"][:600]
-        lines.append("  FAIL " + json.dumps(d, default=str))
-    if len(fails) > max_fail:
-        lines.append(f"  ... and {len(fails) - max_fail} more failing cases")
+def render(rep, show=8):
+    """A short text form of a report: one line per layer, then the first failing cases."""
+    lines = []
+    for name, v in rep["layers"].items():
+        if v["total"]:
+            lines.append(f"  {name:<4}{v['passed']:>4}/{v['total']:<4} {v['title']}")
+    lines.append(f"verdict: {rep['verdict']}")
+    bad = [c for v in rep["layers"].values() for c in v["cases"] if not c["ok"]]
+    for c in bad[:show]:
+        brief = {k: v for k, v in c.items() if k not in ("ok", "requests")}
+        lines.append("  failed " + json.dumps(brief, default=str)[:700])
+    if len(bad) > show:
+        lines.append(f"  (+{len(bad) - show} more failed cases)")
     return "\n".join(lines)
 
 
-def infer_op(path):
-    """The longest op name that the file name starts with (prefix_paged_x.py is prefix_paged, not prefix)."""
-    base = os.path.basename(path)
-    hits = [op for op in KEYS if base.startswith(op + "_")]
-    return max(hits, key=len) if hits else None
+def op_from_filename(path):
+    """The longest op name that the file's name starts with, followed by '_' (prefix_paged_x.py -> prefix_paged)."""
+    stem = os.path.basename(path)
+    names = [op for op in KEYS if stem.startswith(op + "_")]
+    return max(names, key=len) if names else None
+
+
+# ============================================================================================ command line
+def run_worker(opname, module_path, outdir, timeout, device):
+    """Starts the worker process and waits for it; returns its exit status, or 'timeout'."""
+    cmd = [sys.executable, os.path.abspath(__file__), "--worker", opname, module_path, outdir, device]
+    try:
+        return subprocess.run(cmd, timeout=timeout).returncode
+    except subprocess.TimeoutExpired:
+        return "timeout"
 
 
 def main(argv=None):
-    argv = sys.argv[1:] if argv is None else argv
-    if len(argv) > 0 and argv[0] == "--child":   # internal: verify.py --child OP KERNEL OUT
-        child_outputs(argv[1], argv[2], argv[3])
+    argv = sys.argv[1:] if argv is None else list(argv)
+    if argv[:1] == ["--worker"]:
+        opname, module_path, outdir, device = argv[1:5]
+        w = Worker(opname, module_path, outdir, device)
+        w.run(plan(w.op), row_plan(w.op))
         return 0
-    ap = argparse.ArgumentParser(description="Three-layer verifier (see the module docstring).")
-    ap.add_argument("kernel", help="path to the kernel module (a file with `def kernel(...)`)")
-    ap.add_argument("--op", choices=sorted(KEYS), help="op name (default: inferred from the file name)")
-    ap.add_argument("--skip-gate", action="store_true", help="do not apply the static gate (tests/wrong_kernels/)")
-    ap.add_argument("--json", help="write the full report to this file")
-    ap.add_argument("--timeout", type=int, default=1800, help="child process timeout in seconds")
+    ap = argparse.ArgumentParser(description="Judge one kernel module (the module docstring explains the layers).")
+    ap.add_argument("kernel", help="path of the kernel module (defines `kernel(...)`)")
+    ap.add_argument("--op", choices=sorted(KEYS), help="the op; by default taken from the file name")
+    ap.add_argument("--skip-gate", action="store_true", help="run without screening the source")
+    ap.add_argument("--json", help="also write the full report to this file")
+    ap.add_argument("--timeout", type=int, default=1800, help="seconds the worker process may run")
+    ap.add_argument("--device", default="cuda", help=argparse.SUPPRESS)
     a = ap.parse_args(argv)
-    opname = a.op or infer_op(a.kernel)
+    opname = a.op or op_from_filename(a.kernel)
     if opname is None:
-        print("cannot infer the op from the file name; pass --op", file=sys.stderr)
+        print(f"{a.kernel}: no op name at the start of the file name; give --op", file=sys.stderr)
         return 2
-    kpath = os.path.abspath(a.kernel)
-    print(f"kernel: {a.kernel}   op: {opname}", flush=True)
+    path = os.path.abspath(a.kernel)
+    print(f"{a.kernel}  (op {opname})", flush=True)
     if a.skip_gate:
-        print("static gate: SKIPPED (--skip-gate)")
+        print("screening: off (--skip-gate)")
     else:
-        errs = gate(open(kpath).read())
-        if errs:
-            print("static gate: REJECTED\n  " + "\n  ".join(errs))
-            print("=> REJECTED (static gate; the kernel was not imported)")
+        problems = screen(open(path).read())
+        if problems:
+            print("screening: refused, the module was not run")
+            print("\n".join("  " + p for p in problems))
+            print("verdict: REJECTED")
             return 1
-        print("static gate: passed")
+        print("screening: passed")
     t0 = time.time()
     with tempfile.TemporaryDirectory() as td:
-        out = os.path.join(td, "outputs")
-        try:
-            p = subprocess.run([sys.executable, os.path.abspath(__file__), "--child", opname, kpath, out],
-                               timeout=a.timeout)
-            rc = p.returncode
-        except subprocess.TimeoutExpired:
-            rc = "timeout"
-        if rc != 0 or not os.path.exists(out + ".json"):
-            print(f"child process failed ({rc}) before saving its outputs\n=> REJECTED")
-            return 1
-        rep = judge(opname, out)
-    rep.update(kernel=a.kernel, op=opname, seconds=round(time.time() - t0, 1))
-    print(summary(rep))
+        status = run_worker(opname, path, td, a.timeout, a.device)
+        rep = assess(opname, td, a.device)
+    rep.update(kernel=a.kernel, worker_exit=status, seconds=round(time.time() - t0, 1))
+    if status != 0:
+        print(f"worker process ended with status {status}; unfinished cases count as failed")
+    print(render(rep))
     print(f"({rep['seconds']} s)", flush=True)
     if a.json:
-        json.dump(rep, open(a.json, "w"), indent=1, default=str)
+        with open(a.json, "w") as f:
+            json.dump(rep, f, indent=1, default=str)
     return 0 if rep["verdict"] == "CORRECT" else 1
 
 

@@ -2,8 +2,8 @@
 
 Numerically sound on every call: fp32 scores, max-subtracted softmax per chunk of keys and an exact log-sum-exp
 merge of the chunks.  But the keys are cut into B + 1 chunks, one more than the batch has requests, so the
-rounding of a request's output depends on how many requests share the call.  L1-L3 and the extra cases pass; only
-L4 (a row alone against the same row in the batch, bit for bit) rejects it.  It uses no libvmk kernel: run the
+rounding of a request's output depends on how many requests share the call.  L1, L2, L3, X and CFG accept it;
+only L4 (a row alone against the same row in the batch, byte for byte) rejects it.  It uses no libvmk kernel: run the
 verifier with --skip-gate."""
 import math
 

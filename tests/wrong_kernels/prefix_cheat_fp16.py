@@ -1,10 +1,11 @@
-"""DELIBERATELY WRONG kernel for op `prefix` (a verifier calibration fixture; restates the reference's
-wrong_kernels/prefix_cheat_fp16.py:1-33 as a PyTorch composition).
+"""Calibration fixture for op `prefix`: a kernel that is wrong on purpose, and must be REJECTED.
 
-The "optimisation": the shared-prefix cascade keeps scores, probabilities and softmax sums in fp16 (sums are
-accumulated block by block with an fp16 rounding after every block).  It matches the standard op at the nominal
-shape, but its error against the float64 reference grows with context length: layers 2 and 3 reject it.
-It uses no libvmk kernel: run the verifier with --skip-gate."""
+Its flaw: half precision where the softmax needs single.  Scores are rounded to fp16 before the exponentials,
+the probabilities are fp16, and each softmax sum is a running fp16 total rounded again after every 64-key block
+(the reference's calibration set carries the same idea in wrong_kernels/prefix_cheat_fp16.py).  On the nominal
+shape the rounding stays under L1's 1e-2 tolerance; over longer contexts the accumulated rounding exceeds twice
+the standard op's error, so L3 (and some L2 cases) reject it.  Plain torch code, no libvmk call: verify it with
+--skip-gate."""
 import math
 
 import torch

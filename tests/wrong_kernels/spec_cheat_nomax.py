@@ -1,9 +1,10 @@
-"""DELIBERATELY WRONG kernel for op `spec` (a verifier calibration fixture; restates the reference's
-wrong_kernels/spec_cheat_nomax.py:1-28 as a PyTorch composition).
+"""Calibration fixture for op `spec`: a kernel that is wrong on purpose, and must be REJECTED.
 
-The "optimisation": softmax without subtracting the running maximum, exponentials in fp32.  On ordinary inputs the
-result matches (L1 and L3 pass); with large scores exp() overflows and the output is NaN where the float64 reference
-is finite, so the fuzzing layer rejects it.  It uses no libvmk kernel: run the verifier with --skip-gate."""
+Its flaw: the exponentials of the softmax are taken of the raw scaled scores, with no maximum subtracted first
+(the reference's calibration set has the same flaw, wrong_kernels/spec_cheat_nomax.py).  With unit-scale inputs
+exp() stays in float32 range and the outputs agree with the standard op and with float64, so layers L1 and L3
+accept it.  The fuzz case with inputs scaled by 8 drives exp() past float32's range: inf / inf gives NaN where
+float64 is finite, and L2 rejects it.  Plain torch code, no libvmk call: verify it with --skip-gate."""
 import math
 
 import torch

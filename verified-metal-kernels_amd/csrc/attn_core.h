@@ -536,8 +536,9 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
 //
 // Up to 32 partials (every bench shape: 8-32), the O rows are loaded into registers together with the m/l, before
 // the maximum is known, so the merge waits for one round of loads instead of three.  The H loads are unconditional
-// (slots past nparts reload the last partial, never used) so that they issue back to back.  Both forms add the same
-// terms in the same order (partial 0 first), so they give the same bits.
+// (slots past nparts reload the last partial, never used) so that they issue back to back; nparts >= 1 here, which
+// combine_row guarantees.  Both forms add the same terms in the same order (partial 0 first), so they give the same
+// bits.
 template <int NT, int PER, int H, class Part, class E>
 __device__ __forceinline__ void combine_row_held(int nparts, Part part, E* out) {
   __shared__ float sw[H], sl[H], red[NT / 64];
@@ -593,6 +594,12 @@ __device__ __forceinline__ void combine_row_held(int nparts, Part part, E* out) 
 template <int NT, int PER, class Part, class E>
 __device__ __forceinline__ void combine_row(int nparts, Part part, E* out) {
   static_assert(NT >= 32, "one thread per held partial's m/l");
+  if (nparts <= 0) {                                 // uniform: no partial to merge, and none is read
+    // The softmax of no keys is 0 / 0.
+#pragma unroll
+    for (int k = 0; k < PER; ++k) out[threadIdx.x + k * NT] = (E)__builtin_nanf("");
+    return;
+  }
   if (nparts <= 8) return combine_row_held<NT, PER, 8>(nparts, part, out);
   if (nparts <= 16) return combine_row_held<NT, PER, 16>(nparts, part, out);
   if (nparts <= 32) return combine_row_held<NT, PER, 32>(nparts, part, out);

@@ -11,13 +11,14 @@
 //   glist, ekey, epos : B x Ls select_scan's per-slice compacted lists; gcnt, ecnt: their lengths
 //   po/pml : attention partials [b][head block][chunk][32][512] and [..][32][2]
 #include "attn_core.h"
+#include "select_math.h"
 #include "vmk_internal.h"
 
 namespace vmk {
 
 constexpr int kH = 128, kDK = 576, kDC = 512, kHI = 64, kDI = 128, kTopK = 2048;
-constexpr int kBins = 8192;        // first radix digit: key bits 31..19
-constexpr int kCBins = 256;        // coarse bins of the first digit (key bits 31..24)
+constexpr int kBins = kSelBins;    // first radix digit: key bits 31..19
+constexpr int kCBins = kSelCBins;  // coarse bins of the first digit (key bits 31..24)
 constexpr int kIdxWG = 1024;       // positions per indexer workgroup (8 waves x 4 tiles of 32)
 constexpr int kIdxWaves = 8;       // two waves per SIMD hide each other's LDS and MFMA latencies
 constexpr int kIdxStages = 2;      // private DMA ring stages per indexer wave
@@ -90,7 +91,8 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
 }
 
 // Finds, in hist[0..nbins) (nbins a multiple of NT), the bin holding the need-th largest element: out[0] = bin,
-// out[1] = need minus the count strictly above that bin.  Every thread of the block must call it.
+// out[1] = need minus the count strictly above that bin.  Every thread of the block must call it.  The per-thread
+// arithmetic is select_math.h's, which vmk_debug_select_threshold replays on the host.
 template <int NT>
 __device__ void find_threshold(const uint32_t* hist, int nbins, uint32_t need, uint32_t* red, uint32_t* out) {
   // Defaults (bin 0) for a histogram that holds fewer than `need` elements, so callers that index with out[0]
@@ -100,22 +102,15 @@ __device__ void find_threshold(const uint32_t* hist, int nbins, uint32_t need, u
     out[1] = 0;
   }
   const int per = nbins / NT;
-  const int lo = (NT - 1 - threadIdx.x) * per;      // thread 0 owns the highest bins: a prefix scan runs top-down
+  const int lo = threshold_range_lo(threadIdx.x, NT, per);   // a prefix scan over thread ids runs top-down
   uint32_t local = 0;
   for (int i = 0; i < per; ++i) local += hist[lo + i];
   uint32_t total;
   const uint32_t above = block_excl_scan<NT>(local, red, &total);
-  if (above < need && above + local >= need) {
-    uint32_t acc = above;
-    for (int i = per - 1; i >= 0; --i) {
-      const uint32_t c = hist[lo + i];
-      if (acc + c >= need) {
-        out[0] = lo + i;
-        out[1] = need - acc;
-        break;
-      }
-      acc += c;
-    }
+  Threshold t;
+  if (threshold_in_range(hist, lo, per, above, need, &t)) {
+    out[0] = t.bin;
+    out[1] = t.rest;
   }
   __syncthreads();
 }
@@ -270,7 +265,7 @@ __global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
   __syncthreads();
   find_threshold<256>(cnt, kCBins, kTopK, red, thr);
   if (tid < 64) {
-    const uint32_t* fine = a.hist + (size_t)b * kBins + min(thr[0], (uint32_t)kCBins - 1) * 32;
+    const uint32_t* fine = a.hist + (size_t)b * kBins + coarse_bin_clamped(thr[0]) * 32;
     uint32_t v = tid < 32 ? fine[31 - tid] : 0u;            // lane i: fine bin 31 - i (top first)
     uint32_t x = v;                                          // inclusive prefix from the top
 #pragma unroll
@@ -278,7 +273,7 @@ __global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
       const uint32_t y = __shfl_up(x, o, 64);
       if ((tid & 63) >= o) x += y;
     }
-    if (tid < 32 && x >= thr[1] && x - v < thr[1]) b1s = thr[0] * 32 + 31 - tid;
+    if (tid < 32 && fine_hit(x, v, thr[1])) b1s = fine_bin(thr[0], tid);
   }
   __syncthreads();
   const int nv = n - p0;                           // positions p0 + i with i < nv are valid
@@ -626,7 +621,7 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   // which the combine does not read.
   const int* ip = a.idx + (size_t)b * kTopK;
   const int sel = ip[kbeg + (int)(threadIdx.x & (kChunk - 1))];
-  const int cnt = min(a.cnt[b], kTopK);
+  const int cnt = min(max(a.cnt[b], 0), kTopK);     // a caller's count outside [0, kTopK] is clamped
   const int kend = max(kbeg, min(cnt, kbeg + kChunk));
   const int ntiles = (kend - kbeg + kTile - 1) / kTile;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -678,7 +673,7 @@ template <class E>
 __global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
   const int bh = blockIdx.x;
   const int b = bh / kH, head = bh % kH, hb = head / 32, hr = head % 32;
-  const int cnt = min(a.cnt[b], kTopK);
+  const int cnt = min(max(a.cnt[b], 0), kTopK);     // as in dsa_attn_kernel; cnt = 0 merges no chunk (NaN)
   const int nch = (cnt + kChunk - 1) / kChunk;
   const size_t item0 = ((size_t)b * 4 + hb) * kNChunk;
   combine_row<256, 2>(nch,
@@ -868,4 +863,36 @@ extern "C" int vmk_dsa_decode_bf16(const void* q, const void* kv, const void* iq
                                    const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L,
                                    void* workspace, size_t ws_bytes, void* stream) {
   return dsa_decode<bf16x8>(q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace, ws_bytes, stream);
+}
+
+// Host replay of select_scan's threshold-bucket search on histograms in host memory (a test hook; no GPU work):
+// the coarse search as find_threshold<256> runs it (256 thread ranges of one bin, scanned from the top), then the
+// fine bin as the first wave picks it.  out[0] = coarse bin, out[1] = picks left in it, out[2] = fine bucket b1
+// (0 when no fine bin qualifies, as in the kernel).  Returns 1 on a null pointer.
+extern "C" int vmk_debug_select_threshold(const uint32_t* coarse_hist, const uint32_t* fine_hist, uint32_t need,
+                                          uint32_t* out) {
+  using namespace vmk;
+  VMK_CHECK(coarse_hist && fine_hist && out, "null pointer argument");
+  uint32_t thr[2] = {0, 0};
+  uint32_t above = 0;
+  for (int tid = 0; tid < kCBins; ++tid) {         // thread order = exclusive-scan order
+    const int lo = threshold_range_lo(tid, kCBins, 1);
+    Threshold t;
+    if (threshold_in_range(coarse_hist, lo, 1, above, need, &t)) {
+      thr[0] = t.bin;
+      thr[1] = t.rest;
+    }
+    above += coarse_hist[lo];
+  }
+  const uint32_t* fine = fine_hist + coarse_bin_clamped(thr[0]) * 32;
+  uint32_t b1 = 0, incl = 0;
+  for (int lane = 0; lane < 32; ++lane) {
+    const uint32_t v = fine[31 - lane];
+    incl += v;
+    if (fine_hit(incl, v, thr[1])) b1 = fine_bin(thr[0], lane);
+  }
+  out[0] = thr[0];
+  out[1] = thr[1];
+  out[2] = b1;
+  return 0;
 }

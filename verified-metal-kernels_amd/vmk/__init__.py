@@ -6,4 +6,4 @@ tensors on a ROCm device; every call launches on torch's current stream and retu
 """
 from .lib import VmkError, load  # noqa: F401
 from .api import (spec_verify, decode, prefix_decode, prefix_decode_paged, dsa_decode,  # noqa: F401
-                  dsa_indexer_select, dsa_sparse_mla, workspace, device_ok)
+                  dsa_indexer_select, dsa_sparse_mla, workspace, reserve_workspace, device_ok)

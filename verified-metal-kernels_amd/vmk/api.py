@@ -1,15 +1,24 @@
 """torch-facing wrappers of the libvmk C-ABI: argument checks, output and workspace allocation, stream plumbing.
 
 Every wrapper launches on `torch.cuda.current_stream()` of the inputs' device and returns without synchronising.
-Workspaces come from one cached byte buffer per device that only grows; calls that overlap on two streams of one
-device would share it, so they must be ordered by the caller.
+Arguments are checked in this order: types, dtypes and ranks, then shapes against each other, then that every
+tensor is on a ROCm device, so a wrongly shaped tensor is refused before any GPU work.
+
+Workspaces come from one cached byte buffer per device.  Calls that overlap on two streams of one device would
+share it, so they must be ordered by the caller.  The buffer only grows; a buffer it outgrows is kept alive until
+the process ends, because a HIP graph captured before the growth still addresses it.  Growth is refused while the
+current stream is capturing (`reserve_workspace` beforehand, or one eager call of the largest shape, avoids it).
+After a failed call the buffer is set aside the same way and the next call starts from a fresh zeroed one, since a
+call that stops half-way can leave the workspace head (which must stay zero between calls) non-zero.
 """
 import torch
 
 from . import lib
 
 _ws = {}
+_retired = []          # outgrown or possibly dirty workspaces, kept alive for graphs captured over them
 _dev_ok = {}
+HEAD_BYTES = 4 << 20   # VMK_WORKSPACE_HEAD of include/vmk.h: must be zero before a call, is zero after it
 
 
 def device_ok(device):
@@ -25,18 +34,40 @@ def device_ok(device):
     return True
 
 
-def workspace(nbytes, device):
-    """A cached uint8 buffer of at least `nbytes` on `device` (grown, never shrunk).
-
-    Allocated zeroed: libvmk requires the workspace head (its first 4 MiB) to be zero before the first call, and
-    every call leaves it zero again."""
+def _dev_index(device):
     dev = torch.device(device)
-    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    return dev.index if dev.index is not None else torch.cuda.current_device()
+
+
+def workspace(nbytes, device):
+    """A cached uint8 buffer of at least `nbytes` on `device`, allocated zeroed (the head must start at zero)."""
+    key = _dev_index(device)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=dev)
+        if torch.cuda.is_current_stream_capturing():
+            raise lib.VmkError(f"the libvmk workspace would have to grow to {int(nbytes)} bytes during HIP graph "
+                               "capture; call vmk.reserve_workspace (or the op once, eagerly) before capturing")
+        if buf is not None:
+            _retired.append(buf)
+        buf = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=torch.device("cuda", key))
         _ws[key] = buf
     return buf
+
+
+def reserve_workspace(nbytes, device="cuda"):
+    """Grows the cached workspace of `device` to at least `nbytes` now (before a HIP graph capture)."""
+    return workspace(nbytes, device)
+
+
+def _launch(name, ws, *args):
+    """Calls entry point `name`; on failure the workspace `ws` is set aside before the error propagates."""
+    try:
+        lib.call(name, *args)
+    except lib.VmkError:
+        key = ws.device.index
+        if _ws.get(key) is ws:
+            _retired.append(_ws.pop(key))
+        raise
 
 
 def _stream(t):
@@ -48,16 +79,30 @@ def ctypes_ptr(x):
 
 
 def _need(t, name, dtype, ndim):
+    """Type, dtype, rank and layout of one tensor argument (its device is checked later, by `_resident`)."""
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
     if t.dim() != ndim:
         raise ValueError(f"{name} must have {ndim} dims, got shape {tuple(t.shape)}")
-    if not t.is_cuda:
-        raise ValueError(f"{name} must be on a ROCm device")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
+
+
+def _resident(**tensors):
+    """Every given tensor (None skipped) is on the same ROCm device; then that device is checked once."""
+    dev = None
+    for name, t in tensors.items():
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be on a ROCm device")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, the other arguments on {dev}")
+    device_ok(dev)
 
 
 _SUFFIX = {torch.float16: "", torch.bfloat16: "_bf16"}
@@ -84,17 +129,17 @@ def spec_verify(q, k, v, words, out=None):
     Hkv, L = k.shape[1], k.shape[2]
     if tuple(k.shape) != (B, Hkv, L, D) or tuple(v.shape) != tuple(k.shape):
         raise ValueError(f"k/v shape {tuple(k.shape)}/{tuple(v.shape)} do not match q {tuple(q.shape)}")
-    if tuple(words.shape[:2]) != (B, kd):
-        raise ValueError(f"bits shape {tuple(words.shape)} does not match (B, kd) = {(B, kd)}")
-    device_ok(q.device)
+    if tuple(words.shape) != (B, kd, (kd + 31) // 32):
+        raise ValueError(f"bits shape {tuple(words.shape)} is not (B, kd, ceil(kd/32)) = {(B, kd, (kd + 31) // 32)}")
+    _resident(q=q, k=k, v=v, bits=words, out=out)
     if out is None:
         out = torch.empty_like(q)
     ws_n = lib.load().vmk_spec_workspace_size(B, kd, Hq, Hkv, D, L)
     if ws_n == 0:
         raise lib.VmkError(f"unsupported spec shape B={B} kd={kd} Hq={Hq} Hkv={Hkv} D={D} L={L}")
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_spec_verify" + sfx, q.data_ptr(), k.data_ptr(), v.data_ptr(), words.data_ptr(), out.data_ptr(),
-             B, kd, Hq, Hkv, D, L, words.shape[2], ws.data_ptr(), ws.numel(), _stream(q))
+    _launch("vmk_spec_verify" + sfx, ws, q.data_ptr(), k.data_ptr(), v.data_ptr(), words.data_ptr(), out.data_ptr(),
+            B, kd, Hq, Hkv, D, L, words.shape[2], ws.data_ptr(), ws.numel(), _stream(q))
     return out
 
 
@@ -113,15 +158,15 @@ def decode(q, k, v, lens=None, out=None):
         _need(lens, "lens", torch.int32, 1)
         if lens.shape[0] != B:
             raise ValueError("lens must have B entries")
-    device_ok(q.device)
+    _resident(q=q, k=k, v=v, lens=lens, out=out)
     if out is None:
         out = torch.empty_like(q)
     ws_n = lib.load().vmk_decode_workspace_size(B, Hq, Hkv, D, L)
     if ws_n == 0:
         raise lib.VmkError(f"unsupported decode shape B={B} Hq={Hq} Hkv={Hkv} D={D} L={L}")
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_decode" + sfx, q.data_ptr(), k.data_ptr(), v.data_ptr(), 0 if lens is None else lens.data_ptr(),
-             out.data_ptr(), B, Hq, Hkv, D, L, ws.data_ptr(), ws.numel(), _stream(q))
+    _launch("vmk_decode" + sfx, ws, q.data_ptr(), k.data_ptr(), v.data_ptr(), 0 if lens is None else lens.data_ptr(),
+            out.data_ptr(), B, Hq, Hkv, D, L, ws.data_ptr(), ws.numel(), _stream(q))
     return out
 
 
@@ -145,16 +190,16 @@ def prefix_decode(q, kp, vp, ks, vs, slens=None, out=None):
         _need(slens, "slens", torch.int32, 1)
         if slens.shape[0] != N:
             raise ValueError("slens must have N entries")
-    device_ok(q.device)
+    _resident(q=q, kp=kp, vp=vp, ks=ks, vs=vs, slens=slens, out=out)
     if out is None:
         out = torch.empty_like(q)
     ws_n = lib.load().vmk_prefix_workspace_size(N, Hq, Hkv, D, P, S, 0 if slens is None else 1)
     if ws_n == 0:
         raise lib.VmkError(f"unsupported prefix shape N={N} Hq={Hq} Hkv={Hkv} D={D} P={P} S={S}")
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_prefix_decode" + sfx, q.data_ptr(), kp.data_ptr(), vp.data_ptr(), ks.data_ptr(), vs.data_ptr(),
-             0 if slens is None else slens.data_ptr(), out.data_ptr(), N, Hq, Hkv, D, P, S,
-             0 if slens is None else 1, ws.data_ptr(), ws.numel(), _stream(q))
+    _launch("vmk_prefix_decode" + sfx, ws, q.data_ptr(), kp.data_ptr(), vp.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+            0 if slens is None else slens.data_ptr(), out.data_ptr(), N, Hq, Hkv, D, P, S,
+            0 if slens is None else 1, ws.data_ptr(), ws.numel(), _stream(q))
     return out
 
 
@@ -180,7 +225,8 @@ def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=N
         if slens.shape[0] != N:
             raise ValueError("slens must have N entries")
     P, max_sp = prefix_pages.shape[0] * ps, suffix_pages.shape[1]
-    device_ok(q.device)
+    _resident(q=q, k_pages=k_pages, v_pages=v_pages, prefix_pages=prefix_pages, suffix_pages=suffix_pages,
+              slens=slens, out=out)
     if out is None:
         out = torch.empty_like(q)
     ws_n = lib.load().vmk_prefix_paged_workspace_size(N, Hq, Hkv, D, P, ps, max_sp)
@@ -188,94 +234,117 @@ def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=N
         raise lib.VmkError(f"unsupported paged prefix shape N={N} Hq={Hq} Hkv={Hkv} D={D} P={P} page_size={ps} "
                            f"max_suffix_pages={max_sp}")
     ws = workspace(ws_n, q.device)
-    lib.call("vmk_prefix_decode_paged" + sfx, q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
-             prefix_pages.data_ptr() if P else 0, suffix_pages.data_ptr() if max_sp else 0,
-             0 if slens is None else slens.data_ptr(), out.data_ptr(), N, Hq, Hkv, D, num_pages, ps, P, max_sp,
-             ws.data_ptr(), ws.numel(), _stream(q))
+    _launch("vmk_prefix_decode_paged" + sfx, ws, q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
+            prefix_pages.data_ptr() if P else 0, suffix_pages.data_ptr() if max_sp else 0,
+            0 if slens is None else slens.data_ptr(), out.data_ptr(), N, Hq, Hkv, D, num_pages, ps, P, max_sp,
+            ws.data_ptr(), ws.numel(), _stream(q))
     return out
 
 
 DSA_H, DSA_DK, DSA_DC, DSA_HI, DSA_DI, DSA_TOPK = 128, 576, 512, 64, 128, 2048
 
 
-def _dsa_shapes(q, kv, iq, ik, w, lens):
-    dt, _ = _elem(q)
-    _need(q, "q", dt, 3)
-    _need(kv, "kv", dt, 3)
-    _need(iq, "iq", dt, 3)
-    _need(ik, "ik", dt, 3)
-    _need(w, "w", torch.float32, 2)
-    B, L = kv.shape[0], kv.shape[1]
-    if tuple(q.shape) != (B, DSA_H, DSA_DK) or kv.shape[2] != DSA_DK:
-        raise ValueError(f"q {tuple(q.shape)} / kv {tuple(kv.shape)} must be (B,128,576) / (B,L,576)")
-    if tuple(iq.shape) != (B, DSA_HI, DSA_DI) or tuple(ik.shape) != (B, L, DSA_DI) or tuple(w.shape) != (B, DSA_HI):
-        raise ValueError("iq (B,64,128), ik (B,L,128), w (B,64) expected")
-    if lens is not None:
-        _need(lens, "lens", torch.int32, 1)
-        if lens.shape[0] != B:
-            raise ValueError("lens must have B entries")
-    return B, L
-
-
-def dsa_indexer_select(iq, ik, w, lens=None, idx=None, cnt=None):
-    """Indexer scores + exact top-2048 per request; iq/ik both fp16 or both bf16, w fp32.  Returns idx (B, 2048)
-    int32 (unordered, first cnt[b] valid) and cnt (B,) int32."""
-    dt, sfx = _elem(iq)
+def _dsa_indexer_shapes(iq, ik, w, lens):
+    """Checks of the indexer inputs; returns (B, L)."""
+    dt, _ = _elem(iq)
     _need(iq, "iq", dt, 3)
     _need(ik, "ik", dt, 3)
     _need(w, "w", torch.float32, 2)
     B, L = ik.shape[0], ik.shape[1]
     if tuple(iq.shape) != (B, DSA_HI, DSA_DI) or tuple(ik.shape) != (B, L, DSA_DI) or tuple(w.shape) != (B, DSA_HI):
-        raise ValueError("iq (B,64,128), ik (B,L,128), w (B,64) expected")
+        raise ValueError(f"iq {tuple(iq.shape)}, ik {tuple(ik.shape)}, w {tuple(w.shape)}: expected (B,64,128), "
+                         "(B,L,128), (B,64)")
     if lens is not None:
         _need(lens, "lens", torch.int32, 1)
-    device_ok(ik.device)
+        if lens.shape[0] != B:
+            raise ValueError(f"lens has {lens.shape[0]} entries, expected B = {B}")
+    return B, L
+
+
+def _dsa_attention_shapes(q, kv, B):
+    """Checks of the attention inputs against B; returns L."""
+    dt, _ = _elem(q)
+    _need(q, "q", dt, 3)
+    _need(kv, "kv", dt, 3)
+    if tuple(q.shape) != (B, DSA_H, DSA_DK) or kv.shape[0] != B or kv.shape[2] != DSA_DK:
+        raise ValueError(f"q {tuple(q.shape)} / kv {tuple(kv.shape)}: expected (B,128,576) / (B,L,576), B = {B}")
+    return kv.shape[1]
+
+
+def _selection_shapes(idx, cnt, B):
+    _need(idx, "idx", torch.int32, 2)
+    _need(cnt, "cnt", torch.int32, 1)
+    if tuple(idx.shape) != (B, DSA_TOPK) or tuple(cnt.shape) != (B,):
+        raise ValueError(f"idx {tuple(idx.shape)} / cnt {tuple(cnt.shape)}: expected ({B}, 2048) / ({B},)")
+
+
+def dsa_indexer_select(iq, ik, w, lens=None, idx=None, cnt=None):
+    """Indexer scores + exact top-2048 per request; iq/ik both fp16 or both bf16, w fp32.  Returns idx (B, 2048)
+    int32 (unordered, first cnt[b] valid) and cnt (B,) int32."""
+    _, sfx = _elem(iq)
+    B, L = _dsa_indexer_shapes(iq, ik, w, lens)
+    if idx is not None or cnt is not None:
+        if idx is None or cnt is None:
+            raise ValueError("give both idx and cnt, or neither")
+        _selection_shapes(idx, cnt, B)
+    _resident(iq=iq, ik=ik, w=w, lens=lens, idx=idx, cnt=cnt)
     if idx is None:
         idx = torch.empty(B, DSA_TOPK, dtype=torch.int32, device=ik.device)
-    if cnt is None:
         cnt = torch.empty(B, dtype=torch.int32, device=ik.device)
-    ws_n = lib.load().vmk_dsa_workspace_size(B, L)
-    ws = workspace(ws_n, ik.device)
-    lib.call("vmk_dsa_indexer_select" + sfx, iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
-             0 if lens is None else lens.data_ptr(), idx.data_ptr(), cnt.data_ptr(), B, L, ws.data_ptr(),
-             ws.numel(), _stream(ik))
+    ws = workspace(lib.load().vmk_dsa_workspace_size(B, L), ik.device)
+    _launch("vmk_dsa_indexer_select" + sfx, ws, iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
+            0 if lens is None else lens.data_ptr(), idx.data_ptr(), cnt.data_ptr(), B, L, ws.data_ptr(),
+            ws.numel(), _stream(ik))
     return idx, cnt
 
 
 def dsa_sparse_mla(q, kv, idx, cnt, out=None):
-    """Sparse absorbed-MLA attention of q (B,128,576) over rows kv[b, idx[b, :cnt[b]]], q/kv both fp16 or both bf16.
-    Returns (B,128,512) of q's dtype."""
+    """Sparse absorbed-MLA attention of q (B,128,576) over rows kv[b, idx[b, :cnt[b]]], q/kv both fp16 or both bf16;
+    idx (B, 2048) int32, cnt (B,) int32 (clamped to [0, 2048]; a request with cnt 0 gets NaN rows).  Returns
+    (B,128,512) of q's dtype."""
     dt, sfx = _elem(q)
-    _need(q, "q", dt, 3)
-    _need(kv, "kv", dt, 3)
     _need(idx, "idx", torch.int32, 2)
-    _need(cnt, "cnt", torch.int32, 1)
-    B, L = kv.shape[0], kv.shape[1]
-    device_ok(q.device)
+    B = idx.shape[0]
+    L = _dsa_attention_shapes(q, kv, B)
+    _selection_shapes(idx, cnt, B)
+    if out is not None:
+        _need(out, "out", dt, 3)
+        if tuple(out.shape) != (B, DSA_H, DSA_DC):
+            raise ValueError(f"out {tuple(out.shape)}: expected ({B}, 128, 512)")
+    _resident(q=q, kv=kv, idx=idx, cnt=cnt, out=out)
     if out is None:
         out = torch.empty(B, DSA_H, DSA_DC, dtype=dt, device=q.device)
-    ws_n = lib.load().vmk_dsa_workspace_size(B, L)
-    ws = workspace(ws_n, q.device)
-    lib.call("vmk_dsa_sparse_mla" + sfx, q.data_ptr(), kv.data_ptr(), idx.data_ptr(), cnt.data_ptr(), out.data_ptr(),
-             B, L, ws.data_ptr(), ws.numel(), _stream(q))
+    ws = workspace(lib.load().vmk_dsa_workspace_size(B, L), q.device)
+    _launch("vmk_dsa_sparse_mla" + sfx, ws, q.data_ptr(), kv.data_ptr(), idx.data_ptr(), cnt.data_ptr(),
+            out.data_ptr(), B, L, ws.data_ptr(), ws.numel(), _stream(q))
     return out
 
 
 def dsa_decode(q, kv, iq, ik, w, lens=None, out=None, idx=None, cnt=None):
     """Full DSA decode step (indexer -> top-2048 -> sparse MLA); q, kv, iq, ik all fp16 or all bf16, w fp32.
     Returns out (B,128,512) of q's dtype; the selected indices land in `idx`/`cnt` when given."""
-    B, L = _dsa_shapes(q, kv, iq, ik, w, lens)
     dt, sfx = _elem(q)
-    device_ok(q.device)
+    B, L = _dsa_indexer_shapes(iq, ik, w, lens)
+    if _dsa_attention_shapes(q, kv, B) != L:
+        raise ValueError(f"kv has {kv.shape[1]} positions, ik {L}")
+    if iq.dtype != dt:
+        raise TypeError(f"iq/ik are {iq.dtype}, q/kv {dt}: all four must share one dtype")
+    if out is not None:
+        _need(out, "out", dt, 3)
+        if tuple(out.shape) != (B, DSA_H, DSA_DC):
+            raise ValueError(f"out {tuple(out.shape)}: expected ({B}, 128, 512)")
+    if idx is not None or cnt is not None:
+        if idx is None or cnt is None:
+            raise ValueError("give both idx and cnt, or neither")
+        _selection_shapes(idx, cnt, B)
+    _resident(q=q, kv=kv, iq=iq, ik=ik, w=w, lens=lens, out=out, idx=idx, cnt=cnt)
     if out is None:
         out = torch.empty(B, DSA_H, DSA_DC, dtype=dt, device=q.device)
     if idx is None:
         idx = torch.empty(B, DSA_TOPK, dtype=torch.int32, device=q.device)
-    if cnt is None:
         cnt = torch.empty(B, dtype=torch.int32, device=q.device)
-    ws_n = lib.load().vmk_dsa_workspace_size(B, L)
-    ws = workspace(ws_n, q.device)
-    lib.call("vmk_dsa_decode" + sfx, q.data_ptr(), kv.data_ptr(), iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
-             0 if lens is None else lens.data_ptr(), out.data_ptr(), idx.data_ptr(), cnt.data_ptr(), B, L,
-             ws.data_ptr(), ws.numel(), _stream(q))
+    ws = workspace(lib.load().vmk_dsa_workspace_size(B, L), q.device)
+    _launch("vmk_dsa_decode" + sfx, ws, q.data_ptr(), kv.data_ptr(), iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
+            0 if lens is None else lens.data_ptr(), out.data_ptr(), idx.data_ptr(), cnt.data_ptr(), B, L,
+            ws.data_ptr(), ws.numel(), _stream(q))
     return out

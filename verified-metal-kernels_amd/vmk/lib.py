@@ -19,6 +19,7 @@ _SIGS = {
     "vmk_check_device": [],
     "vmk_debug_mfma32": [_c_vp, _c_vp, _c_vp, _c_vp],
     "vmk_debug_tile": [_c_vp] * 7 + [ctypes.c_float, _c_vp],
+    "vmk_debug_select_threshold": [_c_vp, _c_vp, ctypes.c_uint32, _c_vp],
     "vmk_profile_next": [_c_vp, _c_vp, ctypes.c_int],
     "vmk_spec_workspace_size": [_c_i64] * 6,
     "vmk_spec_verify": [_c_vp] * 5 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],

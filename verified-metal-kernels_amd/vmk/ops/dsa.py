@@ -103,7 +103,7 @@ FUZZ = [(dict(B=1, L=1), "randn"), (dict(B=1, L=2048), "randn"), (dict(B=1, L=20
         (dict(B=2, L=6000), "tiny"), (dict(B=4, L=3000), "ragged")]                       # ops/dsa.py:158-161
 L3_CASES = [(dict(B=1, L=1500), "randn"), (dict(B=1, L=8192), "randn"), (dict(B=1, L=65536), "randn"),
             (dict(B=2, L=8192), "large"), (dict(B=2, L=8192), "needle")]                  # ops/dsa.py:162-163
-EXTRA = [(dict(B=4, L=65536), "randn"), (dict(B=5, L=4100), "ragged"), (dict(B=2, L=6000, dtype="bf16"), "randn")]
+EXTRA = [(dict(B=5, L=4100), "ragged"), (dict(B=2, L=6000, dtype="bf16"), "randn"), (dict(B=65, L=2500), "randn")]
 # Row invariance (L4): every request decoded alone (B = 1) must give the same bits as in the batch.
 L4_CASES = [(dict(B=4, L=65536), "randn"), (dict(B=5, L=4100), "ragged"), (dict(B=3, L=2049), "randn")]
 
