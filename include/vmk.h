@@ -51,6 +51,16 @@ int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mas
                     int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, void* workspace,
                     size_t ws_bytes, void* stream);
 
+/* Allocation-free form of vmk_spec_verify.  No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same inputs,
+ * output and result as vmk_spec_verify (same kernels and plan, so the same bits); the partials go to a static
+ * device array of vmk_spec_noalloc_max_bytes() bytes (64 MiB) that each GPU holds until the process ends, so it
+ * calls no hipMalloc/hipFree.  Shapes whose partials exceed it are rejected (return 1, nothing launched).  All calls
+ * on one GPU share that GPU's array: calls that overlap on one GPU (two streams or threads) race. */
+size_t vmk_spec_noalloc_max_bytes(void);
+int vmk_spec_verify_noalloc(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
+                            int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, void* stream);
+
 /* ---------------------------------------------------------------------------------------------- single-token decode
  * No kernel module of the reference ships this op: it is the plain decode that the reference benchmarks against
  * llama.cpp (llama_cpp/test-backend-ops.patch:79-83: 32 q / 8 kv heads, D = 128) and reports at parity

@@ -215,3 +215,16 @@ def test_select_threshold_stays_in_range_on_inconsistent_histograms():
             c, rest, b1 = _select_threshold(coarse, fine, need)
             assert 0 <= c < 256 and 0 <= b1 < 8192
     assert _select_threshold(np.zeros(256), np.zeros(8192)) == [0, 0, 0]
+
+
+def test_noalloc_entry_point_refuses_oversized_shapes_without_a_gpu():
+    """vmk_spec_verify_noalloc checks its arguments and its scratch limit before any HIP call, so a shape whose
+    partials exceed the static scratch is refused here, on a machine without a GPU (dummy aligned pointers)."""
+    from vmk import lib
+    L = lib.load()
+    assert L.vmk_spec_noalloc_max_bytes() == 64 << 20
+    p = 1 << 20                                        # never dereferenced: the call is refused first
+    rc = L.vmk_spec_verify_noalloc(p, p, p, p, p, 8, 64, 32, 8, 128, 64 << 20, 2, None)
+    assert rc == 1 and b"static scratch" in L.vmk_last_error()
+    rc = L.vmk_spec_verify_noalloc(p, p, p, p, p, 2, 64, 32, 8, 128, 65536, 1, None)   # wrong word count
+    assert rc == 1 and b"ceil(kd/32)" in L.vmk_last_error()

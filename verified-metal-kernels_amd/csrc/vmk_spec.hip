@@ -6,6 +6,8 @@
 #include "attn_core.h"
 #include "vmk_internal.h"
 
+#include <mutex>
+
 namespace vmk {
 
 struct SpecArgs {
@@ -213,10 +215,14 @@ extern "C" size_t vmk_spec_workspace_size(int64_t B, int64_t kd, int64_t Hq, int
 }
 
 // Partial launch (key split or row split by the plan) and LSE-combine launch of one spec/decode call; V is the
-// operand type of the inputs (half8: fp16, bf16x8: bf16).
+// operand type of the inputs (half8: fp16, bf16x8: bf16).  `partials` is the 256-byte aligned region of
+// spec_partials_bytes(p) bytes that receives the partials: every partial the combine reads is written first, so the
+// region needs no initialisation.
+static size_t spec_partials_bytes(const SpecPlan& p) { return (p.po_floats + p.pml_floats) * sizeof(float); }
+
 template <class V>
-static int spec_launch(SpecArgs& a, const SpecPlan& p, void* workspace, hipStream_t s) {
-  a.part_o = (float*)align_up((char*)workspace + kWsHead, 256);
+static int spec_launch(SpecArgs& a, const SpecPlan& p, void* partials, hipStream_t s) {
+  a.part_o = (float*)partials;
   a.part_ml = a.part_o + p.po_floats;
   a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;
   a.sl2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
@@ -238,10 +244,9 @@ static int spec_launch(SpecArgs& a, const SpecPlan& p, void* workspace, hipStrea
   return 0;
 }
 
-template <class V>
-static int spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
-                       int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, void* workspace,
-                       size_t ws_bytes, void* stream) {
+// Host-side argument checks shared by vmk_spec_verify and vmk_spec_verify_noalloc (no HIP call).
+static int spec_check_args(const void* q, const void* k, const void* v, const void* mask_words, void* out,
+                           int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W) {
   VMK_CHECK(q && k && v && mask_words && out, "null pointer argument");
   VMK_CHECK(B > 0 && kd > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/batch sizes");
   VMK_CHECK(D == 128, "only head_dim 128 is supported");
@@ -250,6 +255,14 @@ static int spec_verify(const void* q, const void* k, const void* v, const void* 
   VMK_CHECK(kd <= 32 * kMaskWords, "at most 256 drafts");
   VMK_CHECK((Hq / Hkv) * kd <= 1 << 20 && B * Hkv * L <= (int64_t)1 << 40, "sizes out of range");
   VMK_CHECK(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "tensors must be 16-byte aligned");
+  return 0;
+}
+
+template <class V>
+static int spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
+                       int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, void* workspace,
+                       size_t ws_bytes, void* stream) {
+  if (int rc = spec_check_args(q, k, v, mask_words, out, B, kd, Hq, Hkv, D, L, W)) return rc;
   const size_t need = vmk_spec_workspace_size(B, kd, Hq, Hkv, D, L);
   VMK_CHECK(workspace && ws_bytes >= need, "workspace too small (query vmk_spec_workspace_size)");
   SpecPlan p = spec_plan(B, kd, Hq, Hkv, L);
@@ -258,7 +271,7 @@ static int spec_verify(const void* q, const void* k, const void* v, const void* 
   a.lens = nullptr;
   a.out = (f16*)out;
   a.B = (int)B; a.kd = (int)kd; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = (int)W;
-  return spec_launch<V>(a, p, workspace, (hipStream_t)stream);
+  return spec_launch<V>(a, p, align_up((char*)workspace + kWsHead, 256), (hipStream_t)stream);
 }
 
 // Plain single-token decode: the verify path with one query row per request and no mask (the row's own position is
@@ -284,7 +297,7 @@ static int decode(const void* q, const void* k, const void* v, const void* lens,
   a.lens = (const int*)lens;
   a.out = (f16*)out;
   a.B = (int)B; a.kd = 1; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = 1;
-  return spec_launch<V>(a, p, workspace, (hipStream_t)stream);
+  return spec_launch<V>(a, p, align_up((char*)workspace + kWsHead, 256), (hipStream_t)stream);
 }
 
 extern "C" int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mask_words, void* out,
@@ -309,4 +322,60 @@ extern "C" int vmk_decode_bf16(const void* q, const void* k, const void* v, cons
                                int64_t Hq, int64_t Hkv, int64_t D, int64_t L, void* workspace, size_t ws_bytes,
                                void* stream) {
   return decode<bf16x8>(q, k, v, lens, out, B, Hq, Hkv, D, L, workspace, ws_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------------------------- allocation-free
+// vmk_spec_verify without a workspace argument, for callers that cannot allocate device memory.  The partials go to
+// `scratch`, a file-scope device array that every GPU the library is loaded on holds until the process ends.  Host
+// code never passes the array's name to a kernel (on the host it is only a stand-in for the symbol): the device
+// address comes from hipGetSymbolAddress, looked up once per device with that device current, and kept per device.
+// Every call on one GPU uses that GPU's one array, so calls that overlap on a GPU (two streams, two host threads)
+// race; the array keeps the last call's partials, and no part of it must start at zero (every partial the combine
+// reads is written first).
+namespace vmk {
+constexpr size_t kScratchBytes = (size_t)64 << 20;   // partials of every bench shape (C4: 32.5 MiB)
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+static void* g_scratch_ptr[kScratchDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch` (looked up on the first call on that device); 0 on success.
+static int scratch_address(void** ptr) {
+  int dev = -1;
+  VMK_CHECK_HIP(hipGetDevice(&dev));
+  VMK_CHECK(dev >= 0 && dev < kScratchDevices, "device index beyond the per-device scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    VMK_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    VMK_CHECK(p != nullptr && ((uintptr_t)p & 255u) == 0, "scratch symbol address missing or misaligned");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return 0;
+}
+}  // namespace vmk
+
+extern "C" size_t vmk_spec_noalloc_max_bytes(void) { return vmk::kScratchBytes; }
+
+extern "C" int vmk_spec_verify_noalloc(const void* q, const void* k, const void* v, const void* mask_words, void* out,
+                                       int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L,
+                                       int64_t W, void* stream) {
+  // Every check comes before the first HIP call: a rejected call touches no device.
+  if (int rc = spec_check_args(q, k, v, mask_words, out, B, kd, Hq, Hkv, D, L, W)) return rc;
+  const SpecPlan p = spec_plan(B, kd, Hq, Hkv, L);
+  const size_t need = spec_partials_bytes(p);
+  if (need > kScratchBytes) {
+    set_error("vmk_spec_verify_noalloc: this shape needs %zu bytes of partials, more than the %zu bytes of static "
+              "scratch; call vmk_spec_verify with a workspace instead", need, kScratchBytes);
+    return 1;
+  }
+  void* partials = nullptr;
+  if (int rc = scratch_address(&partials)) return rc;
+  SpecArgs a;
+  a.q = (const f16*)q; a.k = (const f16*)k; a.v = (const f16*)v; a.bits = (const uint32_t*)mask_words;
+  a.lens = nullptr;
+  a.out = (f16*)out;
+  a.B = (int)B; a.kd = (int)kd; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = (int)W;
+  return spec_launch<half8>(a, p, partials, (hipStream_t)stream);
 }

@@ -5,5 +5,5 @@ Host side of the C-ABI library libvmk.so (HIP kernels in ../csrc, declared in in
 tensors on a ROCm device; every call launches on torch's current stream and returns without synchronising.
 """
 from .lib import VmkError, load  # noqa: F401
-from .api import (spec_verify, decode, prefix_decode, prefix_decode_paged, dsa_decode,  # noqa: F401
+from .api import (spec_verify, spec_verify_noalloc, decode, prefix_decode, prefix_decode_paged, dsa_decode,  # noqa: F401
                   dsa_indexer_select, dsa_sparse_mla, workspace, reserve_workspace, device_ok)

@@ -143,6 +143,29 @@ def spec_verify(q, k, v, words, out=None):
     return out
 
 
+def spec_verify_noalloc(q, k, v, words, out):
+    """vmk_spec_verify_noalloc: spec_verify without a workspace (the library's static per-GPU scratch holds the
+    partials), for callers that cannot allocate; fp16 only, `out` (B, kd, Hq, 128) fp16 given by the caller.  Calls
+    that overlap on one GPU race on that scratch.  Shapes whose partials exceed vmk_spec_noalloc_max_bytes() are
+    refused with VmkError."""
+    _need(q, "q", torch.float16, 4)
+    _need(k, "k", torch.float16, 4)
+    _need(v, "v", torch.float16, 4)
+    _need(words, "bits", torch.int32, 3)
+    _need(out, "out", torch.float16, 4)
+    B, kd, Hq, D = q.shape
+    Hkv, L = k.shape[1], k.shape[2]
+    if tuple(k.shape) != (B, Hkv, L, D) or tuple(v.shape) != tuple(k.shape) or tuple(out.shape) != tuple(q.shape):
+        raise ValueError(f"k/v/out shapes {tuple(k.shape)}/{tuple(v.shape)}/{tuple(out.shape)} do not match q "
+                         f"{tuple(q.shape)}")
+    if tuple(words.shape) != (B, kd, (kd + 31) // 32):
+        raise ValueError(f"bits shape {tuple(words.shape)} is not (B, kd, ceil(kd/32)) = {(B, kd, (kd + 31) // 32)}")
+    _resident(q=q, k=k, v=v, bits=words, out=out)
+    lib.call("vmk_spec_verify_noalloc", q.data_ptr(), k.data_ptr(), v.data_ptr(), words.data_ptr(), out.data_ptr(),
+             B, kd, Hq, Hkv, D, L, words.shape[2], _stream(q))
+    return out
+
+
 def decode(q, k, v, lens=None, out=None):
     """Single-token decode: q (B, Hq, 128), k/v (B, Hkv, L, 128), all fp16 or all bf16; lens (B,) int32 or None (all
     L in use).  Returns out (B, Hq, 128) of q's dtype."""

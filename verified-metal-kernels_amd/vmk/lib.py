@@ -23,6 +23,8 @@ _SIGS = {
     "vmk_profile_next": [_c_vp, _c_vp, ctypes.c_int],
     "vmk_spec_workspace_size": [_c_i64] * 6,
     "vmk_spec_verify": [_c_vp] * 5 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
+    "vmk_spec_noalloc_max_bytes": [],
+    "vmk_spec_verify_noalloc": [_c_vp] * 5 + [_c_i64] * 7 + [_c_vp],
     "vmk_decode_workspace_size": [_c_i64] * 5,
     "vmk_decode": [_c_vp] * 5 + [_c_i64] * 5 + [_c_vp, _c_sz, _c_vp],
     "vmk_prefix_workspace_size": [_c_i64] * 7,
@@ -41,7 +43,7 @@ _SIGS = {
     "vmk_dsa_sparse_mla": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_decode": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
 }
-_RET = {"vmk_last_error": ctypes.c_char_p, "vmk_spec_workspace_size": _c_sz, "vmk_prefix_workspace_size": _c_sz,
+_RET = {"vmk_last_error": ctypes.c_char_p, "vmk_spec_workspace_size": _c_sz, "vmk_spec_noalloc_max_bytes": _c_sz, "vmk_prefix_workspace_size": _c_sz,
         "vmk_prefix_paged_workspace_size": _c_sz,
         "vmk_dsa_workspace_size": _c_sz, "vmk_decode_workspace_size": _c_sz}
 
