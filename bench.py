@@ -1,22 +1,28 @@
 """Benchmark of the attention ops on one MI355X, in the driver's contract.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs C1,C2,...] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs C1,C2,...] [--no-cpu] [--ab-rounds R]
 
 Prints human-readable progress on stderr and ONE JSON line on stdout.  A "step" is one call of the op on one batch
 of the headline configuration (BASELINE configs[1] = C2, shared-prefix decode at scale); `value` is its achieved
 HBM throughput (algorithmic bytes / time per call, inputs resident in HBM), `ops` holds the same figures for every
-configuration (C1..C5, and this build's D1-D3 decode, P2 paged prefix, C2b bf16).  Method (a counterpart of the
-reference's bench.py:44-140 timing):
+configuration (C1..C5, and this build's D1-D3 decode, P2 paged prefix, C2b bf16).  Method:
   * the kernel's output on the timed inputs is checked against the PyTorch standard op first
     (allclose atol=rtol=1e-2, bench.py:180-192 of the reference), and the inputs are checked for modification;
   * every call reads a different input set, rotating over enough distinct sets (>= 1 GiB in total) that the
     256 MB Infinity Cache cannot serve a repeat;
-  * W untimed warm-up calls, then the per-call time: the K calls captured once in a HIP graph and replayed between
-    two HIP events (synchronised before and after), after 3 replays checked bit for bit against an eager call;
-    `eager` gives the same K calls launched one by one from Python, which adds the host's per-call overhead;
+  * W untimed warm-up calls, then the per-call time: the K calls captured once in a HIP graph, replayed 15 times,
+    each replay between two HIP events (synchronised before and after); the median is `us_per_call`, with p10/p90.
+    Before timing, 3 replays are checked bit for bit against an eager call.  `eager` gives the same K calls
+    launched one by one from Python, which adds the host's per-call overhead;
   * the dominant kernel of each op is bracketed by its own pair of HIP events on its launch stream inside the eager
-    loop (libvmk's vmk_profile_next hook), which gives the roofline figure.
-The CPU baseline is the float64 NumPy oracle (oracle/) on the host, on a bounded sample of the same workload.
+    loop (libvmk's vmk_profile_next hook), which gives the roofline figure;
+  * A/B against the torch standard ops (the reference's headline form, bench.py:99-126, 157-236): on the
+    reference's BENCH_SHAPES and on this build's configurations, the kernel module and every TORCH_REFS op each
+    time a 16-call chain (each call's query is the previous call's output; DSA: [output | rope part of q]) after
+    a 1 GiB cache flush, in R shuffled rounds; reported: medians with p10/p90, and the median over rounds of
+    t(strongest op) / t(kernel), with its p10/p90, and the geomean over BENCH_SHAPES.
+The CPU baseline is the float64 NumPy oracle (oracle/) on the host, on a bounded sample of the same workload, the
+median of 3 runs.
 """
 import argparse
 import json
@@ -139,11 +145,11 @@ def op_bytes_flops(opname, shape, inp_host):
     return total, indexer, dsa.flops(shape)
 
 
-def distinct_sets(opname, inp0, total_bytes):
+def distinct_sets(opname, inp0, total_bytes, count=None):
     """Extra input sets with the same shapes and dtypes (synthetic N(0,1) data made on the GPU), so that the calls
-    of the timed loop rotate over >= 1 GiB of inputs; masks/lengths are shared."""
+    of the timed loop rotate over >= 1 GiB of inputs (or `count` sets in all); masks/lengths are shared."""
     import torch
-    n = max(2, int(math.ceil((1 << 30) / max(total_bytes, 1))))
+    n = count or max(2, int(math.ceil((1 << 30) / max(total_bytes, 1))))
     sets = [inp0]
     big = {"prefix": ("q", "kp", "vp", "ks", "vs"), "spec": ("q", "k", "v"), "dsa": ("q", "kv", "iq", "ik"),
            "decode": ("q", "k", "v"), "prefix_paged": ("q", "k_pages", "v_pages")}[opname]
@@ -157,59 +163,60 @@ def distinct_sets(opname, inp0, total_bytes):
     return sets
 
 
-def cpu_baseline(opname, shape, dist, inp_host, total_bytes):
-    """Times the float64 oracle on a bounded sample of the workload on the host cores; returns a dict."""
+def cpu_baseline(opname, shape, dist, inp_host, total_bytes, runs=3):
+    """Times the float64 oracle on a bounded sample of the workload on the host cores: the median of `runs` runs
+    (one when a run exceeds 60 s), scaled from the sample to a whole call; returns a dict."""
     import oracle
+    host_cpus = os.cpu_count() or 1
     try:
         from threadpoolctl import threadpool_limits, threadpool_info
-        cores = min(16, os.cpu_count() or 1)
+        cores = min(16, host_cpus)          # the GPU box's CPU share for one GPU
         ctx = threadpool_limits(limits=cores)
         blas = [d.get("num_threads") for d in threadpool_info() if d.get("user_api") == "blas"]
     except Exception:  # pragma: no cover - threadpoolctl missing
         import contextlib
-        ctx, cores, blas = contextlib.nullcontext(), os.cpu_count() or 1, []
+        ctx, cores, blas = contextlib.nullcontext(), host_cpus, []
+    sl = lambda x, n: None if x is None else x[:n]
+    if opname == "prefix":
+        N = shape["N"]
+        ns = min(N, 8)
+        sub = {k: inp_host[k][:ns] for k in ("q", "ks", "vs")}
+        sub.update(kp=inp_host["kp"], vp=inp_host["vp"], slens=sl(inp_host.get("slens"), ns))
+        work, scale = (lambda: oracle.prefix.ref64(**sub)), N / ns
+        sample = f"requests 0-{ns - 1} of {N}, time scaled x{N / ns:g}"
+    elif opname == "spec":
+        B = shape["B"]
+        work = lambda: oracle.spec.ref64(inp_host["q"][:1], inp_host["k"][:1], inp_host["v"][:1], inp_host["bits"][:1])
+        scale, sample = B, f"batch 0 of {B}, time scaled x{B}"
+    elif opname == "prefix_paged":
+        N = shape["N"]
+        ns = min(N, 8)
+        sub = dict(inp_host, q=inp_host["q"][:ns], suffix_pages=inp_host["suffix_pages"][:ns],
+                   slens=sl(inp_host.get("slens"), ns))
+        work, scale = (lambda: oracle.prefix_paged.ref64(**sub)), N / ns
+        sample = f"requests 0-{ns - 1} of {N}, time scaled x{N / ns:g}"
+    elif opname == "decode":
+        B = shape["B"]
+        work = lambda: oracle.decode.ref64(inp_host["q"][:1], inp_host["k"][:1], inp_host["v"][:1],
+                                           sl(inp_host.get("lens"), 1))
+        scale, sample = B, f"request 0 of {B}, time scaled x{B}"
+    else:
+        B = shape["B"]
+        work = lambda: oracle.dsa.ref64(inp_host["q"][:1], inp_host["kv"][:1], inp_host["iq"][:1],
+                                        inp_host["ik"][:1], inp_host["w"][:1], None)
+        scale, sample = B, f"request 0 of {B} (scores, top-2048, attention), time scaled x{B}"
+    times = []
     with ctx:
-        if opname == "prefix":
-            N = shape["N"]
-            ns = min(N, 8)
-            sub = {k: inp_host[k][:ns] for k in ("q", "ks", "vs")}
-            sub.update(kp=inp_host["kp"], vp=inp_host["vp"],
-                       slens=None if inp_host.get("slens") is None else inp_host["slens"][:ns])
+        for _ in range(runs):
             t0 = time.perf_counter()
-            oracle.prefix.ref64(**sub)
-            dt = (time.perf_counter() - t0) * N / ns
-            sample = f"requests 0-{ns - 1} of {N}, time scaled x{N / ns:g}"
-        elif opname == "spec":
-            B = shape["B"]
-            t0 = time.perf_counter()
-            oracle.spec.ref64(inp_host["q"][:1], inp_host["k"][:1], inp_host["v"][:1], inp_host["bits"][:1])
-            dt = (time.perf_counter() - t0) * B
-            sample = f"batch 0 of {B}, time scaled x{B}"
-        elif opname == "prefix_paged":
-            N = shape["N"]
-            ns = min(N, 8)
-            sub = dict(inp_host, q=inp_host["q"][:ns], suffix_pages=inp_host["suffix_pages"][:ns],
-                       slens=None if inp_host.get("slens") is None else inp_host["slens"][:ns])
-            t0 = time.perf_counter()
-            oracle.prefix_paged.ref64(**sub)
-            dt = (time.perf_counter() - t0) * N / ns
-            sample = f"requests 0-{ns - 1} of {N}, time scaled x{N / ns:g}"
-        elif opname == "decode":
-            B = shape["B"]
-            t0 = time.perf_counter()
-            oracle.decode.ref64(inp_host["q"][:1], inp_host["k"][:1], inp_host["v"][:1],
-                                None if inp_host.get("lens") is None else inp_host["lens"][:1])
-            dt = (time.perf_counter() - t0) * B
-            sample = f"request 0 of {B}, time scaled x{B}"
-        else:
-            B = shape["B"]
-            t0 = time.perf_counter()
-            oracle.dsa.ref64(inp_host["q"][:1], inp_host["kv"][:1], inp_host["iq"][:1], inp_host["ik"][:1],
-                             inp_host["w"][:1], None)
-            dt = (time.perf_counter() - t0) * B
-            sample = f"request 0 of {B} (scores, top-2048, attention), time scaled x{B}"
+            work()
+            times.append(time.perf_counter() - t0)
+            if times[-1] > 60:
+                break
+    dt = float(np.median(times)) * scale
     return dict(value=round(total_bytes / dt / 1e9, 3), unit="GB/s", us_per_call=round(dt * 1e6, 1), cores=cores,
-                blas_threads=blas, kind="port", sample=sample)
+                host_cpu_count=host_cpus, blas_threads=blas, runs=len(times), kind="port",
+                sample=f"{sample}; median of {len(times)} runs")
 
 
 def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
@@ -255,17 +262,20 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     eager_us = e0.elapsed_time(e1) * 1e3 / steps
     dom_us = sum(hev.elapsed_ms(i) for i in range(steps)) * 1e3 / steps
     hev.close()
-    us = graph_us_per_call(opname, sets, steps)
+    gt = graph_us_per_call(opname, sets, steps)
+    us = gt["median"]
     gbs = total_bytes / us / 1e3
     dom_gbs = dom_bytes / dom_us / 1e3
-    row = dict(op=opname, shape=shape, dist=dist, us_per_call=round(us, 2), gbs=round(gbs, 1),
+    row = dict(op=opname, shape=shape, dist=dist, us_per_call=round(us, 2),
+               us_spread=dict(p10=round(gt["p10"], 2), p90=round(gt["p90"], 2), replays=gt["n"]), gbs=round(gbs, 1),
                pct_peak=round(100 * gbs / PEAK_HBM_GBS, 2), algorithmic_bytes=int(total_bytes),
                tflops=round(flops / us / 1e6, 2), mfma_pct=round(100 * flops / us / 1e6 / PEAK_FP16_TFLOPS, 2),
                eager=dict(us_per_call=round(eager_us, 2), gbs=round(total_bytes / eager_us / 1e3, 1)),
                dominant=dict(kernel=DOMINANT[opname], us=round(dom_us, 2), bytes=int(dom_bytes),
                              gbs=round(dom_gbs, 1), frac=round(dom_gbs / PEAK_HBM_GBS, 4)),
                output_check="ok", distinct_input_sets=len(sets))
-    log(f"[{name}] {us:9.2f} us/call  {gbs:7.1f} GB/s ({row['pct_peak']:.1f}% of 8 TB/s)  [HIP graph of {steps} calls; "
+    log(f"[{name}] {us:9.2f} us/call (p10 {gt['p10']:.2f}, p90 {gt['p90']:.2f})  {gbs:7.1f} GB/s "
+        f"({row['pct_peak']:.1f}% of 8 TB/s)  [median of {gt['n']} replays of a HIP graph of {steps} calls; "
         f"eager loop {eager_us:.2f} us/call]   dominant {DOMINANT[opname]} {dom_us:.2f} us = {dom_gbs:.0f} GB/s")
     if do_cpu:
         row["cpu_baseline"] = cpu_baseline(opname, shape, dist, host, total_bytes)
@@ -276,12 +286,13 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     return row
 
 
-def graph_us_per_call(opname, sets, steps):
+def graph_us_per_call(opname, sets, steps, replays=15):
     """µs per call of the K calls captured once in a HIP graph (torch.cuda.CUDAGraph over the calls' launches on the
-    capture stream, rotating over the same input sets) and replayed once between two events, synchronised before and
-    after: the GPU time of K steps without the Python and launch overhead of an eager loop, which dominates ops of a
-    few µs.  Before timing, the output of the last captured call after each of 3 replays (with eager work and
-    synchronisation in between) must equal an eager call on the same inputs bit for bit."""
+    capture stream, rotating over the same input sets), each replay timed between two events and synchronised:
+    the GPU time of K steps without the Python and launch overhead of an eager loop, which dominates ops of a few
+    µs.  Returns the median, p10 and p90 over `replays` replays.  Before timing, the output of the last captured call
+    after each of 3 replays (with eager work and synchronisation in between) must equal an eager call on the same
+    inputs bit for bit."""
     import torch
     n = steps
     side = torch.cuda.Stream()
@@ -303,13 +314,156 @@ def graph_us_per_call(opname, sets, steps):
             raise SystemExit(f"{opname}: a graph replay differs from the eager call")
         call_op(opname, sets[0])                          # eager work between replays
         torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    g.replay()
-    e1.record()
-    torch.cuda.synchronize()
+    times = []
+    for _ in range(replays):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3 / n)
     del g, outs
-    return e0.elapsed_time(e1) * 1e3 / n
+    return spread(times)
+
+
+def spread(xs):
+    """median, p10 and p90 of a list of timings (nearest-rank percentiles), and how many there are."""
+    t = sorted(xs)
+    rank = lambda p: t[min(len(t) - 1, max(0, int(math.ceil(p * len(t))) - 1))]
+    return dict(median=float(np.median(t)), p10=rank(0.1), p90=rank(0.9), n=len(t))
+
+
+# ------------------------------------------------------------------------------------------------ A/B vs torch
+# The reference's benchmark scores a kernel by its speedup over the strongest standard op, interleaved in shuffled
+# rounds (reference bench.py:99-126, 157-236).  Here the standard ops are the op contracts' PyTorch-ROCm
+# compositions (TORCH_REFS), on the reference's BENCH_SHAPES and on this build's configurations.
+AB_OPS = ("prefix", "spec", "dsa")
+
+
+class CacheFlush:
+    """Writes 1 GiB before each timed chain, which evicts the 256 MB Infinity Cache and every L2."""
+
+    def __init__(self):
+        import torch
+        self.buf = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+
+    def __call__(self):
+        self.buf.fill_(1.0)
+
+
+def ab_chain(opname):
+    """How a chain layer's output becomes the next layer's query: the output itself (prefix, spec: same shape as
+    q), or [output | the layer's rope part of q] for DSA (ops/dsa.py:145-147, chain_torch)."""
+    from vmk.ops import dsa
+    return dsa.chain_torch if opname == "dsa" else (lambda out, kw: out)
+
+
+def ab_inputs(op, shape, dist, keys):
+    """Input sets on the GPU for one shape: set 0 from the op's seeded generator, the others N(0,1) of the same
+    shapes made on the GPU (masks and lengths shared), as many as make about 1.5 GiB of distinct kernel inputs
+    (1 to 8, as the reference's bench.py:171-175); prefix sets also carry the standard ops' cache layouts (kf/vf,
+    ku/vu), built outside the timed region as the reference's generator builds them."""
+    import torch
+    host = op.make_inputs(shape, seed=0, dist=dist)
+    if op.NAME == "dsa":
+        host["lens"] = None                           # the reference benchmarks full caches (bench.py:177-178)
+    s0 = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in host.items()}
+    per_set = sum(v.numel() * v.element_size() for k, v in s0.items() if isinstance(v, torch.Tensor) and k in keys)
+    n = int(max(1, min(8, (3 << 29) // max(per_set, 1))))
+    sets = distinct_sets(op.NAME, s0, 0, count=n)
+    if op.NAME == "prefix":
+        for st in sets:
+            st.update(op.build_layouts(st["kp"], st["vp"], st["ks"], st["vs"]))
+    return sets
+
+
+def ab_runner(fn, layers, chain, flush):
+    """A timed chain: flush, then every layer's call with q taken from the previous layer's output, between two
+    events; returns µs per call."""
+    import torch
+
+    def run():
+        flush()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        q = layers[0]["q"]
+        e0.record()
+        for kw in layers:
+            kw = dict(kw, q=q)
+            q = chain(fn(**kw), kw)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / len(layers)
+    return run
+
+
+def ab_shape(op, shape, dist, rounds, flush, seed):
+    """One shape: output check, then `rounds` shuffled rounds of the kernel module and every standard op."""
+    import random
+    import torch
+    from vmk.ops import KEYS
+    mod = __import__(f"{op.NAME}_mi355x")
+    keys = KEYS[op.NAME]
+    kernel = lambda **kw: mod.kernel(**{k: kw.get(k) for k in keys})
+    sets = ab_inputs(op, shape, dist, keys)
+    n = len(sets)
+    layers = [sets[i % n] for i in range(max(16, n))]
+    std = getattr(op, op.L1_REF)
+    out, ref = kernel(**sets[0]), std(**sets[0])
+    torch.cuda.synchronize()
+    if not torch.allclose(out.float(), ref.float(), atol=1e-2, rtol=1e-2, equal_nan=True):
+        raise SystemExit(f"A/B {op.NAME} {shape}: the kernel differs from {op.L1_REF} on the benchmark inputs")
+    chain = ab_chain(op.NAME)
+    runners = {"kernel": ab_runner(kernel, layers, chain, flush)}
+    runners.update({name: ab_runner(f, layers, chain, flush) for name, f in op.TORCH_REFS.items()})
+    for r in runners.values():                        # warm-up: compile paths, allocator, clocks
+        r()
+    rng = random.Random(seed)
+    times = {name: [] for name in runners}
+    for _ in range(rounds):
+        order = list(runners)
+        rng.shuffle(order)
+        for name in order:
+            times[name].append(runners[name]())
+    refs = [k for k in runners if k != "kernel"]
+    med = {k: spread(v) for k, v in times.items()}
+    strongest = min(refs, key=lambda k: med[k]["median"])
+    ratios = {k: spread([b / a for a, b in zip(times["kernel"], times[k])]) for k in refs}
+    del sets, layers, runners
+    torch.cuda.empty_cache()
+    return dict(shape=shape, dist=dist, distinct_sets=n, chain=max(16, n),
+                median_us={k: round(v["median"], 2) for k, v in med.items()},
+                p10_us={k: round(v["p10"], 2) for k, v in med.items()},
+                p90_us={k: round(v["p90"], 2) for k, v in med.items()},
+                strongest_ref=strongest, speedup_vs_strongest_ref=round(ratios[strongest]["median"], 3),
+                speedup_p10=round(ratios[strongest]["p10"], 3), speedup_p90=round(ratios[strongest]["p90"], 3),
+                speedup_vs_each_ref={k: round(v["median"], 3) for k, v in ratios.items()})
+
+
+def ab_bench(rounds, configs):
+    """The A/B table: per op, every BENCH_SHAPE (geomean of the speedups, as the reference publishes) and every
+    configuration of this build that belongs to the op."""
+    from vmk.ops import OPS
+    flush = CacheFlush()
+    res = {}
+    for opname in AB_OPS:
+        op = OPS[opname]
+        shapes = [(None, s, "randn") for s in op.BENCH_SHAPES]
+        shapes += [(c, s, d) for c, (s, d) in op.CONFIGS.items() if c in configs and "dtype" not in s]
+        rows = []
+        for i, (cname, shape, dist) in enumerate(shapes):
+            log(f"[A/B] {opname} {cname or 'bench shape'} {shape} {dist}")
+            r = ab_shape(op, shape, dist, rounds, flush, seed=i)
+            r["config"] = cname
+            log(f"[A/B]   kernel {r['median_us']['kernel']:.1f} us, {r['strongest_ref']} "
+                f"{r['median_us'][r['strongest_ref']]:.1f} us: {r['speedup_vs_strongest_ref']:.2f}x "
+                f"(p10 {r['speedup_p10']:.2f}, p90 {r['speedup_p90']:.2f})")
+            rows.append(r)
+        sp = [r["speedup_vs_strongest_ref"] for r in rows if r["config"] is None]
+        res[opname] = dict(rounds=rounds, shapes=rows,
+                           geomean_bench_shapes=round(float(np.exp(np.mean(np.log(sp)))), 3),
+                           min_bench_shapes=min(sp), max_bench_shapes=max(sp))
+    del flush
+    return res
 
 
 def measured_traffic(name, dom):
@@ -332,6 +486,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2,C2b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle timings")
+    ap.add_argument("--ab-rounds", type=int, default=10,
+                    help="shuffled rounds of the A/B comparison with the torch standard ops (0: skip it)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="first run a plain streaming kernel that reads BYTES and writes BYTES (torch.bitwise_not "
                          "on int32), the calibration of the PMC traffic counters")
@@ -359,6 +515,13 @@ def main():
         if name in want:
             rows[name] = bench_config(name, opname, shape, dist, a.steps, a.warmup,
                                       do_cpu=not a.no_cpu)
+    ab = ab_bench(a.ab_rounds, want) if a.ab_rounds > 0 else None
+    if ab:
+        for opname, r in ab.items():
+            for sh in r["shapes"]:
+                if sh["config"] in rows:
+                    rows[sh["config"]]["ab"] = {k: sh[k] for k in ("strongest_ref", "speedup_vs_strongest_ref",
+                                                                    "speedup_p10", "speedup_p90", "median_us")}
     head = rows.get(HEADLINE) or next(iter(rows.values()))
     head_name = HEADLINE if HEADLINE in rows else next(iter(rows))
     dom = head["dominant"]
@@ -374,6 +537,9 @@ def main():
                       kernel=dom["kernel"], kernel_us=dom["us"], traffic=measured_traffic(head_name, dom)),
         cpu_baseline={k: v for k, v in head.get("cpu_baseline", {}).items()} or None,
         ops=rows,
+        ab_vs_torch=None if ab is None else {
+            op: dict(geomean_bench_shapes=r["geomean_bench_shapes"], min=r["min_bench_shapes"],
+                     max=r["max_bench_shapes"], rounds=r["rounds"], shapes=r["shapes"]) for op, r in ab.items()},
         device=torch.cuda.get_device_name(0),
     )
     print(json.dumps(line), flush=True)
