@@ -24,15 +24,24 @@ constexpr int kVTileHalfs = 128 * kVStride;
 
 struct RowState {
   floatx16 o[4];
-  float m;   // running max of scaled scores (log2 domain); equal in lanes l and l^32
+  float m;   // running max of scaled scores (log2 domain); equal in lanes l and l^32; -inf before the first
   float l;   // this lane's partial sum of p (the row total is the sum over lanes l and l^32)
+  float mu;  // the subtrahend p = exp2(scaled score - mu) uses: m, or kMuNone while m is -inf
 };
+
+// Subtrahend of a row that has seen no finite score yet: a finite score minus it gives p = +inf, which the
+// overflow check of softmax_update catches, while a masked (-inf) score still gives p = 0.
+constexpr float kMuNone = -1e30f;
+// A lane's sum of one tile's 16 p values at or below this bound keeps every p <= 2^15, inside fp16's range
+// (65504) with a factor 2 to spare; a larger sum, or +inf, sends the tile through the exact path.
+constexpr float kTileSumMax = 32768.f;
 
 __device__ __forceinline__ void row_state_init(RowState& st) {
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) st.o[dt] = floatx16{};
   st.m = kNegInf;
   st.l = 0.f;
+  st.mu = kMuNone;
 }
 
 // Loads are never predicated: every address is clamped in bounds by the caller and out-of-range data is replaced
@@ -98,38 +107,73 @@ __device__ __forceinline__ floatx16 qk_tile(const u32x4 (&kr)[8], const half8 (&
   return acc;
 }
 
-// Online-softmax update of raw scores s (masked keys = -inf); p = exp2(scale * s - m) with m in the scaled (log2)
-// domain, so the scale costs one FMA per score.  Returns P^T operands.
-// The reference point m only moves when a tile's max exceeds it by more than 8 (a factor 256): p = exp2(.) then
-// stays <= 256, which fp16 (or bf16) P and the fp32 sums hold as well as p <= 1, and the O rescale is skipped for
-// the whole wave unless some row moved.  Guard: while a row has seen only -inf, the subtrahend is 0 so exp2(-inf) = 0
-// and a NaN score still yields NaN.  scale must be positive (max commutes with it).  P is rounded to the operand type
-// V of the values it multiplies.
+// Sum of the 16 rounded p values of a lane (the P^T operands), in fp32: dot products with (1, 1) of the packed
+// pairs, so the row sum counts exactly the values the P.V product multiplies.
+__device__ __forceinline__ float rowsum16(const half8 (&pb)[2]) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  float acc = 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2(h2{pb[t][2 * i], pb[t][2 * i + 1]}, h2{1, 1}, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float rowsum16(const bf16x8 (&pb)[2]) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  float acc = 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(b2{pb[t][2 * i], pb[t][2 * i + 1]}, b2{1, 1}, acc, false);
+  return acc;
+}
+
+// p = exp2(scale * s - mu) for a lane's 16 raw scores, rounded to the operand type V as the P^T operands.
 template <class V>
-__device__ __forceinline__ void softmax_update(RowState& st, floatx16& s, float scale, V (&pb)[2]) {
-  float tmax = s[0];
+__device__ __forceinline__ void exp_tile(const floatx16& s, float scale, float mu, V (&pb)[2]) {
+  float p[16];
 #pragma unroll
-  for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-  tmax = fmaxf(tmax, xor32(tmax)) * scale;
-  const bool move = tmax > st.m + 8.f;          // false for NaN / -inf tiles
-  const float mnew = move ? tmax : st.m;
-  const float muse = (mnew == kNegInf) ? 0.f : mnew;
-  float lsum = 0.f;
+  for (int i = 0; i < 16; ++i) p[i] = fast_exp2(__builtin_fmaf(s[i], scale, -mu));
+  pb[0] = pack8v<V>(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
+  pb[1] = pack8v<V>(p[8], p[9], p[10], p[11], p[12], p[13], p[14], p[15]);
+}
+
+// Online-softmax update of raw scores s (masked keys = -inf), returning the P^T operands; scale is the positive
+// log2-domain softmax scale, so p = exp2(scale * s - mu) costs one FMA per score.
+// Fast path (almost every tile): p with the row's current subtrahend mu, and no tile maximum at all.  The lane's sum
+// of its 16 rounded p values bounds each of them, so a sum <= 2^15 proves that no p overflowed fp16 (or grew past
+// 2^15 in bf16), and the tile is accepted as it is.  Otherwise (the first tile with a finite score, whose p are
+// +inf against kMuNone, or a tile whose scores rose by more than ~11 in the log2 domain) the whole wave takes the
+// exact path: row maxima over both lane halves, m moved up to them, O and l rescaled, p recomputed.
+// Non-finite scores: a NaN score gives a NaN sum, which passes the check and carries NaN into P, O and l (the row's
+// output is NaN, as in float64); a +inf score takes the exact path and gives m = +inf and p = NaN for it (inf - inf).
+// P is rounded to the operand type V of the values it multiplies; l sums those rounded values.
+template <class V>
+__device__ __forceinline__ void softmax_update(RowState& st, const floatx16& s, float scale, V (&pb)[2]) {
+  exp_tile(s, scale, st.mu, pb);
+  float lsum = rowsum16(pb);
+  if (__builtin_amdgcn_ballot_w64(lsum > kTileSumMax)) {      // rare: uniform for the wave
+    // Only the rows whose own lanes overflowed move: the others keep m, get alpha = 1 and the same p bit for bit,
+    // so a row's arithmetic never depends on the other rows of its wave (batch invariance).
+    const float trig = lsum > kTileSumMax ? 1.f : 0.f;
+    const bool row_trig = trig + xor32(trig) > 0.f;
+    float tmax = s[0];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    s[i] = fast_exp2(__builtin_fmaf(s[i], scale, -muse));
-    lsum += s[i];
-  }
-  if (__builtin_amdgcn_ballot_w64(move)) {       // rare after the first tiles
-    const float alpha = fast_exp2(st.m - muse);
+    for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
+    tmax = fmaxf(tmax, xor32(tmax)) * scale;                     // NaN scores are ignored here
+    const float mnew = row_trig ? fmaxf(st.m, tmax) : st.m;
+    const float munew = (mnew == kNegInf) ? kMuNone : mnew;
+    const float alpha = fast_exp2(st.mu - munew);                // 0 when leaving kMuNone; 1 if unchanged
     st.l *= alpha;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) st.o[dt] *= alpha;
+    st.m = mnew;
+    st.mu = munew;
+    exp_tile(s, scale, st.mu, pb);
+    lsum = rowsum16(pb);
   }
   st.l += lsum;
-  st.m = mnew;
-  pb[0] = pack8v<V>(s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7]);
-  pb[1] = pack8v<V>(s[8], s[9], s[10], s[11], s[12], s[13], s[14], s[15]);
 }
 
 // O^T += V^T . P^T using the transposed V tile in LDS.
