@@ -274,6 +274,7 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
                dominant=dict(kernel=DOMINANT[opname], us=round(dom_us, 2), bytes=int(dom_bytes),
                              gbs=round(dom_gbs, 1), frac=round(dom_gbs / PEAK_HBM_GBS, 4)),
                output_check="ok", distinct_input_sets=len(sets))
+    row["dominant"]["traffic"] = measured_traffic(name, row["dominant"])
     log(f"[{name}] {us:9.2f} us/call (p10 {gt['p10']:.2f}, p90 {gt['p90']:.2f})  {gbs:7.1f} GB/s "
         f"({row['pct_peak']:.1f}% of 8 TB/s)  [median of {gt['n']} replays of a HIP graph of {steps} calls; "
         f"eager loop {eager_us:.2f} us/call]   dominant {DOMINANT[opname]} {dom_us:.2f} us = {dom_gbs:.0f} GB/s")
@@ -534,7 +535,7 @@ def main():
                     timing=f"{a.steps} calls replayed from one HIP graph; eager loop {head['eager']['us_per_call']} "
                            f"us/call"),
         roofline=dict(bound="hbm", achieved=dom["gbs"], peak=PEAK_HBM_GBS, unit="GB/s", frac=dom["frac"],
-                      kernel=dom["kernel"], kernel_us=dom["us"], traffic=measured_traffic(head_name, dom)),
+                      kernel=dom["kernel"], kernel_us=dom["us"], traffic=dom.get("traffic")),
         cpu_baseline={k: v for k, v in head.get("cpu_baseline", {}).items()} or None,
         ops=rows,
         ab_vs_torch=None if ab is None else {
