@@ -447,24 +447,25 @@ __global__ __launch_bounds__(1024) void dsa_hist_zero_kernel(DsaArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ sparse MLA
-// Workgroup = (request b, block of 32 heads, chunk of 128 selected keys); 4 waves.  Every wave computes the full
-// S^T tile (all 576 QK dims, in the same order, so all four hold bit-identical scores, softmax state and P) and owns
-// the value dims [128w, 128w+128) of O.
-// The selected latent rows of the chunk's four 32-key tiles are gathered by direct-to-LDS buffer loads into four
-// stages, all issued before the first tile is computed, so the chunk waits for one gather round trip.  In a stage,
+// Workgroup = (request b, block of 32 heads, chunk of 128 selected keys); 4 waves.  Wave w computes the share of
+// the S^T tile over QK dims [144w, 144w+144) and the four shares are summed through LDS in a fixed order, so all
+// four waves hold bit-identical scores, softmax state and P; wave w owns the value dims [128w, 128w+128) of O.
+// The selected latent rows of the chunk's four 32-key tiles are gathered by direct-to-LDS buffer loads into three
+// stages: tiles 0-2 are requested before the first tile is computed and tile 3 replaces tile 0.  In a stage,
 // row r starts at byte r * kLatStride: 1152 bytes of the row plus 16 of padding, so the 73-chunk stride is odd and
 // 16 consecutive rows at one chunk fall on 16 distinct bank groups (conflict-free K-operand reads).  DMA block j
 // (0 <= j < 37) fills stage bytes [1024j, 1024j + 1024): lane i's 16 bytes go to slot 64j + i, which is chunk
 // (slot % 73) of row (slot / 73); padding slots and slots past the 32 rows take copies of real chunks.  Wave w
 // fills blocks w + 4q (q < 9) and all four waves fill block 36 with the same bytes, so every wave issues exactly
 // kLatPerWave loads per tile.  V^T is read from the same rows with the transposing LDS read.
-constexpr int kSSlot = 16 * 64;          // floats of one wave's partial S^T tile
+constexpr int kSSlot = 16 * 64;          // floats of one wave's share of an S^T tile
 constexpr int kLatChunks = kDK / 8;      // 72 chunks of 16 bytes per latent row
 constexpr int kLatStride = (kLatChunks + 1) * 16;           // 1168 bytes
 constexpr int kLatInstr = 37;            // DMA blocks per tile (>= 32 * 73 / 64 slots)
 constexpr int kLatPerWave = 10;          // DMA loads per wave and tile
 constexpr int kLatStageBytes = kLatInstr * 1024;
-constexpr int kLatStages = kChunk / kTile;                  // one stage per tile of the chunk
+constexpr int kLatStages = 3;                                // tile 3 of a chunk reuses stage 0
+constexpr int kQkSteps = kDK / 16 / 4;                       // QK k-steps of one wave (a quarter of the 576 dims)
 static_assert(kLatInstr * 64 >= kTile * (kLatChunks + 1) && kLatInstr == 4 * (kLatPerWave - 1) + 1,
               "a stage holds 32 padded rows; block 36 is shared");
 // The gather addresses a request's rows by 32-bit offsets from one buffer resource, and an offset of 2^31 (past
@@ -489,29 +490,39 @@ __device__ __forceinline__ void dsa_issue_rows(char* __restrict__ stage, __amdgp
   }
 }
 
-// S^T of the tile in stage over all 576 QK dims (36 MFMAs; the same order in every wave).
+// This wave's share of S^T for the tile in stage: QK dims 144w .. 144w + 143 (k-steps 9w .. 9w + 8), nine MFMAs in
+// the same order in every workgroup.  The nine K operands are read from LDS before the first MFMA.
 template <class V>
-__device__ __forceinline__ floatx16 dsa_qk(const char* __restrict__ stage, const V (&qb)[36], int r, int g) {
-  // K operands are read from LDS one group of six ahead of their MFMAs (the scheduling barriers keep that order): a
-  // wave is alone on its SIMD, so nothing else hides the LDS latency.
+__device__ __forceinline__ floatx16 dsa_qk_part(const char* __restrict__ stage, const V (&qb)[kQkSteps], int r,
+                                                int g, int w) {
+  const char* kb = stage + r * kLatStride + (2 * kQkSteps * w + g) * 16;
+  u32x4 k[kQkSteps];
+#pragma unroll
+  for (int j = 0; j < kQkSteps; ++j) k[j] = *reinterpret_cast<const u32x4*>(kb + 2 * j * 16);
   floatx16 s = floatx16{};
-  const char* kb = stage + r * kLatStride + g * 16;
-  u32x4 k[2][6];
 #pragma unroll
-  for (int j = 0; j < 6; ++j) k[0][j] = *reinterpret_cast<const u32x4*>(kb + 2 * j * 16);
-  __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+  for (int j = 0; j < kQkSteps; ++j) s = mfma32(as_v8<V>(k[j]), qb[j], s);
+  return s;
+}
+
+// Full S^T from the four waves' shares: each wave stores its share in its slot of sred (register-major, so every
+// 16-byte access of a wave covers 1 KB contiguously), and after the barrier every wave adds the four slots in the
+// order 0, 1, 2, 3, so all waves hold bit-identical scores.
+__device__ __forceinline__ floatx16 dsa_reduce_s(float* __restrict__ sred, const floatx16& part, int lane, int w) {
 #pragma unroll
-  for (int c0 = 0; c0 < 36; c0 += 6) {
-    const int cur = (c0 / 6) & 1;
-    if (c0 + 6 < 36) {
+  for (int i4 = 0; i4 < 4; ++i4)
+    *reinterpret_cast<floatx4*>(sred + w * kSSlot + (i4 * 64 + lane) * 4) =
+        floatx4{part[4 * i4], part[4 * i4 + 1], part[4 * i4 + 2], part[4 * i4 + 3]};
+  lds_barrier();
+  floatx16 s;
 #pragma unroll
-      for (int j = 0; j < 6; ++j) k[cur ^ 1][j] = *reinterpret_cast<const u32x4*>(kb + 2 * (c0 + 6 + j) * 16);
-      __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+  for (int v = 0; v < 4; ++v)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const floatx4 x = *reinterpret_cast<const floatx4*>(sred + v * kSSlot + (i4 * 64 + lane) * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[4 * i4 + e] = v == 0 ? x[e] : s[4 * i4 + e] + x[e];
     }
-#pragma unroll
-    for (int j = 0; j < 6; ++j) s = mfma32(as_v8<V>(k[cur][j]), qb[c0 + j], s);
-    __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
-  }
   return s;
 }
 
@@ -547,12 +558,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// One tile: S^T over all QK dims, masked online softmax, PV over this wave's value dims.
+// One tile: this wave's QK share, the cross-wave sum of S^T, masked online softmax (identical in every wave), PV
+// over this wave's value dims.
 template <class V>
-__device__ __forceinline__ void dsa_tile(RowState& st, const V (&qb)[36], const char* __restrict__ stage,
-                                         int key0, int kend, float sl2, int lane, int w) {
+__device__ __forceinline__ void dsa_tile(RowState& st, const V (&qb)[kQkSteps], const char* __restrict__ stage,
+                                         float* __restrict__ sred, int key0, int kend, float sl2, int lane, int w) {
   const int r = lane & 31, g = lane >> 5;
-  floatx16 s = dsa_qk(stage, qb, r, g);
+  floatx16 s = dsa_reduce_s(sred, dsa_qk_part(stage, qb, r, g, w), lane, w);
   if (key0 + kTile > kend)
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
@@ -564,51 +576,54 @@ __device__ __forceinline__ void dsa_tile(RowState& st, const V (&qb)[36], const 
   dsa_pv(st, stage, pb, lane, w);
 }
 
-// Walk over the chunk's tiles: every tile has its own stage and all four are requested up front (rows past kend
-// read zeros).  Before tile t a wave waits until at most kLatPerWave * (3 - t) of its loads are in flight, i.e. its
-// part of tile t (and every older load, such as the Q operands) has landed, and the barrier makes every wave's part
-// visible.  The stages are separate LDS arrays and every LDS
-// array the walk touches is a restrict-qualified parameter, so the compiler can tell the stages apart (it would
-// otherwise wait for every load in flight before each LDS read).  The last wait drains every load, so no DMA is
-// still writing LDS when the workgroup ends.
+// Walk over the chunk's four tiles through three stages: tiles 0-2 are requested up front (rows past kend read
+// zeros) and tile 3 goes into stage 0 once every wave has finished tile 0 (the barrier before tile 1).  Before a tile
+// a wave waits until only its loads of later tiles are in flight, i.e. its part of this tile (and every older load,
+// such as the Q operands) has landed, and the barrier makes every wave's part visible.  The stages are separate LDS
+// arrays and every LDS array the walk touches is a restrict-qualified parameter, so the compiler can tell them apart
+// (it would otherwise wait for every load in flight before each LDS read).  The last wait drains every load, so no
+// DMA is still writing LDS when the workgroup ends.
 template <class V>
 __device__ __forceinline__ void dsa_chunk_walk(char* __restrict__ st0, char* __restrict__ st1, char* __restrict__ st2,
-                                               char* __restrict__ st3, RowState& st, const V (&qb)[36],
+                                               float* __restrict__ sred, RowState& st, const V (&qb)[kQkSteps],
                                                __amdgpu_buffer_rsrc_t rows, const int* __restrict__ sidx, int kbeg,
-                                               int kend,
-                                               int ntiles, const int (&drow)[10], const int (&dchk)[10], float sl2,
-                                               int lane, int w) {
-  static_assert(kLatStages == 4 && 3 * kLatPerWave < 64, "four stages, vmcnt range");
+                                               int kend, int ntiles, const int (&drow)[10], const int (&dchk)[10],
+                                               float sl2, int lane, int w) {
+  static_assert(kLatStages == 3 && kChunk == 4 * kTile && 2 * kLatPerWave < 64, "three stages, vmcnt range");
   dsa_issue_rows(st0, rows, sidx, kbeg, kend, kbeg, drow, dchk, w);
   dsa_issue_rows(st1, rows, sidx, kbeg, kend, kbeg + kTile, drow, dchk, w);
   dsa_issue_rows(st2, rows, sidx, kbeg, kend, kbeg + 2 * kTile, drow, dchk, w);
-  dsa_issue_rows(st3, rows, sidx, kbeg, kend, kbeg + 3 * kTile, drow, dchk, w);
   if (ntiles > 0) {
-    wait_vmcnt<3 * kLatPerWave>();
-    lds_barrier();
-    dsa_tile(st, qb, st0, kbeg, kend, sl2, lane, w);
-  }
-  if (ntiles > 1) {
     wait_vmcnt<2 * kLatPerWave>();
     lds_barrier();
-    dsa_tile(st, qb, st1, kbeg + kTile, kend, sl2, lane, w);
+    dsa_tile(st, qb, st0, sred, kbeg, kend, sl2, lane, w);
+  }
+  if (ntiles > 1) {
+    wait_vmcnt<kLatPerWave>();
+    lds_barrier();                              // every wave is done with stage 0
+    if (ntiles > 3) dsa_issue_rows(st0, rows, sidx, kbeg, kend, kbeg + 3 * kTile, drow, dchk, w);
+    dsa_tile(st, qb, st1, sred, kbeg + kTile, kend, sl2, lane, w);
+  }
+  if (ntiles > 3) {
+    wait_vmcnt<kLatPerWave>();
+  } else {
+    wait_vmcnt<0>();
   }
   if (ntiles > 2) {
-    wait_vmcnt<kLatPerWave>();
     lds_barrier();
-    dsa_tile(st, qb, st2, kbeg + 2 * kTile, kend, sl2, lane, w);
+    dsa_tile(st, qb, st2, sred, kbeg + 2 * kTile, kend, sl2, lane, w);
   }
   wait_vmcnt<0>();
   if (ntiles > 3) {
     lds_barrier();
-    dsa_tile(st, qb, st3, kbeg + 3 * kTile, kend, sl2, lane, w);
+    dsa_tile(st, qb, st0, sred, kbeg + 3 * kTile, kend, sl2, lane, w);
   }
 }
 
 template <class V>
 __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
-  __shared__ __attribute__((aligned(16))) char st0[kLatStageBytes], st1[kLatStageBytes], st2[kLatStageBytes],
-      st3[kLatStageBytes];
+  __shared__ __attribute__((aligned(16))) char st0[kLatStageBytes], st1[kLatStageBytes], st2[kLatStageBytes];
+  __shared__ __attribute__((aligned(16))) float sred[4 * kSSlot];
   __shared__ int sidx[kChunk];
   const int item = blockIdx.x;                  // (b * 4 + hb) * kNChunk + chunk
   const int chunk = item % kNChunk;
@@ -627,11 +642,12 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 31, g = lane >> 5;
 
-  // Q^T operand of k-step c: head r's dims 16c + 8g .. 16c + 8g + 7 (chunk 2c + g of the query row).
-  const f16* qrow = a.q + ((size_t)b * kH + hb * 32 + r) * kDK;
-  V qb[36];
+  // Q^T operand of this wave's k-step j: head r's dims 16c + 8g .. 16c + 8g + 7 with c = 9w + j (chunk 2c + g of
+  // the query row).
+  const f16* qrow = a.q + ((size_t)b * kH + hb * 32 + r) * kDK + 16 * kQkSteps * w + 8 * g;
+  V qb[kQkSteps];
 #pragma unroll
-  for (int c = 0; c < 36; ++c) qb[c] = as_v8<V>(ld16(qrow + 16 * c + 8 * g));
+  for (int j = 0; j < kQkSteps; ++j) qb[j] = as_v8<V>(ld16(qrow + 16 * j));
 
   // Clamped into the cache; keys past kend read the zero row whatever their entry holds.
   // Threads t and t + kChunk store the same value.
@@ -651,7 +667,7 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
       __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(a.kv + (size_t)b * a.L * kDK), 0, a.L * kDK * 2, 0x00020000);
   RowState st;
   row_state_init(st);
-  dsa_chunk_walk(st0, st1, st2, st3, st, qb, rows, sidx, kbeg, kend, ntiles, drow, dchk, a.sl2, lane, w);
+  dsa_chunk_walk(st0, st1, st2, sred, st, qb, rows, sidx, kbeg, kend, ntiles, drow, dchk, a.sl2, lane, w);
   // Partial: O[head][128w + d'] for this wave's value dims; m and l are identical in all waves.
   float* po = a.po + (size_t)item * 32 * kDC;
   const float ltot = st.l + xor32(st.l);
