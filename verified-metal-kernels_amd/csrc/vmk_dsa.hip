@@ -137,16 +137,34 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
   const int n = valid_len(a, b);
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, g = lane >> 5;
-  // Issue order: iq and w loads, then the ring's first tiles, so that the first wait for tile 0 covers both and
-  // their latencies overlap; the histogram is cleared meanwhile behind a barrier that waits for LDS only.
-  V qa[2][8];
+  // Every wave needs all of iq (16 KB) and w (256 B) as operands.  They are loaded once per workgroup, by direct-to-
+  // LDS loads into ring stages that the walk has not started on (stage 1 of waves 0, 1 and 2), ahead of the ring's
+  // first tiles: per-wave loads would push 8x the bytes through the CU's load path in front of tile 0.  iq row r
+  // lands at byte 256 r of its half (heads 0-31, 32-63) with 16-byte chunk c at position c ^ (r & 15), so the
+  // operand reads below, 32 rows at one chunk, hit 16 distinct bank groups.
+  V qa[2][8];                                                // filled from LDS before the walk
   float wv[2][16];
   const f16* iqb = a.iq + (size_t)b * kHI * kDI;
+  char* const iq_lds0 = ring + kIdxStageBytes;
+  char* const iq_lds1 = ring + 3 * kIdxStageBytes;
+  char* const w_lds = ring + 5 * kIdxStageBytes;
+  static_assert(kIdxWaves == 8 && kIdxStages == 2, "16 iq loads of 1 KB, two per wave; stage 1 of waves 0-2 free");
+  {
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(iqb), 0, kHI * kDI * 2, 0x00020000);
 #pragma unroll
-  for (int ht = 0; ht < 2; ++ht) {
-    load_qt(qa[ht], iqb + (ht * 32 + r) * kDI, g, true);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) wv[ht][i] = a.w[b * kHI + ht * 32 + 8 * (i >> 2) + 4 * g + (i & 3)];
+    for (int q = 0; q < 2; ++q) {
+      const int j = 2 * wave + q;                            // rows 4j .. 4j + 3
+      const int row = 4 * j + (lane >> 4);
+      const uint32_t off = (uint32_t)(row * 256 + (((lane & 15) ^ (row & 15)) << 4));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, VMK_LPTR((j < 8 ? iq_lds0 : iq_lds1) + (j & 7) * 1024), 16, off,
+                                               0, 0, 0);
+    }
+    if (wave == 0) {
+      const __amdgpu_buffer_rsrc_t rw =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.w + b * kHI), 0, kHI * 4, 0x00020000);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, VMK_LPTR(w_lds), 4, (uint32_t)lane * 4, 0, 0, 0);
+    }
   }
 
   IkSrc src;
@@ -198,11 +216,27 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
     return true;
   };
   unroll_while<0, kIdxStages - 1>(pre);
+  // The histogram is cleared while the loads fly; the wait lets only tile 0's loads (issued last) stay in flight, so
+  // after the barrier every wave's part of iq and w is in LDS.  A second barrier frees stage 1 for the walk.
   for (int i = tid; i < kBins / 2; i += 64 * kIdxWaves) hist2[i] = 0;
   if (tid < kCBins) chist[tid] = 0;
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
+  wait_vmem_dyn(nt > 0 ? 8 : 0);
+  lds_barrier();
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {                              // Q^T operand: head r's dims 64g + 8s .. (chunk 8g + s)
+    const int pos = ((8 * g + s) ^ (r & 15)) << 4;
+    qa[0][s] = as_v8<V>(*reinterpret_cast<const u32x4*>(iq_lds0 + r * 256 + pos));
+    qa[1][s] = as_v8<V>(*reinterpret_cast<const u32x4*>(iq_lds1 + r * 256 + pos));
+  }
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {                         // weights of the rows 8 i4 + 4g .. + 3 of S^T
+      const floatx4 v = *reinterpret_cast<const floatx4*>(w_lds + 4 * (ht * 32 + 8 * i4 + 4 * g));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wv[ht][4 * i4 + e] = v[e];
+    }
+  lds_barrier();
   for (int j0 = 0; j0 < nt; j0 += kIdxStages) {
     auto step = [&](auto S) {
       const int j = j0 + S, jn = j + kIdxStages - 1;
