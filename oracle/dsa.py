@@ -50,12 +50,39 @@ def ref64(q, kv, iq, ik, w, lens=None, sel=None):
     return out
 
 
-def topk_set_check(idx, cnt, s64, n, eps=1e-5):
+def score_error_bound(iq, ik, w, lens=None):
+    """Per request, a bound B on |s32(p) - s64(p)| over its positions p, where s32 is any fp32 evaluation of
+    ops/dsa.py:57-58 from the same 16-bit inputs (this build's indexer: MFMA products, fp32 sums).
+
+    Derivation (u = 2^-24, gamma_n = n u / (1 - n u)):
+      * a product of two fp16 or bf16 values needs at most 22 significand bits, so it is exact in fp32;
+      * the 128-term dot product, summed in any order, errs by at most gamma_127 * sum_i |iq_hi ik_pi|;
+      * max(., 0) is 1-Lipschitz; w_h times it rounds once (u);
+      * the 64-term weighted sum errs by at most gamma_63 times the sum of its terms' magnitudes.
+    To first order the total is gamma_(DI+HI) * sum_h |w_h| * sum_i |iq_hi ik_pi|; gamma_(DI+HI+2) covers the
+    second-order terms.  B is its maximum over the request's first n positions."""
+    iq, ik = np.abs(to64(iq)), np.abs(to64(ik))
+    w = np.abs(toint(w).astype(np.float64))
+    nu = (DI + HI + 2) * 2.0 ** -24
+    gamma = nu / (1.0 - nu)
+    mag = ((iq @ ik.transpose(0, 2, 1)) * w[:, :, None]).sum(1)          # (B, L)
+    ln = toint(lens)
+    out = np.zeros(mag.shape[0])
+    for b in range(mag.shape[0]):
+        n = mag.shape[1] if ln is None else int(ln[b])
+        out[b] = gamma * mag[b, :max(n, 1)].max()
+    return out
+
+
+def topk_set_check(idx, cnt, s64, n, bound):
     """This build's top-k exactness check for one request.  `idx` are the kernel's selected positions (first `cnt`
-    entries valid), `s64` the float64 scores.  Passes when the count is min(n, 2048), the indices are distinct and
-    in [0, n), and the selected set equals the float64 top set on every position whose score is farther than
-    eps * max(1, |tau|) from the 2048-th largest score tau (positions inside that band may swap one for one).
-    Returns (ok, detail dict)."""
+    entries valid), `s64` the float64 scores, `bound` the request's score_error_bound.  Passes when the count is
+    min(n, 2048), the indices are distinct and in [0, n), and the selected set equals the float64 top set on every
+    position whose score is farther than 2 * bound from the 2048-th largest score tau.  Within that band an fp32
+    evaluation may legitimately reorder: every fp32 score is within `bound` of its float64 value, so the fp32
+    2048-th score is within `bound` of tau, and a position more than 2 * bound above (below) tau is above (below)
+    it in fp32 too.  Returns (ok, detail dict); detail["boundary"] counts the positions inside the band and
+    detail["swapped"] the selected positions outside the float64 top set (ties at tau taken by position)."""
     idx = np.asarray(idx)[:cnt].astype(np.int64)
     k = min(n, TOPK)
     det = dict(cnt=int(cnt), expected=k)
@@ -67,13 +94,15 @@ def topk_set_check(idx, cnt, s64, n, eps=1e-5):
         return bool(np.array_equal(np.sort(idx), np.arange(n))), det
     s = s64[:n]
     tau = np.partition(s, n - TOPK)[n - TOPK]
-    band = eps * max(1.0, abs(tau))
+    band = 2.0 * float(bound)
     must = np.nonzero(s > tau + band)[0]
     never = s < tau - band
     chosen = np.zeros(n, dtype=bool)
     chosen[idx] = True
     missing = int((~chosen[must]).sum())
     wrong = int((chosen & never).sum())
-    det.update(tau=float(tau), band=float(band), missing=missing, wrong=wrong,
-               boundary=int(((s >= tau - band) & (s <= tau + band)).sum()))
+    top = np.zeros(n, dtype=bool)
+    top[np.argsort(-s, kind="stable")[:TOPK]] = True
+    det.update(tau=float(tau), band=band, missing=missing, wrong=wrong,
+               boundary=int(((s >= tau - band) & (s <= tau + band)).sum()), swapped=int((chosen & ~top).sum()))
     return missing == 0 and wrong == 0, det

@@ -69,11 +69,12 @@ def test_bf16_dsa_parity(shape, dist, seed):
     torch.cuda.synchronize()
     assert out.dtype == torch.bfloat16
     s64, sel = oracle.dsa.ref_select64(inp["iq"], inp["ik"], inp["w"], inp["lens"])
+    bound = oracle.dsa.score_error_bound(inp["iq"], inp["ik"], inp["w"], inp["lens"])
     idx, cnt = idx.cpu().numpy(), cnt.cpu().numpy()
     lens = None if inp["lens"] is None else inp["lens"].cpu().numpy()
     for b in range(B):
         n = shape["L"] if lens is None else int(lens[b])
-        ok, det = oracle.dsa.topk_set_check(idx[b], int(cnt[b]), s64[b], n)
+        ok, det = oracle.dsa.topk_set_check(idx[b], int(cnt[b]), s64[b], n, bound[b])
         assert ok, (b, det)
     o = out.float().cpu().numpy().astype(np.float64)
     r = oracle.dsa.ref64(**inp, sel=sel)

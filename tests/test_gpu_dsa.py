@@ -25,12 +25,15 @@ def test_dsa_parity(shape, dist, seed):
     out = vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], inp["lens"], idx=idx, cnt=cnt)
     torch.cuda.synchronize()
     s64, sel = oracle.dsa.ref_select64(inp["iq"], inp["ik"], inp["w"], inp["lens"])
+    bound = oracle.dsa.score_error_bound(inp["iq"], inp["ik"], inp["w"], inp["lens"])
     idx, cnt = idx.cpu().numpy(), cnt.cpu().numpy()
     lens = None if inp["lens"] is None else inp["lens"].cpu().numpy()
     for b in range(B):
         n = shape["L"] if lens is None else int(lens[b])
-        ok, det = oracle.dsa.topk_set_check(idx[b], int(cnt[b]), s64[b], n)
+        ok, det = oracle.dsa.topk_set_check(idx[b], int(cnt[b]), s64[b], n, bound[b])
         assert ok, (b, det)
+        print(f"  request {b}: band {det.get('band', 0):.2e} boundary {det.get('boundary', 0)} "
+              f"swapped {det.get('swapped', 0)}")
     o = out.float().cpu().numpy().astype(np.float64)
     r = oracle.dsa.ref64(**inp, sel=sel)
     assert out.shape == tuple(r.shape) and out.dtype == inp["q"].dtype
@@ -92,10 +95,11 @@ def test_dsa_select_exact_ties_broken_by_position(L, n_high, n_tied):
     torch.cuda.synchronize()
     idx, cnt = idx.cpu().numpy(), cnt.cpu().numpy()
     s64, _ = oracle.dsa.ref_select64(inp["iq"], inp["ik"], inp["w"], None)
+    bound = oracle.dsa.score_error_bound(inp["iq"], inp["ik"], inp["w"], None)
     sel = []
     for b in range(2):
         assert cnt[b] == 2048
-        ok, det = oracle.dsa.topk_set_check(idx[b], 2048, s64[b], L)
+        ok, det = oracle.dsa.topk_set_check(idx[b], 2048, s64[b], L, bound[b])
         assert ok and det["boundary"] == n_tied, det
         assert np.array_equal(np.sort(idx[b]), np.sort(want[b]))
         sel.append(idx[b].astype(np.int64))
@@ -120,9 +124,10 @@ def test_dsa_batch_above_64_keeps_histograms_outside_the_head():
         out = vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], None, idx=idx, cnt=cnt)
         torch.cuda.synchronize()
         s64, sel = oracle.dsa.ref_select64(inp["iq"], inp["ik"], inp["w"], None)
+        bound = oracle.dsa.score_error_bound(inp["iq"], inp["ik"], inp["w"], None)
         idx, cnt = idx.cpu().numpy(), cnt.cpu().numpy()
         for b in range(65):
-            ok, det = oracle.dsa.topk_set_check(idx[b], int(cnt[b]), s64[b], 2500)
+            ok, det = oracle.dsa.topk_set_check(idx[b], int(cnt[b]), s64[b], 2500, bound[b])
             assert ok, (seed, b, det)
         em, _ = nerr(out.float().cpu().numpy(), oracle.dsa.ref64(**inp, sel=sel))
         assert em <= 1e-2

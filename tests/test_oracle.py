@@ -358,19 +358,68 @@ def test_topk_set_check_accepts_boundary_swaps_only():
     s = rng.standard_normal(5000)
     s[100] = s[200] = np.sort(s)[-2048]                  # an exact tie at the threshold
     top = np.argsort(-s, kind="stable")[:2048]
-    ok, _ = odsa.topk_set_check(top, 2048, s, 5000)
-    assert ok
+    bound = 1e-12
+    ok, det = odsa.topk_set_check(top, 2048, s, 5000, bound)
+    assert ok and det["boundary"] == 3                   # the value's own position and its two copies
     alt = top.copy()
     tied = [i for i in (100, 200) if i in set(top)]
     other = 300 - tied[0] if len(tied) == 1 else None
     if other is not None:                                # swapping the tied pair keeps the set valid
         alt[list(top).index(tied[0])] = other
-        assert odsa.topk_set_check(alt, 2048, s, 5000)[0]
+        assert odsa.topk_set_check(alt, 2048, s, 5000, bound)[0]
     bad = top.copy()
     bad[0] = np.argsort(s)[0]                            # the smallest score is never in the top set
-    assert not odsa.topk_set_check(bad, 2048, s, 5000)[0]
-    assert not odsa.topk_set_check(top[:2047], 2047, s, 5000)[0]
-    assert odsa.topk_set_check(np.arange(1500)[::-1], 1500, s, 1500)[0]
+    assert not odsa.topk_set_check(bad, 2048, s, 5000, bound)[0]
+    assert not odsa.topk_set_check(top[:2047], 2047, s, 5000, bound)[0]
+    assert odsa.topk_set_check(np.arange(1500)[::-1], 1500, s, 1500, bound)[0]
+    s2 = rng.standard_normal(5000)                       # no ties: the 2049th position for the 2048th passes
+    order = np.argsort(-s2)                              # only if the band covers their gap
+    near = order[:2048].copy()
+    near[2047] = order[2048]
+    gap = s2[order[2047]] - s2[order[2048]]
+    assert odsa.topk_set_check(near, 2048, s2, 5000, gap)[0]
+    assert not odsa.topk_set_check(near, 2048, s2, 5000, gap / 4)[0]
+
+
+def _scores32(iq, ik, w, sequential):
+    """An fp32 evaluation of the indexer scores from the same 16-bit values: products exact in fp32, the 128-term
+    dot products by float32 BLAS (sequential=False) or summed strictly left to right (sequential=True), then the
+    ReLU, the weight and a float32 sum over the heads."""
+    q = iq.float().numpy().astype(np.float32)
+    k = ik.float().numpy().astype(np.float32)
+    w = w.numpy().astype(np.float32)
+    if sequential:
+        prod = q[:, :, None, :] * k[:, None, :, :]                 # (B, HI, L, DI), exact
+        dots = np.add.accumulate(prod, axis=3, dtype=np.float32)[..., -1]
+    else:
+        dots = np.matmul(q, k.transpose(0, 2, 1))
+    terms = (np.maximum(dots, np.float32(0)) * w[:, :, None]).astype(np.float32)
+    return np.add.accumulate(terms, axis=1, dtype=np.float32)[:, -1].astype(np.float64)
+
+
+@pytest.mark.parametrize("dist,L,seq", [("randn", 3000, False), ("randn", 300, True), ("needle", 300, True)])
+def test_score_error_bound_covers_fp32_evaluations(dist, L, seq):
+    inp = dsa.make_inputs(dict(B=2, L=L), seed=3, dist=dist)
+    s64 = odsa.scores64(inp["iq"], inp["ik"], inp["w"])
+    bound = odsa.score_error_bound(inp["iq"], inp["ik"], inp["w"])
+    err = np.abs(_scores32(inp["iq"], inp["ik"], inp["w"], seq) - s64).max(1)
+    assert np.all(err <= bound), (err, bound)
+    assert np.all(bound < 2e-3 * s64.std(1)), (bound, s64.std(1))   # far below the scores' spread
+
+
+def test_score_error_bound_keeps_the_c5_check_tight():
+    """At C5's inputs the band (2 x bound, about 1.4e-3) holds 15-35 of each request's positions around the
+    2048th score, and a selection from scores with one head dropped fails the check."""
+    inp = dsa.make_inputs(dict(B=4, L=65536), seed=0, dist="randn")
+    s64, sel = odsa.ref_select64(inp["iq"], inp["ik"], inp["w"])
+    bound = odsa.score_error_bound(inp["iq"], inp["ik"], inp["w"])
+    w_bad = inp["w"].clone()
+    w_bad[:, 0] = 0
+    s_bad, sel_bad = odsa.ref_select64(inp["iq"], inp["ik"], w_bad)
+    for b in range(4):
+        ok, det = odsa.topk_set_check(sel[b], 2048, s64[b], 65536, bound[b])
+        assert ok and det["boundary"] <= 64 and det["swapped"] == 0, det
+        assert not odsa.topk_set_check(sel_bad[b], 2048, s64[b], 65536, bound[b])[0]
 
 
 DECODE_SHAPES = [(dict(B=2, L=37), "randn"), (dict(B=1, L=1), "randn"), (dict(B=4, L=90, L_min=1), "randn"),

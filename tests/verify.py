@@ -31,7 +31,8 @@ verify.py:48-53 and 160-241 of the reference); the others are this build's.
   CFG  the op's benchmark configurations (CONFIGS, seed 0 as in bench.py), scored like L2 and like L3.
   TK   (dsa, when the module also defines `select(iq, ik, w, lens)`) on every case above: the count is
        min(n, 2048), the positions are distinct and below n, and the set equals the float64 top-2048 except inside
-       the tie band around the 2048th score (oracle.dsa.topk_set_check).
+       a band of twice the fp32 score error bound around the 2048th score (oracle.dsa.score_error_bound and
+       topk_set_check).
   L4   the op's L4_CASES, seed 200 + i: each batch row run alone gives the same output bytes as in the batch.
 The verdict is CORRECT when every case of every layer passes.  Exit status: 0 CORRECT, 1 REJECTED, 2 bad usage.
 """
@@ -438,16 +439,19 @@ class Scorer:
         res = case.describe()
         refs = self.context(case)
         s64, _ = refs.selection()
-        lens = refs.inputs.get("lens")
+        i = refs.inputs
+        bound = self.oracle.score_error_bound(i["iq"], i["ik"], i["w"], i.get("lens"))
+        lens = i.get("lens")
         lens = None if lens is None else lens.cpu().numpy()
         per = []
         ok = True
         for b in range(s64.shape[0]):
             n = s64.shape[1] if lens is None else int(lens[b])
-            okb, det = self.oracle.topk_set_check(arrays["idx"][b], int(arrays["cnt"][b]), s64[b], n)
+            okb, det = self.oracle.topk_set_check(arrays["idx"][b], int(arrays["cnt"][b]), s64[b], n, bound[b])
             ok = ok and okb
             per.append(det)
-        res.update(ok=bool(ok), boundary=[d.get("boundary", 0) for d in per])
+        res.update(ok=bool(ok), boundary=[d.get("boundary", 0) for d in per],
+                   swapped=[d.get("swapped", 0) for d in per])
         if not ok:
             res["requests"] = per
         return res
