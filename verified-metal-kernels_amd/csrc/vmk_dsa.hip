@@ -27,7 +27,8 @@ constexpr int kChunk = 128;        // selected keys per attention workgroup
 constexpr int kNChunk = kTopK / kChunk;
 constexpr int kCand = 4096;        // LDS candidate capacity of the select kernel
 constexpr int kScanWG = 4096;      // positions per select_scan workgroup (256 threads x 16)
-constexpr int kMaxSlices = 1024;   // select_final handles up to 1024 scan slices (L <= 4M)
+constexpr int kMaxSlices = 1024;   // the select handles up to 1024 scan slices (L <= 4M)
+constexpr int kCandAttn = 1024;    // LDS candidate capacity of the select in an attention workgroup
 
 struct DsaArgs {
   const f16* q;         // (B, 128, 576)
@@ -51,6 +52,7 @@ struct DsaArgs {
   int B, L, nb;         // nb = scan slices per request
   int Ls;               // row stride of scores and the scan lists: nb * kScanWG
   int hist_in_head;     // 1: hist lives in the zero-invariant workspace head (no zero-fill launch needed)
+  int fused_select;     // 1: every attention workgroup selects its own chunk (decode entry); 0: idx/cnt are inputs
   uint32_t* chist;      // (B, 256) coarse histogram: 32 first-digit bins per coarse bin (zero-invariant like hist)
   float sl2;            // attention scale * log2(e)
 };
@@ -108,7 +110,8 @@ __device__ void find_threshold(const uint32_t* hist, int nbins, uint32_t need, u
   uint32_t total;
   const uint32_t above = block_excl_scan<NT>(local, red, &total);
   Threshold t;
-  if (threshold_in_range(hist, lo, per, above, need, &t)) {
+  // A range whose counts cannot reach the need-th element from `above` has no hit; skip its walk.
+  if (above < need && above + local >= need && threshold_in_range(hist, lo, per, above, need, &t)) {
     out[0] = t.bin;
     out[1] = t.rest;
   }
@@ -333,10 +336,14 @@ __global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
   if (tid == 0) { a.gcnt[b * a.nb + wg] = (int)t_gt; a.ecnt[b * a.nb + wg] = (int)t_eq; }
 }
 
+// LDS of the select: the second and third radix digits' histogram, the threshold bucket's candidates when there are
+// at most CAND of them (more are read from the slices' lists in memory), and both lists' slice offsets.
+template <int CAND>
 struct SelectShared {
-  uint32_t hist[2048];
-  uint32_t cand_key[kCand];
-  int cand_pos[kCand];
+  uint32_t hist[2048];           // second digit (bits 18..8)
+  uint32_t hist3[1024];          // third digit (bits 7..0); the upper bins stay zero (a bin per thread and more)
+  uint32_t cand_key[CAND];
+  int cand_pos[CAND];
   uint32_t goff[kMaxSlices + 1], eoff[kMaxSlices + 1];
   uint32_t red[16], thr[2];
 };
@@ -351,29 +358,119 @@ __device__ __forceinline__ int slice_of(const uint32_t* off, int ns, uint32_t e)
   return lo;
 }
 
-// Requests with n <= kTopK valid positions select all of them (idx = 0..n-1).  When the indexer ran, its histograms
-// are left zero for the next call.
-__device__ __forceinline__ void select_all(const DsaArgs& a, int b, int n, int* idx, uint32_t* gh) {
+// The picks of output slots [lo, hi) of request b, after select_scan.  Every form of the select produces the same
+// order: the positions above the threshold bucket b1 in increasing order (the slices' lists back to back), then the
+// bucket's keys above the exact threshold key T in position order, then its first need_eq keys equal to T in
+// position order; a request with n <= 2048 valid positions selects 0..n-1 and fills the other slots with 0.  The
+// bucket is refined to T by the second (bits 18..8) and third (bits 7..0) digits over LDS histograms.  None of this
+// depends on NT, the block size, or on which window is asked for: every result is an integer count or a position.
+// emit(slot, position) is called for each slot of the window that holds a pick (every slot, for consistent inputs).
+// Returns the request's count, min(n, 2048).  Every thread of the block calls it.
+template <int NT, int CAND, class Emit>
+__device__ int select_window(const DsaArgs& a, SelectShared<CAND>& sh, int b, int lo, int hi, Emit emit) {
+  static_assert(kMaxSlices % NT == 0, "slices per thread");
   const int tid = threadIdx.x;
-  for (int i = tid; i < kTopK; i += 1024) idx[i] = i < n ? i : 0;
-  if (a.L > kTopK) {
-    for (int i = tid; i < kBins; i += 1024) gh[i] = 0;
-    if (tid < kCBins) a.chist[(size_t)b * kCBins + tid] = 0;
+  const int n = valid_len(a, b);
+  if (n <= kTopK) {
+    for (int s = lo + tid; s < hi; s += NT) emit(s, s < n ? s : 0);
+    return n;
   }
-  if (tid == 0) a.cnt[b] = n;
-}
-
-// The common tail of both select forms.  The n_gt positions above the threshold bucket b1 are in idx[0, n_gt); the
-// bucket's ncand candidates are in position order, in LDS (in_lds) or read by gcand(c, key, pos).  Refines the bucket
-// to the exact threshold key T by the second and third radix digits, then writes the keys above T and the first
-// need_eq keys equal to T (position order) after the n_gt, and leaves the histograms zero for the next call.
-template <class GCand>
-__device__ __forceinline__ void select_refine(const DsaArgs& a, SelectShared& sh, int b, int* idx, uint32_t n_gt,
-                                              uint32_t ncand, bool in_lds, uint32_t b1, GCand gcand) {
-  const int tid = threadIdx.x;
-  uint32_t need = kTopK - n_gt;                      // picks still to make from the bucket (>= 1)
+  // The digits' histograms are cleared while the first loads fly (the scans' barriers below order it).
+  for (int i = tid; i < 2048; i += NT) sh.hist[i] = 0;
+  for (int i = tid; i < 1024; i += NT) sh.hist3[i] = 0;
+  const int ns = (n + kScanWG - 1) / kScanWG;
+  const int* glb = a.glist + (size_t)b * a.Ls;
+  const uint32_t* ekb = a.ekey + (size_t)b * a.Ls;
+  const int* epb = a.epos + (size_t)b * a.Ls;
+  // Up to kSpecSlices slices, the first kSpecCand bucket candidates of every slice (its list starts at a fixed
+  // offset) are loaded together with the counts, so a bucket that fits needs no second round trip.  Entries past a
+  // list's length are loaded too (inside the slice's kScanWG entries) and dropped.
+  constexpr int kSpecSlices = 16, kSpecCand = 64, kTps = NT / kSpecSlices, kEpt = kSpecCand / kTps;
+  static_assert(NT % kSpecSlices == 0 && kSpecCand % kTps == 0, "candidate heads per thread");
+  const bool spec = ns <= kSpecSlices;
+  const int spec_sl = tid / kTps, spec_e0 = (tid % kTps) * kEpt;
+  uint32_t sk[kEpt];
+  int sp[kEpt];
+  if (spec && spec_sl < ns)
+#pragma unroll
+    for (int k = 0; k < kEpt; ++k) {
+      sk[k] = ekb[spec_sl * kScanWG + spec_e0 + k];
+      sp[k] = epb[spec_sl * kScanWG + spec_e0 + k];
+    }
+  // Slice offsets of both lists: thread t owns slices [t per, t per + per).
+  constexpr int kPer = kMaxSlices / NT;
+  const int per = (ns + NT - 1) / NT;
+  const int sbase = tid * per;
+  uint32_t gc[kPer], ec[kPer], g = 0, e = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int sl = sbase + k;
+    gc[k] = k < per && sl < ns ? (uint32_t)a.gcnt[b * a.nb + sl] : 0u;
+    ec[k] = k < per && sl < ns ? (uint32_t)a.ecnt[b * a.nb + sl] : 0u;
+    g += gc[k];
+    e += ec[k];
+  }
+  uint32_t n_gt, ncand;
+  uint32_t go = block_excl_scan<NT>(g, sh.red, &n_gt);
+  uint32_t eo = block_excl_scan<NT>(e, sh.red, &ncand);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int sl = sbase + k;
+    if (k < per && sl < ns) {
+      sh.goff[sl] = go;
+      sh.eoff[sl] = eo;
+    }
+    go += gc[k];
+    eo += ec[k];
+  }
+  if (tid == 0) {
+    sh.goff[ns] = n_gt;
+    sh.eoff[ns] = ncand;
+  }
+  __syncthreads();
+  // Positions above the bucket.
+  const int gend = min(hi, (int)min(n_gt, (uint32_t)kTopK));
+  for (int s = lo + tid; s < gend; s += NT) {
+    const int sl = slice_of(sh.goff, ns, (uint32_t)s);
+    emit(s, glb[sl * kScanWG + (s - (int)sh.goff[sl])]);
+  }
+  if (n_gt >= (uint32_t)hi) return kTopK;                     // the window holds no pick from the bucket
+  // The bucket's candidates in position order.
+  const bool in_lds = ncand <= (uint32_t)CAND;
+  if (in_lds) {
+    if (spec && spec_sl < ns) {
+      const uint32_t e0 = sh.eoff[spec_sl], elen = sh.eoff[spec_sl + 1] - e0;
+#pragma unroll
+      for (int k = 0; k < kEpt; ++k)
+        if ((uint32_t)(spec_e0 + k) < elen) {
+          sh.cand_key[e0 + spec_e0 + k] = sk[k];
+          sh.cand_pos[e0 + spec_e0 + k] = sp[k];
+        }
+    }
+    for (uint32_t c = tid; c < ncand; c += NT) {
+      const int sl = slice_of(sh.eoff, ns, c);
+      const uint32_t o = c - sh.eoff[sl];
+      if (spec && o < (uint32_t)kSpecCand) continue;            // placed from the heads above
+      sh.cand_key[c] = ekb[sl * kScanWG + o];
+      sh.cand_pos[c] = epb[sl * kScanWG + o];
+    }
+  }
+  auto gcand = [&](int c, uint32_t& key, int& pos) {
+    const int sl = slice_of(sh.eoff, ns, (uint32_t)c);
+    const size_t o = (size_t)sl * kScanWG + (c - sh.eoff[sl]);
+    key = ekb[o];
+    pos = epb[o];
+  };
+  __syncthreads();                                            // the candidates in LDS
+  // b1 from the first candidate (the bucket is non-empty: at least one pick comes from it).
+  uint32_t key0;
+  int pos0;
+  if (in_lds) key0 = sh.cand_key[0];
+  else gcand(0, key0, pos0);
+  const uint32_t b1 = key0 >> 19;
+  const uint32_t need = kTopK - n_gt;                         // picks to make from the bucket (>= 1)
   // Candidate walk over thread-contiguous ranges of the ordered candidate list.
-  const int cper = (int)((ncand + 1023) / 1024);
+  const int cper = (int)((ncand + NT - 1) / NT);
   const int c_lo = min((int)ncand, tid * cper), c_hi = min((int)ncand, c_lo + cper);
   auto for_each = [&](auto&& f) {
     for (int c = c_lo; c < c_hi; ++c) {
@@ -387,90 +484,66 @@ __device__ __forceinline__ void select_refine(const DsaArgs& a, SelectShared& sh
       }
     }
   };
-  for (int i = tid; i < 2048; i += 1024) sh.hist[i] = 0;
-  __syncthreads();
   for_each([&](uint32_t key, int) { atomicAdd(&sh.hist[(key >> 8) & 0x7FF], 1u); });
   __syncthreads();
-  find_threshold<1024>(sh.hist, 2048, need, sh.red, sh.thr);
+  find_threshold<NT>(sh.hist, 2048, need, sh.red, sh.thr);
   const uint32_t b2 = sh.thr[0];
-  need = sh.thr[1];
-  sh.hist[tid] = 0;
-  __syncthreads();
+  const uint32_t need2 = sh.thr[1];
   for_each([&](uint32_t key, int) {
-    if (((key >> 8) & 0x7FF) == b2) atomicAdd(&sh.hist[key & 0xFF], 1u);
+    if (((key >> 8) & 0x7FF) == b2) atomicAdd(&sh.hist3[key & 0xFF], 1u);
   });
   __syncthreads();
-  find_threshold<1024>(sh.hist, 1024, need, sh.red, sh.thr);
+  find_threshold<NT>(sh.hist3, 1024, need2, sh.red, sh.thr);
   const uint32_t T = (b1 << 19) | (b2 << 8) | sh.thr[0];
   const uint32_t need_eq = sh.thr[1];
-  // Bucket picks: keys above T, then the first need_eq keys equal to T in position order.
-  uint32_t c_above = 0, c_tie = 0, above_total, tie_total;
+  // Bucket picks: keys above T, then the first need_eq keys equal to T in position order.  With the candidates in
+  // LDS (at most CAND < 2^16 of them) both counts travel in one scan, 16 bits each.
+  uint32_t c_above = 0, c_tie = 0, above_total, tie_total, o_above, o_tie;
   for_each([&](uint32_t key, int) { c_above += key > T; c_tie += key == T; });
-  uint32_t o_above = block_excl_scan<1024>(c_above, sh.red, &above_total);
-  uint32_t o_tie = block_excl_scan<1024>(c_tie, sh.red, &tie_total);
+  if (in_lds) {
+    static_assert(CAND < 65536, "16-bit packed counts");
+    uint32_t tot;
+    const uint32_t o = block_excl_scan<NT>(c_above | (c_tie << 16), sh.red, &tot);
+    o_above = o & 0xFFFFu;
+    o_tie = o >> 16;
+    above_total = tot & 0xFFFFu;
+    tie_total = tot >> 16;
+  } else {
+    o_above = block_excl_scan<NT>(c_above, sh.red, &above_total);
+    o_tie = block_excl_scan<NT>(c_tie, sh.red, &tie_total);
+  }
   for_each([&](uint32_t key, int p) {
     if (key > T) {
       const uint32_t slot = n_gt + o_above++;
-      if (slot < (uint32_t)kTopK) idx[slot] = p;
+      if (slot >= (uint32_t)lo && slot < (uint32_t)hi && slot < (uint32_t)kTopK) emit((int)slot, p);
     } else if (key == T) {
       const uint32_t slot = n_gt + above_total + o_tie;
-      if (o_tie < need_eq && slot < (uint32_t)kTopK) idx[slot] = p;
+      if (o_tie < need_eq && slot >= (uint32_t)lo && slot < (uint32_t)hi && slot < (uint32_t)kTopK)
+        emit((int)slot, p);
       ++o_tie;
     }
   });
-  uint32_t* gh = a.hist + (size_t)b * kBins;
-  for (int i = tid; i < kBins; i += 1024) gh[i] = 0;               // leave the histograms zero for the next call
-  if (tid < kCBins) a.chist[(size_t)b * kCBins + tid] = 0;
-  if (tid == 0) a.cnt[b] = kTopK;
+  return kTopK;
 }
 
+// Leaves request b's histograms zero for the next call, after the indexer ran: fine bins [fine0, fine1) and the
+// coarse bins they make up, by nthr threads.
+__device__ __forceinline__ void clear_histograms(const DsaArgs& a, int b, int fine0, int fine1, int tid, int nthr) {
+  if (a.L <= kTopK) return;
+  uint32_t* gh = a.hist + (size_t)b * kBins;
+  for (int i = fine0 + tid; i < fine1; i += nthr) gh[i] = 0;
+  for (int i = fine0 / 32 + tid; i < fine1 / 32; i += nthr) a.chist[(size_t)b * kCBins + i] = 0;
+}
+
+// The whole selection of one request (one 1024-thread workgroup): idx, cnt, and the histograms left zero.  Used by
+// the indexer-select entry; the decode entry lets every attention workgroup select its own chunk instead.
 __global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
-  __shared__ SelectShared sh;
+  __shared__ SelectShared<kCand> sh;
   const int b = blockIdx.x, tid = threadIdx.x;
-  const int n = valid_len(a, b);
   int* idx = a.idx + (size_t)b * kTopK;
-  if (n <= kTopK) {
-    select_all(a, b, n, idx, a.hist + (size_t)b * kBins);
-    return;
-  }
-  const int ns = (n + kScanWG - 1) / kScanWG;
-  // Slice offsets of both lists (one slice per thread).
-  const uint32_t g = tid < ns ? (uint32_t)a.gcnt[b * a.nb + tid] : 0u;
-  const uint32_t e = tid < ns ? (uint32_t)a.ecnt[b * a.nb + tid] : 0u;
-  uint32_t n_gt, ncand;
-  const uint32_t go = block_excl_scan<1024>(g, sh.red, &n_gt);
-  const uint32_t eo = block_excl_scan<1024>(e, sh.red, &ncand);
-  if (tid < ns) { sh.goff[tid] = go; sh.eoff[tid] = eo; }
-  if (tid == 0) { sh.goff[ns] = n_gt; sh.eoff[ns] = ncand; }
-  __syncthreads();
-  // Positions above the bucket: the slices' lists back to back.
-  const int* glb = a.glist + (size_t)b * a.Ls;
-  for (uint32_t s = tid; s < n_gt && s < (uint32_t)kTopK; s += 1024) {
-    const int sl = slice_of(sh.goff, ns, s);
-    idx[s] = glb[sl * kScanWG + (s - sh.goff[sl])];
-  }
-  const uint32_t* ekb = a.ekey + (size_t)b * a.Ls;
-  const int* epb = a.epos + (size_t)b * a.Ls;
-  const bool in_lds = ncand <= (uint32_t)kCand;
-  if (in_lds)
-    for (uint32_t c = tid; c < ncand; c += 1024) {
-      const int sl = slice_of(sh.eoff, ns, c);
-      sh.cand_key[c] = ekb[sl * kScanWG + (c - sh.eoff[sl])];
-      sh.cand_pos[c] = epb[sl * kScanWG + (c - sh.eoff[sl])];
-    }
-  auto gcand = [&](int c, uint32_t& key, int& pos) {
-    const int sl = slice_of(sh.eoff, ns, (uint32_t)c);
-    const size_t o = (size_t)sl * kScanWG + (c - sh.eoff[sl]);
-    key = ekb[o];
-    pos = epb[o];
-  };
-  __syncthreads();                                   // the candidates in LDS
-  // b1 from the first candidate (the bucket is non-empty: need >= 1 of it).
-  uint32_t key0;
-  int pos0;
-  if (in_lds) key0 = sh.cand_key[0];
-  else gcand(0, key0, pos0);
-  select_refine(a, sh, b, idx, n_gt, ncand, in_lds, key0 >> 19, gcand);
+  const int cnt = select_window<1024>(a, sh, b, 0, kTopK, [&](int s, int p) { idx[s] = p; });
+  clear_histograms(a, b, 0, kBins, tid, 1024);
+  if (tid == 0) a.cnt[b] = cnt;
 }
 
 // Zero-fills the per-request histograms before the indexer accumulates into them (when they are not in the head).
@@ -659,20 +732,12 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   __shared__ __attribute__((aligned(16))) char st0[kLatStageBytes], st1[kLatStageBytes], st2[kLatStageBytes];
   __shared__ __attribute__((aligned(16))) float sred[4 * kSSlot];
   __shared__ int sidx[kChunk];
+  __shared__ SelectShared<kCandAttn> sel;
   const int item = blockIdx.x;                  // (b * 4 + hb) * kNChunk + chunk
   const int chunk = item % kNChunk;
   const int hb = (item / kNChunk) % 4;
   const int b = item / (kNChunk * 4);
   const int kbeg = chunk * kChunk;
-  // The chunk's selected positions: idx holds kTopK entries per request, so every thread loads one without waiting
-  // for the count (entries past it are masked below), and the Q loads are issued before the positions are used.  No
-  // branch depends on the count: a chunk past it (lens, or L < kTopK) runs no tiles and writes an empty partial,
-  // which the combine does not read.
-  const int* ip = a.idx + (size_t)b * kTopK;
-  const int sel = ip[kbeg + (int)(threadIdx.x & (kChunk - 1))];
-  const int cnt = min(max(a.cnt[b], 0), kTopK);     // a caller's count outside [0, kTopK] is clamped
-  const int kend = max(kbeg, min(cnt, kbeg + kChunk));
-  const int ntiles = (kend - kbeg + kTile - 1) / kTile;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 31, g = lane >> 5;
 
@@ -683,9 +748,34 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
 #pragma unroll
   for (int j = 0; j < kQkSteps; ++j) qb[j] = as_v8<V>(ld16(qrow + 16 * j));
 
-  // Clamped into the cache; keys past kend read the zero row whatever their entry holds.
-  // Threads t and t + kChunk store the same value.
-  sidx[threadIdx.x & (kChunk - 1)] = min(max(sel, 0), a.L - 1);
+  // The chunk's selected positions.  Decode entry: the workgroup selects them itself from select_scan's lists
+  // (select_window, the same picks as select_final's), and the workgroups of head block 0 write idx, cnt and clear
+  // their share of the histograms.  Sparse-attention entry: idx holds kTopK entries per request, so every thread
+  // loads one without waiting for the count (entries past it are masked below).  No branch depends on the count: a
+  // chunk past it (lens, or L < kTopK) runs no tiles and writes an empty partial, which the combine does not read.
+  int cnt;
+  if (a.fused_select) {
+    int* idxo = a.idx + (size_t)b * kTopK;
+    cnt = select_window<256>(a, sel, b, kbeg, kbeg + kChunk, [&](int s, int p) {
+      sidx[s - kbeg] = p;
+      if (hb == 0) idxo[s] = p;
+    });
+    if (hb == 0) {
+      clear_histograms(a, b, chunk * (kBins / kNChunk), (chunk + 1) * (kBins / kNChunk), threadIdx.x, 256);
+      if (chunk == 0 && threadIdx.x == 0) a.cnt[b] = cnt;
+    }
+    __syncthreads();
+    // Clamped into the cache; keys past kend read the zero row whatever their entry holds.
+    if (threadIdx.x < kChunk) sidx[threadIdx.x] = min(max(sidx[threadIdx.x], 0), a.L - 1);
+  } else {
+    const int* ip = a.idx + (size_t)b * kTopK;
+    const int sl = ip[kbeg + (int)(threadIdx.x & (kChunk - 1))];
+    cnt = min(max(a.cnt[b], 0), kTopK);                // a caller's count outside [0, kTopK] is clamped
+    // Threads t and t + kChunk store the same value.
+    sidx[threadIdx.x & (kChunk - 1)] = min(max(sl, 0), a.L - 1);
+  }
+  const int kend = max(kbeg, min(cnt, kbeg + kChunk));
+  const int ntiles = (kend - kbeg + kTile - 1) / kTile;
 
   // This wave's DMA loads q (block lat_block(w, q)): the (row, chunk) its lane fetches for each.
   int drow[kLatPerWave], dchk[kLatPerWave];
@@ -786,13 +876,14 @@ static int dsa_fill_args(DsaArgs& a, const void* q, const void* kv, const void* 
   a.nb = (int)((L + kScanWG - 1) / kScanWG);
   a.Ls = a.nb * kScanWG;
   a.hist_in_head = lay.hist_in_head ? 1 : 0;
+  a.fused_select = 0;
   a.sl2 = (float)(1.0 / sqrt(192.0)) * kLog2e;
   return 0;
 }
 
 // V: operand type of iq/ik (half8: fp16, bf16x8: bf16); the select works on fp32 scores.
 template <class V>
-static int launch_index_select(const DsaArgs& a, hipStream_t s) {
+static int launch_index_select(const DsaArgs& a, hipStream_t s, bool final_select) {
   if (a.L > kTopK) {
     if (!a.hist_in_head) {
       hipLaunchKernelGGL(dsa_hist_zero_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
@@ -808,10 +899,12 @@ static int launch_index_select(const DsaArgs& a, hipStream_t s) {
     prof_after(kKDsaSelectScan, s);
     VMK_CHECK_HIP(hipGetLastError());
   }
-  prof_before(kKDsaSelect, s);
-  hipLaunchKernelGGL(dsa_select_final_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
-  prof_after(kKDsaSelect, s);
-  VMK_CHECK_HIP(hipGetLastError());
+  if (final_select) {
+    prof_before(kKDsaSelect, s);
+    hipLaunchKernelGGL(dsa_select_final_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
+    prof_after(kKDsaSelect, s);
+    VMK_CHECK_HIP(hipGetLastError());
+  }
   return 0;
 }
 
@@ -851,7 +944,7 @@ static int dsa_indexer_select(const void* iq, const void* ik, const void* w, con
   VMK_CHECK(aligned16(iq) && aligned16(ik), "iq/ik must be 16-byte aligned");
   DsaArgs a;
   dsa_fill_args(a, nullptr, nullptr, iq, ik, w, lens, nullptr, idx, cnt, B, L, workspace);
-  return launch_index_select<V>(a, (hipStream_t)stream);
+  return launch_index_select<V>(a, (hipStream_t)stream, true);
 }
 
 template <class V>
@@ -876,8 +969,9 @@ static int dsa_decode(const void* q, const void* kv, const void* iq, const void*
   VMK_CHECK(L <= kMaxAttnL, "sparse attention needs L * 1152 bytes < 2 GiB per request (L <= 1864134)");
   DsaArgs a;
   dsa_fill_args(a, q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace);
+  a.fused_select = 1;                                // the attention workgroups select their own chunks
   hipStream_t s = (hipStream_t)stream;
-  if (int rc = launch_index_select<V>(a, s)) return rc;
+  if (int rc = launch_index_select<V>(a, s, false)) return rc;
   return launch_attention<V>(a, s);
 }
 
