@@ -126,6 +126,8 @@ int vmk_prefix_decode_paged_bf16(const void* q, const void* k_pages, const void*
                                  int64_t max_suffix_pages, void* workspace, size_t ws_bytes, void* stream);
 int vmk_dsa_indexer_select_bf16(const void* iq, const void* ik, const void* w, const void* lens, void* idx, void* cnt,
                                 int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream);
+int vmk_dsa_indexer_bf16(const void* iq, const void* ik, const void* w, const void* lens, void* scores, int64_t B,
+                         int64_t L, void* workspace, size_t ws_bytes, void* stream);
 int vmk_dsa_sparse_mla_bf16(const void* q, const void* kv, const void* idx, const void* cnt, void* out, int64_t B,
                             int64_t L, void* workspace, size_t ws_bytes, void* stream);
 int vmk_dsa_decode_bf16(const void* q, const void* kv, const void* iq, const void* ik, const void* w, const void* lens,
@@ -153,6 +155,16 @@ size_t vmk_dsa_workspace_size(int64_t B, int64_t L);
 /* Indexer + exact top-2048 only (the reference's indexer_mpp/indexer_float + select, dsa_opus55_v7.py:963-973). */
 int vmk_dsa_indexer_select(const void* iq, const void* ik, const void* w, const void* lens, void* idx, void* cnt,
                            int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream);
+/* The two stages of the select on their own, as llama.cpp decomposes DSA decode (LIGHTNING_INDEXER and TOP_K,
+ * llama_cpp/test-backend-ops.patch:96-97; the reference's separate dsa_indexer and dsa_select kernels,
+ * dsa_opus55_v7.py:27-98, 100-307).  vmk_dsa_indexer writes scores (B, L) fp32, row stride L; positions at or past
+ * lens[b] are not written.  vmk_dsa_topk takes such scores and writes idx/cnt exactly as vmk_dsa_indexer_select does
+ * (the same picks in the same order for the same scores).  The mask of llama.cpp's TOP_K_MASK step has no
+ * counterpart: vmk_dsa_sparse_mla reads the indices directly. */
+int vmk_dsa_indexer(const void* iq, const void* ik, const void* w, const void* lens, void* scores, int64_t B, int64_t L,
+                    void* workspace, size_t ws_bytes, void* stream);
+int vmk_dsa_topk(const void* scores, const void* lens, void* idx, void* cnt, int64_t B, int64_t L, void* workspace,
+                 size_t ws_bytes, void* stream);
 /* Sparse absorbed-MLA attention over given indices (the reference's attn_mpp/attn_float, dsa_opus55_v7.py:975). */
 int vmk_dsa_sparse_mla(const void* q, const void* kv, const void* idx, const void* cnt, void* out, int64_t B,
                        int64_t L, void* workspace, size_t ws_bytes, void* stream);

@@ -145,6 +145,10 @@ def test_dsa_wrappers_check_every_shape_before_the_device():
         (vmk.dsa_indexer_select, (iq, torch.zeros(B, L, 64, **f16), w), "ik"),
         (vmk.dsa_decode, (q, torch.zeros(B, L + 1, 576, **f16), iq, ik, w), "positions"),
         (vmk.dsa_decode, (q, kv, iq, ik, w, torch.ones(1, dtype=torch.int32)), "lens"),
+        (vmk.dsa_indexer, (iq, ik, w, None, torch.zeros(B, L + 1)), "scores"),
+        (vmk.dsa_indexer, (iq, ik, torch.zeros(B, 63)), "w"),
+        (vmk.dsa_topk, (torch.zeros(B, L), torch.ones(B + 1, dtype=torch.int32)), "lens"),
+        (vmk.dsa_topk, (torch.zeros(B, L), None, torch.zeros(B, 2047, dtype=torch.int32), cnt), "idx"),
     ]
     for fn, args, needle in bad:
         with pytest.raises(ValueError, match=needle):
@@ -153,6 +157,8 @@ def test_dsa_wrappers_check_every_shape_before_the_device():
         vmk.dsa_sparse_mla(q, kv, idx, cnt)
     with pytest.raises(TypeError, match="share one dtype"):
         vmk.dsa_decode(q, kv, iq.bfloat16(), ik.bfloat16(), w)
+    with pytest.raises(TypeError, match="scores"):
+        vmk.dsa_topk(torch.zeros(B, L, **f16))
 
 
 def test_failed_call_sets_the_workspace_aside(monkeypatch):

@@ -131,3 +131,50 @@ def test_dsa_batch_above_64_keeps_histograms_outside_the_head():
             assert ok, (seed, b, det)
         em, _ = nerr(out.float().cpu().numpy(), oracle.dsa.ref64(**inp, sel=sel))
         assert em <= 1e-2
+
+
+@pytest.mark.parametrize("shape,dist,seed", [(dict(B=2, L=5003), "randn", 61), (dict(B=3, L=9000), "ragged", 62),
+                                             (dict(B=4, L=65536), "randn", 0), (dict(B=1, L=1500), "randn", 63)])
+def test_dsa_split_entries(shape, dist, seed):
+    """llama.cpp's decomposition of the select: vmk_dsa_indexer's scores lie within the fp32 error bound of the
+    float64 scores, vmk_dsa_topk picks exactly the top-2048 of the scores it is given (ties by position), and
+    the two together give the fused entry's idx and cnt bit for bit."""
+    import vmk
+    print(f"dsa split entries {shape} {dist} seed={seed}", flush=True)
+    inp = dsa.make_inputs(shape, seed=seed, dist=dist, device="cuda")
+    B, L = shape["B"], shape["L"]
+    scores = vmk.dsa_indexer(inp["iq"], inp["ik"], inp["w"], inp["lens"])
+    idx, cnt = vmk.dsa_topk(scores, inp["lens"])
+    idx2, cnt2 = vmk.dsa_indexer_select(inp["iq"], inp["ik"], inp["w"], inp["lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(cnt, cnt2) and torch.equal(idx, idx2)
+    s32 = scores.cpu().numpy().astype(np.float64)
+    s64 = oracle.dsa.scores64(inp["iq"], inp["ik"], inp["w"])
+    bound = oracle.dsa.score_error_bound(inp["iq"], inp["ik"], inp["w"], inp["lens"])
+    lens = None if inp["lens"] is None else inp["lens"].cpu().numpy()
+    idx, cnt = idx.cpu().numpy(), cnt.cpu().numpy()
+    for b in range(B):
+        n = L if lens is None else int(lens[b])
+        assert np.abs(s32[b, :n] - s64[b, :n]).max() <= bound[b]
+        k = min(n, 2048)
+        assert cnt[b] == k
+        want = np.argsort(-s32[b, :n], kind="stable")[:k]           # the fp32 top-k, ties taken by position
+        assert np.array_equal(np.sort(idx[b, :k]), np.sort(want)), b
+
+
+def test_dsa_topk_exact_on_tied_scores():
+    """vmk_dsa_topk on scores with large exact ties (more than 4096 equal values at the threshold take the
+    global-memory walk): the lowest positions of the tied value are taken."""
+    import vmk
+    rng = np.random.default_rng(71)
+    B, L = 2, 20000
+    s = rng.standard_normal((B, L)).astype(np.float32)
+    s[0, rng.permutation(L)[:6000]] = 1.25                          # 6000 ties, above about 2000 positions
+    s[1, rng.permutation(L)[:300]] = 1.25
+    scores = torch.from_numpy(s).cuda()
+    idx, cnt = vmk.dsa_topk(scores)
+    torch.cuda.synchronize()
+    idx = idx.cpu().numpy()
+    for b in range(B):
+        want = np.argsort(-s[b], kind="stable")[:2048]
+        assert np.array_equal(np.sort(idx[b]), np.sort(want)), b

@@ -53,6 +53,8 @@ struct DsaArgs {
   int Ls;               // row stride of scores and the scan lists: nb * kScanWG
   int hist_in_head;     // 1: hist lives in the zero-invariant workspace head (no zero-fill launch needed)
   int fused_select;     // 1: every attention workgroup selects its own chunk (decode entry); 0: idx/cnt are inputs
+  int scores_only;      // 1: the indexer writes scores (row stride Ls) and no histograms (vmk_dsa_indexer)
+  const float* scores_in;  // (B, L) caller scores for vmk_dsa_topk, copied into `scores` by dsa_scores_hist_kernel
   uint32_t* chist;      // (B, 256) coarse histogram: 32 first-digit bins per coarse bin (zero-invariant like hist)
   float sl2;            // attention scale * log2(e)
 };
@@ -208,9 +210,11 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
     const int pos = (t0 + j) * kTile + r;
     if (g == 0 && pos < n) {
       sc[pos] = tot;
-      const uint32_t bin = fkey(tot) >> 19;
-      atomicAdd(&hist2[bin >> 1], 1u << (16 * (bin & 1)));
-      atomicAdd(&chist[bin >> 5], 1u);
+      if (!a.scores_only) {
+        const uint32_t bin = fkey(tot) >> 19;
+        atomicAdd(&hist2[bin >> 1], 1u << (16 * (bin & 1)));
+        atomicAdd(&chist[bin >> 5], 1u);
+      }
     }
   };
   auto pre = [&](auto S) {
@@ -252,6 +256,7 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
     };
     if (!unroll_while<0, kIdxStages>(step)) break;
   }
+  if (a.scores_only) return;                                // uniform: no histograms to add
   __syncthreads();
   uint32_t* gh = a.hist + (size_t)b * kBins;
   for (int i = tid; i < kBins / 2; i += 64 * kIdxWaves) {
@@ -275,6 +280,40 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
 // All compaction uses block scans over thread-contiguous position ranges, so the output order (positions above the
 // bucket in increasing order, then the bucket's picks in increasing order, ties at T broken by position) does not
 // depend on scheduling, and neither do the attention sums that follow.
+
+// vmk_dsa_topk: caller scores (B, L) into the workspace's scores (row stride Ls, the padding zero-filled) and the same
+// histograms the indexer builds, 1024 positions per workgroup (4 per thread).
+__global__ __launch_bounds__(256) void dsa_scores_hist_kernel(DsaArgs a) {
+  __shared__ uint32_t hist2[kBins / 2];
+  __shared__ uint32_t chist[kCBins];
+  const int b = blockIdx.y, tid = threadIdx.x;
+  const int n = valid_len(a, b);
+  for (int i = tid; i < kBins / 2; i += 256) hist2[i] = 0;
+  chist[tid] = 0;
+  __syncthreads();
+  const float* src = a.scores_in + (size_t)b * a.L;
+  float* dst = a.scores + (size_t)b * a.Ls;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int p = blockIdx.x * 1024 + k * 256 + tid;       // < Ls by the grid
+    const float v = p < a.L ? src[p] : 0.f;
+    dst[p] = v;
+    if (p < n) {
+      const uint32_t bin = fkey(v) >> 19;
+      atomicAdd(&hist2[bin >> 1], 1u << (16 * (bin & 1)));
+      atomicAdd(&chist[bin >> 5], 1u);
+    }
+  }
+  __syncthreads();
+  uint32_t* gh = a.hist + (size_t)b * kBins;
+  for (int i = tid; i < kBins / 2; i += 256) {
+    const uint32_t c = hist2[i];
+    if (c & 0xFFFFu) atomicAdd(&gh[2 * i], c & 0xFFFFu);
+    if (c >> 16) atomicAdd(&gh[2 * i + 1], c >> 16);
+  }
+  const uint32_t c = chist[tid];
+  if (c) atomicAdd(&a.chist[(size_t)b * kCBins + tid], c);
+}
 
 __global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
   __shared__ uint32_t cnt[kCBins], red[4], thr[2], b1s;
@@ -877,6 +916,8 @@ static int dsa_fill_args(DsaArgs& a, const void* q, const void* kv, const void* 
   a.Ls = a.nb * kScanWG;
   a.hist_in_head = lay.hist_in_head ? 1 : 0;
   a.fused_select = 0;
+  a.scores_only = 0;
+  a.scores_in = nullptr;
   a.sl2 = (float)(1.0 / sqrt(192.0)) * kLog2e;
   return 0;
 }
@@ -905,6 +946,24 @@ static int launch_index_select(const DsaArgs& a, hipStream_t s, bool final_selec
     prof_after(kKDsaSelect, s);
     VMK_CHECK_HIP(hipGetLastError());
   }
+  return 0;
+}
+
+// The select from caller scores (vmk_dsa_topk): scores into the workspace with the histograms, then the two select
+// launches, as after the indexer.
+static int launch_topk(const DsaArgs& a, hipStream_t s) {
+  if (a.L > kTopK) {
+    if (!a.hist_in_head) {
+      hipLaunchKernelGGL(dsa_hist_zero_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
+      VMK_CHECK_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(dsa_scores_hist_kernel, dim3((unsigned)(a.Ls / 1024), (unsigned)a.B), dim3(256), 0, s, a);
+    VMK_CHECK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(dsa_select_scan_kernel, dim3((unsigned)a.nb, (unsigned)a.B), dim3(256), 0, s, a);
+    VMK_CHECK_HIP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(dsa_select_final_kernel, dim3((unsigned)a.B), dim3(1024), 0, s, a);
+  VMK_CHECK_HIP(hipGetLastError());
   return 0;
 }
 
@@ -947,6 +1006,25 @@ static int dsa_indexer_select(const void* iq, const void* ik, const void* w, con
   return launch_index_select<V>(a, (hipStream_t)stream, true);
 }
 
+// Indexer scores only: written into the caller's (B, L) buffer (row stride L), no histograms, so the workspace head
+// stays zero.
+template <class V>
+static int dsa_indexer_only(const void* iq, const void* ik, const void* w, const void* lens, void* scores, int64_t B,
+                            int64_t L, void* workspace, size_t ws_bytes, void* stream) {
+  VMK_CHECK(iq && ik && w && scores, "null pointer argument");
+  DSA_COMMON_CHECKS();
+  VMK_CHECK(aligned16(iq) && aligned16(ik), "iq/ik must be 16-byte aligned");
+  DsaArgs a;
+  dsa_fill_args(a, nullptr, nullptr, iq, ik, w, lens, nullptr, nullptr, nullptr, B, L, workspace);
+  a.scores = (float*)scores;
+  a.Ls = (int)L;
+  a.scores_only = 1;
+  hipLaunchKernelGGL(dsa_indexer_kernel<V>, dim3((unsigned)((L + kIdxWG - 1) / kIdxWG), (unsigned)B),
+                     dim3(64 * kIdxWaves), 0, (hipStream_t)stream, a);
+  VMK_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
 template <class V>
 static int dsa_sparse_mla(const void* q, const void* kv, const void* idx, const void* cnt, void* out, int64_t B,
                           int64_t L, void* workspace, size_t ws_bytes, void* stream) {
@@ -973,6 +1051,26 @@ static int dsa_decode(const void* q, const void* kv, const void* iq, const void*
   hipStream_t s = (hipStream_t)stream;
   if (int rc = launch_index_select<V>(a, s, false)) return rc;
   return launch_attention<V>(a, s);
+}
+
+extern "C" int vmk_dsa_indexer(const void* iq, const void* ik, const void* w, const void* lens, void* scores, int64_t B,
+                               int64_t L, void* workspace, size_t ws_bytes, void* stream) {
+  return dsa_indexer_only<half8>(iq, ik, w, lens, scores, B, L, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_dsa_indexer_bf16(const void* iq, const void* ik, const void* w, const void* lens, void* scores,
+                                    int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream) {
+  return dsa_indexer_only<bf16x8>(iq, ik, w, lens, scores, B, L, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_dsa_topk(const void* scores, const void* lens, void* idx, void* cnt, int64_t B, int64_t L,
+                            void* workspace, size_t ws_bytes, void* stream) {
+  VMK_CHECK(scores && idx && cnt, "null pointer argument");
+  DSA_COMMON_CHECKS();
+  DsaArgs a;
+  dsa_fill_args(a, nullptr, nullptr, nullptr, nullptr, nullptr, lens, nullptr, idx, cnt, B, L, workspace);
+  a.scores_in = (const float*)scores;
+  return launch_topk(a, (hipStream_t)stream);
 }
 
 extern "C" int vmk_dsa_indexer_select(const void* iq, const void* ik, const void* w, const void* lens, void* idx,

@@ -6,4 +6,5 @@ tensors on a ROCm device; every call launches on torch's current stream and retu
 """
 from .lib import VmkError, load  # noqa: F401
 from .api import (spec_verify, spec_verify_noalloc, decode, prefix_decode, prefix_decode_paged, dsa_decode,  # noqa: F401
-                  dsa_indexer_select, dsa_sparse_mla, workspace, reserve_workspace, device_ok)
+                  dsa_indexer_select, dsa_indexer, dsa_topk, dsa_sparse_mla, workspace, reserve_workspace,
+                  device_ok)

@@ -321,6 +321,47 @@ def dsa_indexer_select(iq, ik, w, lens=None, idx=None, cnt=None):
     return idx, cnt
 
 
+def dsa_indexer(iq, ik, w, lens=None, scores=None):
+    """Indexer scores alone: score[b, l] = sum_h w[b, h] * max(iq[b, h] . ik[b, l], 0) in fp32; iq/ik both fp16 or
+    both bf16, w fp32.  Returns scores (B, L) float32; positions at or past lens[b] are left as they were."""
+    _, sfx = _elem(iq)
+    B, L = _dsa_indexer_shapes(iq, ik, w, lens)
+    if scores is not None:
+        _need(scores, "scores", torch.float32, 2)
+        if tuple(scores.shape) != (B, L):
+            raise ValueError(f"scores {tuple(scores.shape)}: expected ({B}, {L})")
+    _resident(iq=iq, ik=ik, w=w, lens=lens, scores=scores)
+    if scores is None:
+        scores = torch.empty(B, L, dtype=torch.float32, device=ik.device)
+    ws = workspace(lib.load().vmk_dsa_workspace_size(B, L), ik.device)
+    _launch("vmk_dsa_indexer" + sfx, ws, iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
+            0 if lens is None else lens.data_ptr(), scores.data_ptr(), B, L, ws.data_ptr(), ws.numel(), _stream(ik))
+    return scores
+
+
+def dsa_topk(scores, lens=None, idx=None, cnt=None):
+    """Exact top-2048 of given fp32 scores (B, L) per request, among the first lens[b] positions; the same picks in
+    the same order as dsa_indexer_select for the same scores.  Returns idx (B, 2048) int32 and cnt (B,) int32."""
+    _need(scores, "scores", torch.float32, 2)
+    B, L = scores.shape
+    if lens is not None:
+        _need(lens, "lens", torch.int32, 1)
+        if lens.shape[0] != B:
+            raise ValueError(f"lens has {lens.shape[0]} entries, expected B = {B}")
+    if idx is not None or cnt is not None:
+        if idx is None or cnt is None:
+            raise ValueError("give both idx and cnt, or neither")
+        _selection_shapes(idx, cnt, B)
+    _resident(scores=scores, lens=lens, idx=idx, cnt=cnt)
+    if idx is None:
+        idx = torch.empty(B, DSA_TOPK, dtype=torch.int32, device=scores.device)
+        cnt = torch.empty(B, dtype=torch.int32, device=scores.device)
+    ws = workspace(lib.load().vmk_dsa_workspace_size(B, L), scores.device)
+    _launch("vmk_dsa_topk", ws, scores.data_ptr(), 0 if lens is None else lens.data_ptr(), idx.data_ptr(),
+            cnt.data_ptr(), B, L, ws.data_ptr(), ws.numel(), _stream(scores))
+    return idx, cnt
+
+
 def dsa_sparse_mla(q, kv, idx, cnt, out=None):
     """Sparse absorbed-MLA attention of q (B,128,576) over rows kv[b, idx[b, :cnt[b]]], q/kv both fp16 or both bf16;
     idx (B, 2048) int32, cnt (B,) int32 (clamped to [0, 2048]; a request with cnt 0 gets NaN rows).  Returns

@@ -40,6 +40,9 @@ _SIGS = {
     "vmk_dsa_decode_bf16": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_workspace_size": [_c_i64] * 2,
     "vmk_dsa_indexer_select": [_c_vp] * 6 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_indexer": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_indexer_bf16": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_topk": [_c_vp] * 4 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_sparse_mla": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_decode": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
 }
