@@ -178,3 +178,26 @@ def test_dsa_topk_exact_on_tied_scores():
     for b in range(B):
         want = np.argsort(-s[b], kind="stable")[:2048]
         assert np.array_equal(np.sort(idx[b]), np.sort(want)), b
+
+
+def test_dsa_sparse_mla_counts_outside_the_range():
+    """Counts a caller passes to vmk_dsa_sparse_mla are clamped to [0, 2048]: 0 and a negative count give NaN rows
+    (the softmax of no keys) without reading any partial, 3000 acts as 2048, and 100 attends over the first 100
+    indices."""
+    import vmk
+    shape = dict(B=4, L=6000)
+    print(f"dsa counts outside the range {shape}", flush=True)
+    inp = dsa.make_inputs(shape, seed=81, dist="randn", device="cuda")
+    idx, _ = vmk.dsa_indexer_select(inp["iq"], inp["ik"], inp["w"])
+    cnt = torch.tensor([0, -5, 3000, 100], dtype=torch.int32, device="cuda")
+    out = vmk.dsa_sparse_mla(inp["q"], inp["kv"], idx, cnt)
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    assert np.isnan(o[0]).all() and np.isnan(o[1]).all()
+    ix = idx.cpu().numpy().astype(np.int64)
+    for b, k in ((2, 2048), (3, 100)):
+        sel = [ix[i, :k] for i in range(4)]
+        r = oracle.dsa.ref64(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], sel=sel)[b]
+        assert np.isfinite(o[b]).all()
+        em, _ = nerr(o[b], r)
+        assert em <= 1e-2, (b, em)
