@@ -831,16 +831,28 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   RowState st;
   row_state_init(st);
   dsa_chunk_walk(st0, st1, st2, sred, st, qb, rows, sidx, kbeg, kend, ntiles, drow, dchk, a.sl2, lane, w);
-  // Partial: O[head][128w + d'] for this wave's value dims; m and l are identical in all waves.
-  float* po = a.po + (size_t)item * 32 * kDC;
+  // Partial: O[head][128w + d'] for this wave's value dims; m and l are identical in all waves.  The wave's 32 x 128
+  // block goes through LDS (stages 0 and 1 are free once every wave is past its last tile), row r's 16-byte chunk c
+  // at position (c + r) & 31, so that every store instruction writes two whole 512-byte pieces of rows instead of
+  // 32-byte pieces of 32 rows.
   const float ltot = st.l + xor32(st.l);
+  __syncthreads();
+  float* lds = reinterpret_cast<float*>(w < 2 ? st0 : st1) + (w & 1) * 32 * 128;
+  static_assert(2 * 32 * 128 * 4 <= kLatStageBytes, "two waves' blocks per stage");
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-      floatx4 v = floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]};
-      *reinterpret_cast<floatx4*>(po + r * kDC + 128 * w + dt * 32 + 8 * blk + 4 * g) = v;
-    }
+    for (int blk = 0; blk < 4; ++blk)
+      *reinterpret_cast<floatx4*>(lds + r * 128 + (((dt * 8 + 2 * blk + g) + r) & 31) * 4) =
+          floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]};
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");       // the wave reads back only its own block
+  float* po = a.po + (size_t)item * 32 * kDC + 128 * w;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = 2 * i + g;
+    *reinterpret_cast<floatx4*>(po + row * kDC + r * 4) =
+        *reinterpret_cast<const floatx4*>(lds + row * 128 + ((r + row) & 31) * 4);
+  }
   if (w == 0 && g == 0) {
     a.pml[((size_t)item * 32 + r) * 2] = st.m;
     a.pml[((size_t)item * 32 + r) * 2 + 1] = ltot;
