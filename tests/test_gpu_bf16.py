@@ -20,6 +20,7 @@ CASES = [("spec", dict(B=4, L=32768, k=8, dtype="bf16"), "chain", 1),
          ("prefix", dict(N=64, P=16384, S=2048, S_min=128, dtype="bf16"), "outlier", 7),
          ("prefix", dict(N=8, P=2048, S=256, dtype="bf16"), "randn", 8),
          ("prefix", dict(N=20, P=5000, S=3000, S_min=1, dtype="bf16"), "tiny", 9),
+         ("prefix", dict(N=4, P=8192, S=256, S_min=1, dtype="bf16"), "randn", 11),   # single-wave prefix units
          ("prefix_paged", dict(N=12, P=3072, S=700, S_min=1, ps=64, absent=2, dtype="bf16"), "randn", 10)]
 OPS = {"spec": spec, "decode": decode, "prefix": prefix, "prefix_paged": prefix_paged, "dsa": dsa}
 

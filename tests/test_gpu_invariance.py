@@ -28,6 +28,9 @@ def run(kernel, op, shape, dist, seed):
 @pytest.mark.parametrize("shape,dist", [(dict(N=64, P=16384, S=2048, S_min=128), "outlier"),
                                         (dict(N=8, P=2048, S=256), "randn"),
                                         (dict(N=12, P=3000, S=2500, S_min=1), "randn"),
+                                        # the batch runs single-wave prefix units, a request alone the row blocks
+                                        (dict(N=8, P=3000, S=2500, S_min=1), "randn"),
+                                        (dict(N=4, P=8192, S=256), "randn"),
                                         (dict(N=3, P=0, S=300), "randn"), (dict(N=5, P=700, S=0), "randn")])
 def test_prefix_rows_alone_equal_batch(shape, dist):
     import prefix_mi355x

@@ -45,6 +45,23 @@ ROWS_CASES = [
 ]
 
 
+# At most 32 rows per KV head and more mixed-launch items than CUs: the prefix runs as single-wave units, 2 or 4 per
+# workgroup (the mixed launch's row blocks give the same bits; see the invariance test below).
+UNITS_CASES = [
+    (dict(N=4, P=4096, S=512), "randn", 120),                              # 2 units per workgroup
+    (dict(N=4, P=8192, S=256, S_min=1), "outlier", 121),                   # ragged suffixes
+    (dict(N=1, P=65536, S=100), "randn", 122),                             # 4 per workgroup, 64 chunks: general merge
+    (dict(N=4, P=4096, S=300, S_min=1, Hq=64, Hkv=8), "randn", 123),       # G = 8: the general merge
+    (dict(N=10, P=6000, S=200, Hq=24, Hkv=8), "randn", 124),               # G = 3, 30 rows, a partial last chunk
+    (dict(N=8, P=3000, S=2500, S_min=1), "randn", 125),                    # suffixes of two chunks: combine launch
+]
+
+
+@pytest.mark.parametrize("shape,dist,seed", UNITS_CASES)
+def test_prefix_units_parity(shape, dist, seed):
+    test_prefix_parity(shape, dist, seed)
+
+
 def _head_is_zero():
     from vmk import api
     ws = api.workspace(0, "cuda")

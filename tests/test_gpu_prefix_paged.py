@@ -17,7 +17,9 @@ SAME = [(dict(N=64, P=16384, S=2048, S_min=128, ps=64), "outlier", 1), (dict(N=8
         (dict(N=5, P=1024, S=77, ps=64), "randn", 3), (dict(N=4, P=384, S=300, ps=96), "randn", 4),
         (dict(N=3, P=0, S=300, ps=32), "randn", 5), (dict(N=6, P=4096, S=1000, ps=512), "randn", 6),
         (dict(N=20, P=40960, S=3000, S_min=1, ps=256), "randn", 7), (dict(N=40, P=2048, S=64, S_min=0, ps=32),
-                                                                     "randn", 8)]
+                                                                     "randn", 8),
+        # single-wave prefix units (2 and 4 per workgroup)
+        (dict(N=4, P=8192, S=256, S_min=1, ps=64), "randn", 9), (dict(N=1, P=65536, S=64, ps=128), "randn", 10)]
 ORACLE = [(dict(N=6, P=3072, S=500, S_min=0, ps=64, absent=3), "randn", 11),
           (dict(N=33, P=640, S=40, ps=32, absent=2), "randn", 12),
           (dict(N=4, P=2048, S=256, ps=64), "nan_inf", 13), (dict(N=4, P=2048, S=256, ps=256), "large", 14),

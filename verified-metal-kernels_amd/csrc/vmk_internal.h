@@ -20,6 +20,8 @@ void prof_after(int kernel_id, hipStream_t s);
 // Layout of the head: [0, 2 MiB) histograms, [2 MiB, 4 MiB) counters.
 constexpr size_t kWsHead = (size_t)4 << 20;
 constexpr size_t kWsCounters = (size_t)2 << 20;
+// Compute units of the target GPU (MI355X): plans size their grids to one dispatch round of one workgroup per CU.
+constexpr int kDeviceCUs = 256;
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline void* align_up(void* p, size_t a) { return (void*)(((uintptr_t)p + a - 1) & ~(uintptr_t)(a - 1)); }
 }  // namespace vmk

@@ -12,6 +12,9 @@
 //   writes the output.
 // Launch 3 (prefix_combine_kernel, only when a suffix spans several chunks or there is no prefix): per output row,
 //   the log-sum-exp merge of its prefix and suffix partials.
+// With at most 128 rows per KV head, launches 1 and 2 are one grid (prefix_mixed_kernel; with at most 32 rows and
+// more items than CUs, its prefix items are single-wave units packed 2 or 4 per workgroup) and prefix_merge_kernel
+// does the whole-suffix merges.
 #include "attn_core.h"
 #include "vmk_internal.h"
 
@@ -39,6 +42,7 @@ struct PrefixArgs {
   int2* order;             // (N,) (request, suffix length) by decreasing length (written by the prefix launch), or null
   int fuse;                // 1: suffix items are whole suffixes and merge the (finished) prefix partials themselves
   int merge;               // 1: whole-suffix partials are merged with the prefix partials by prefix_merge_kernel
+  int units;               // mixed launch, N*G <= 32: prefix units (one wave each) per workgroup; 0: row blocks
   float sl2;
 };
 
@@ -362,16 +366,66 @@ __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
   prefix_rows_item<NW, kPaged, V>(a, smem, blockIdx.x);
 }
 
-// Both item kinds in one grid when a KV head has at most 128 rows: prefix items (4 waves sharing a ring) first, then
-// suffix items writing their partials.  No item depends on another.
+// Prefix unit u (KV head h, prefix chunk) of a mixed launch when a KV head has at most 32 rows: one wave walks the
+// chunk for all rows through a private ring of NS stages and writes rows 0..31 of the row-block partial.  A row's
+// arithmetic is that of a row-block wave (the same tiles in the same order through the same tile function), so the
+// output bits do not depend on which form ran; several units share a workgroup so that the grid stays within one
+// dispatch round when the row-block grid would not.
+template <int NS, bool kPaged, class V>
+__device__ __forceinline__ void prefix_unit(const PrefixArgs& a, char* smem, int u, int w) {
+  const int lane = threadIdx.x & 63;
+  const int split = u % a.nsplit_p, h = u / a.nsplit_p;            // one row block (nrb_p == 1)
+  const int kbeg = split * a.chunk_p, kend = min(a.P, kbeg + a.chunk_p);
+  const int ntiles = (kend - kbeg + kTile - 1) / kTile;
+  const int nrows = a.N * a.G, r = lane & 31;
+  const int qr = r < nrows ? r : 0;
+  V qb[8];
+  load_qt(qb, a.q + ((size_t)(qr / a.G) * a.Hq + h * a.G + qr % a.G) * 128, lane >> 5, r < nrows);
+  RowState st;
+  row_state_init(st);
+  const uint32_t ring_off = (uint32_t)w * NS * kStageBytes;
+  const TileLanes tl = tile_lanes(lane, ring_off);
+  auto walk = [&](const auto& src) {
+    wave_walk<NS>(st, qb, smem + ring_off, smem, tl, src, kbeg, 0, ntiles, 1, lane);
+  };
+  if constexpr (kPaged) {
+    walk(paged_src(a, a.prefix_pages, a.P / a.ps, h, kbeg, kend));
+  } else {
+    RangeSrc src;
+    src.scale = a.sl2;
+    const size_t off = (size_t)h * a.P * 128;
+    src.kbase = a.kp + off;
+    src.vbase = a.vp + off;
+    src.kend = kend;
+    walk(src);
+  }
+  const size_t rows_wg = 32 * a.WRp;
+  store_partial(a.po_p + (size_t)u * rows_wg * 128, a.pml_p + (size_t)u * rows_wg * 2, st, lane, nrows);
+}
+
+// Both item kinds in one grid when a KV head has at most 128 rows: prefix items first (row blocks of 4 waves
+// sharing a ring, or a.units single-wave units per workgroup), then suffix items writing their partials.  No item
+// depends on another.
 constexpr int kMixedSmemBytes = kRowsSmemBytes > kAttnSmemBytes ? kRowsSmemBytes : kAttnSmemBytes;
 template <bool kPaged, class V>
 __global__ __launch_bounds__(256) void prefix_mixed_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kMixedSmemBytes];
-  if ((int)blockIdx.x < a.n_prefix_items)
+  const int upw = a.units;
+  const int npw = upw ? (a.n_prefix_items + upw - 1) / upw : a.n_prefix_items;
+  if ((int)blockIdx.x >= npw) {
+    suffix_item<kPaged, V>(a, smem, blockIdx.x - npw);
+  } else if (upw == 0) {
     prefix_rows_item<4, kPaged, V>(a, smem, blockIdx.x);
-  else
-    suffix_item<kPaged, V>(a, smem, blockIdx.x - a.n_prefix_items);
+  } else {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), u = (int)blockIdx.x * upw + w;
+    if (w < upw && u < a.n_prefix_items) {
+      static_assert(2 * 4 * kStageBytes <= kMixedSmemBytes && 4 * 2 * kStageBytes <= kMixedSmemBytes, "unit rings");
+      if (upw == 2)
+        prefix_unit<4, kPaged, V>(a, smem, u, w);                   // the whole 128-key chunk in flight
+      else
+        prefix_unit<2, kPaged, V>(a, smem, u, w);
+    }
+  }
 }
 
 // After a mixed launch with whole suffixes: the final merge of the G rows of (request, KV head), by the functions a
@@ -427,6 +481,7 @@ struct PrefixPlan {
   int WRp, nrb_p, nsplit_p, chunk_p, nsplit_s, chunk_s;
   size_t po_p, pml_p, po_s, pml_s, order;
   int n_prefix_items, n_items;
+  int units, n_wg_mixed;    // mixed launch: prefix units per workgroup (0: row blocks) and its grid
   bool fuse;
 };
 
@@ -461,6 +516,16 @@ static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int
   p.order = (size_t)2 * N;
   // With the prefix partials finished by the prefix launch, whole-suffix items finish their rows themselves.
   p.fuse = p.n_prefix_items > 0 && p.nsplit_s == 1;
+  // Mixed launch (R <= 128): one workgroup per prefix item while the grid fits one dispatch round (each workgroup
+  // holds 128 KB of LDS, so one per CU); with R <= 32, 2 or 4 single-wave units per workgroup otherwise.  The units
+  // compute the same bits as the row blocks, so this choice (which depends on N) does not break batch invariance.
+  const int n_suffix = p.n_items - p.n_prefix_items;
+  p.units = 0;
+  if (p.WRp == 4 && R <= 32 && p.n_items > kDeviceCUs) {
+    p.units = 2;
+    if ((p.n_prefix_items + 1) / 2 + n_suffix > kDeviceCUs) p.units = 4;
+  }
+  p.n_wg_mixed = p.units ? (p.n_prefix_items + p.units - 1) / p.units + n_suffix : p.n_items;
   return p;
 }
 
@@ -483,13 +548,14 @@ static int prefix_launch(PrefixArgs& a, const void* q, void* out, const void* sl
   a.order = (ragged && p.n_prefix_items > 0 && !mixed) ? (int2*)align_up(a.pml_s + p.pml_s, 256) : nullptr;
   a.fuse = p.fuse && !mixed ? 1 : 0;
   a.merge = p.fuse && mixed ? 1 : 0;
+  a.units = mixed ? p.units : 0;
   a.N = (int)N; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.P = (int)P; a.S = (int)S;
   a.WRp = p.WRp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;
   a.nsplit_s = p.nsplit_s; a.chunk_s = p.chunk_s; a.n_prefix_items = p.n_prefix_items;
   a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
   prof_before(kKPrefixPartial, s);
   if (mixed) {
-    hipLaunchKernelGGL((prefix_mixed_kernel<kPaged, V>), dim3((unsigned)p.n_items), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((prefix_mixed_kernel<kPaged, V>), dim3((unsigned)p.n_wg_mixed), dim3(256), 0, s, a);
     VMK_CHECK_HIP(hipGetLastError());
   } else {
     if (p.n_prefix_items > 0) {
