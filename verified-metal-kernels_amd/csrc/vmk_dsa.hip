@@ -70,7 +70,9 @@ __device__ __forceinline__ int valid_len(const DsaArgs& a, int b) {
 }
 
 // ------------------------------------------------------------------------------------------------ indexer
-// Block-wide exclusive prefix sum of v over thread ids (NT threads); *total receives the sum of all v.
+// Block-wide exclusive prefix sum of v over thread ids (NT threads); *total receives the sum of all v.  The block
+// helpers exchange data through LDS only, so their barriers wait for LDS operations only: global loads of the
+// caller stay in flight across them.
 template <int NT>
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -81,7 +83,7 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
     if (lane >= o) x += y;
   }
   if (lane == 63) red[wave] = x;
-  __syncthreads();
+  lds_barrier();
   uint32_t before = 0, all = 0;
 #pragma unroll
   for (int w2 = 0; w2 < NT / 64; ++w2) {
@@ -89,7 +91,7 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
     all += t;
     if (w2 < wave) before += t;
   }
-  __syncthreads();
+  lds_barrier();
   *total = all;
   return before + x - v;
 }
@@ -117,7 +119,7 @@ __device__ void find_threshold(const uint32_t* hist, int nbins, uint32_t need, u
     out[0] = t.bin;
     out[1] = t.rest;
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // ik rows of one request as a key source of the DMA tile loader (K half of a stage only).
@@ -397,6 +399,12 @@ __device__ __forceinline__ int slice_of(const uint32_t* off, int ns, uint32_t e)
   return lo;
 }
 
+// A compile-time bool as a type (selects an instantiation of a generic lambda).
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
+
 // The picks of output slots [lo, hi) of request b, after select_scan.  Every form of the select produces the same
 // order: the positions above the threshold bucket b1 in increasing order (the slices' lists back to back), then the
 // bucket's keys above the exact threshold key T in position order, then its first need_eq keys equal to T in
@@ -466,7 +474,7 @@ __device__ int select_window(const DsaArgs& a, SelectShared<CAND>& sh, int b, in
     sh.goff[ns] = n_gt;
     sh.eoff[ns] = ncand;
   }
-  __syncthreads();
+  lds_barrier();
   // Positions above the bucket.
   const int gend = min(hi, (int)min(n_gt, (uint32_t)kTopK));
   for (int s = lo + tid; s < gend; s += NT) {
@@ -500,69 +508,75 @@ __device__ int select_window(const DsaArgs& a, SelectShared<CAND>& sh, int b, in
     key = ekb[o];
     pos = epb[o];
   };
-  __syncthreads();                                            // the candidates in LDS
-  // b1 from the first candidate (the bucket is non-empty: at least one pick comes from it).
-  uint32_t key0;
-  int pos0;
-  if (in_lds) key0 = sh.cand_key[0];
-  else gcand(0, key0, pos0);
-  const uint32_t b1 = key0 >> 19;
-  const uint32_t need = kTopK - n_gt;                         // picks to make from the bucket (>= 1)
-  // Candidate walk over thread-contiguous ranges of the ordered candidate list.
-  const int cper = (int)((ncand + NT - 1) / NT);
-  const int c_lo = min((int)ncand, tid * cper), c_hi = min((int)ncand, c_lo + cper);
-  auto for_each = [&](auto&& f) {
-    for (int c = c_lo; c < c_hi; ++c) {
-      if (in_lds) {
-        f(sh.cand_key[c], sh.cand_pos[c]);
-      } else {
-        uint32_t key;
-        int pos;
-        gcand(c, key, pos);
-        f(key, pos);
+  lds_barrier();                                              // the candidates in LDS
+  // The refine, instantiated separately for candidates in LDS and in the global lists, so that the LDS form never
+  // waits for a global load of the other form (a merged form shares registers and waits between them).
+  auto refine = [&](auto LDS) -> int {
+    constexpr bool kLds = decltype(LDS)::value;
+    // b1 from the first candidate (the bucket is non-empty: at least one pick comes from it).
+    uint32_t key0;
+    int pos0;
+    if constexpr (kLds) key0 = sh.cand_key[0];
+    else gcand(0, key0, pos0);
+    const uint32_t b1 = key0 >> 19;
+    const uint32_t need = kTopK - n_gt;                       // picks to make from the bucket (>= 1)
+    // Candidate walk over thread-contiguous ranges of the ordered candidate list.
+    const int cper = (int)((ncand + NT - 1) / NT);
+    const int c_lo = min((int)ncand, tid * cper), c_hi = min((int)ncand, c_lo + cper);
+    auto for_each = [&](auto&& f) {
+      for (int c = c_lo; c < c_hi; ++c) {
+        if constexpr (kLds) {
+          f(sh.cand_key[c], sh.cand_pos[c]);
+        } else {
+          uint32_t key;
+          int pos;
+          gcand(c, key, pos);
+          f(key, pos);
+        }
       }
+    };
+    for_each([&](uint32_t key, int) { atomicAdd(&sh.hist[(key >> 8) & 0x7FF], 1u); });
+    lds_barrier();
+    find_threshold<NT>(sh.hist, 2048, need, sh.red, sh.thr);
+    const uint32_t b2 = sh.thr[0];
+    const uint32_t need2 = sh.thr[1];
+    for_each([&](uint32_t key, int) {
+      if (((key >> 8) & 0x7FF) == b2) atomicAdd(&sh.hist3[key & 0xFF], 1u);
+    });
+    lds_barrier();
+    find_threshold<NT>(sh.hist3, 1024, need2, sh.red, sh.thr);
+    const uint32_t T = (b1 << 19) | (b2 << 8) | sh.thr[0];
+    const uint32_t need_eq = sh.thr[1];
+    // Bucket picks: keys above T, then the first need_eq keys equal to T in position order.  With the candidates
+    // in LDS (at most CAND < 2^16 of them) both counts travel in one scan, 16 bits each.
+    uint32_t c_above = 0, c_tie = 0, above_total, tie_total, o_above, o_tie;
+    for_each([&](uint32_t key, int) { c_above += key > T; c_tie += key == T; });
+    if constexpr (kLds) {
+      static_assert(CAND < 65536, "16-bit packed counts");
+      uint32_t tot;
+      const uint32_t o = block_excl_scan<NT>(c_above | (c_tie << 16), sh.red, &tot);
+      o_above = o & 0xFFFFu;
+      o_tie = o >> 16;
+      above_total = tot & 0xFFFFu;
+      tie_total = tot >> 16;
+    } else {
+      o_above = block_excl_scan<NT>(c_above, sh.red, &above_total);
+      o_tie = block_excl_scan<NT>(c_tie, sh.red, &tie_total);
     }
+    for_each([&](uint32_t key, int p) {
+      if (key > T) {
+        const uint32_t slot = n_gt + o_above++;
+        if (slot >= (uint32_t)lo && slot < (uint32_t)hi && slot < (uint32_t)kTopK) emit((int)slot, p);
+      } else if (key == T) {
+        const uint32_t slot = n_gt + above_total + o_tie;
+        if (o_tie < need_eq && slot >= (uint32_t)lo && slot < (uint32_t)hi && slot < (uint32_t)kTopK)
+          emit((int)slot, p);
+        ++o_tie;
+      }
+    });
+    return kTopK;
   };
-  for_each([&](uint32_t key, int) { atomicAdd(&sh.hist[(key >> 8) & 0x7FF], 1u); });
-  __syncthreads();
-  find_threshold<NT>(sh.hist, 2048, need, sh.red, sh.thr);
-  const uint32_t b2 = sh.thr[0];
-  const uint32_t need2 = sh.thr[1];
-  for_each([&](uint32_t key, int) {
-    if (((key >> 8) & 0x7FF) == b2) atomicAdd(&sh.hist3[key & 0xFF], 1u);
-  });
-  __syncthreads();
-  find_threshold<NT>(sh.hist3, 1024, need2, sh.red, sh.thr);
-  const uint32_t T = (b1 << 19) | (b2 << 8) | sh.thr[0];
-  const uint32_t need_eq = sh.thr[1];
-  // Bucket picks: keys above T, then the first need_eq keys equal to T in position order.  With the candidates in
-  // LDS (at most CAND < 2^16 of them) both counts travel in one scan, 16 bits each.
-  uint32_t c_above = 0, c_tie = 0, above_total, tie_total, o_above, o_tie;
-  for_each([&](uint32_t key, int) { c_above += key > T; c_tie += key == T; });
-  if (in_lds) {
-    static_assert(CAND < 65536, "16-bit packed counts");
-    uint32_t tot;
-    const uint32_t o = block_excl_scan<NT>(c_above | (c_tie << 16), sh.red, &tot);
-    o_above = o & 0xFFFFu;
-    o_tie = o >> 16;
-    above_total = tot & 0xFFFFu;
-    tie_total = tot >> 16;
-  } else {
-    o_above = block_excl_scan<NT>(c_above, sh.red, &above_total);
-    o_tie = block_excl_scan<NT>(c_tie, sh.red, &tie_total);
-  }
-  for_each([&](uint32_t key, int p) {
-    if (key > T) {
-      const uint32_t slot = n_gt + o_above++;
-      if (slot >= (uint32_t)lo && slot < (uint32_t)hi && slot < (uint32_t)kTopK) emit((int)slot, p);
-    } else if (key == T) {
-      const uint32_t slot = n_gt + above_total + o_tie;
-      if (o_tie < need_eq && slot >= (uint32_t)lo && slot < (uint32_t)hi && slot < (uint32_t)kTopK)
-        emit((int)slot, p);
-      ++o_tie;
-    }
-  });
-  return kTopK;
+  return in_lds ? refine(BoolC<true>{}) : refine(BoolC<false>{});
 }
 
 // Leaves request b's histograms zero for the next call, after the indexer ran: fine bins [fine0, fine1) and the
