@@ -5,7 +5,8 @@
 Prints human-readable progress on stderr and ONE JSON line on stdout.  A "step" is one call of the op on one batch
 of the headline configuration (BASELINE configs[1] = C2, shared-prefix decode at scale); `value` is its achieved
 HBM throughput (algorithmic bytes / time per call, inputs resident in HBM), `ops` holds the same figures for every
-configuration (C1..C5, and this build's D1-D3 decode, P2 paged prefix, C2b bf16).  Method:
+configuration (C1..C5, and this build's D1-D3 decode, P2 paged prefix, C2b bf16, DP the DSA input projections).
+Method:
   * the kernel's output on the timed inputs is checked against the PyTorch standard op first
     (allclose atol=rtol=1e-2, bench.py:180-192 of the reference), and the inputs are checked for modification;
   * every call reads a different input set, rotating over enough distinct sets (>= 1 GiB in total) that the
@@ -44,21 +45,29 @@ PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16 MFMA
 METRIC = "µs/call per op + achieved HBM GB/s (% of MI355X peak) at bench shapes"
 HEADLINE = "C2"
 DOMINANT = {"prefix": "prefix_partial", "spec": "spec_partial", "dsa": "dsa_indexer", "decode": "spec_partial",
-            "prefix_paged": "prefix_partial"}
+            "prefix_paged": "prefix_partial", "dsa_project": "dsa_project_q"}
+# Inputs the ops write by contract (the projections append the new token's cache rows), left out of the
+# input-mutation check.
+WRITES = {"dsa_project": ("kv", "ik")}
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def op_module(opname):
+    from vmk.ops import OPS, dsa_project
+    return dsa_project if opname == "dsa_project" else OPS[opname]
+
+
 def config_table():
-    from vmk.ops import decode, dsa, prefix, prefix_paged, spec
+    from vmk.ops import decode, dsa, dsa_project, prefix, prefix_paged, spec
     return [("C1", "prefix", *prefix.CONFIGS["C1"]), ("C2", "prefix", *prefix.CONFIGS["C2"]),
             ("C3", "spec", *spec.CONFIGS["C3"]), ("C4", "spec", *spec.CONFIGS["C4"]),
             ("C5", "dsa", *dsa.CONFIGS["C5"]),
             ("D1", "decode", *decode.CONFIGS["D1"]), ("D2", "decode", *decode.CONFIGS["D2"]),
             ("D3", "decode", *decode.CONFIGS["D3"]), ("P2", "prefix_paged", *prefix_paged.CONFIGS["P2"]),
-            ("C2b", "prefix", *prefix.CONFIGS["C2b"])]
+            ("C2b", "prefix", *prefix.CONFIGS["C2b"]), ("DP", "dsa_project", *dsa_project.CONFIGS["DP"])]
 
 
 class HipEvents:
@@ -101,6 +110,9 @@ def call_op(opname, inp):
     if opname == "prefix_paged":
         return vmk.prefix_decode_paged(inp["q"], inp["k_pages"], inp["v_pages"], inp["prefix_pages"],
                                        inp["suffix_pages"], inp.get("slens"))
+    if opname == "dsa_project":                           # q stands for the three outputs in the checks
+        return vmk.dsa_project(inp["x"], inp["pos"], inp["rope_cos"], inp["rope_sin"], inp["weights"], inp["kv"],
+                               inp["ik"])[0]
     return vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], inp.get("lens"))
 
 
@@ -115,11 +127,20 @@ def std_op(opname, inp):
         return spec.torch_sdpa(inp["q"], inp["k"], inp["v"], inp["bits"])
     if opname == "decode":
         return decode.torch_sdpa(inp["q"], inp["k"], inp["v"], inp.get("lens"))
+    if opname == "dsa_project":
+        from vmk.ops import dsa_project
+        return dsa_project.torch_ref(inp["x"], inp["pos"], inp["rope_cos"], inp["rope_sin"], inp["weights"])[0]
     return dsa.torch_fp32_ref(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], inp.get("lens"))
 
 
 def op_bytes_flops(opname, shape, inp_host):
-    from vmk.ops import decode, dsa, prefix, prefix_paged, spec
+    from vmk.ops import decode, dsa, dsa_project, prefix, prefix_paged, spec
+    if opname == "dsa_project":                            # dominant: the q products (Wq_b and Wiq_b) and cq
+        total = dsa_project.algorithmic_bytes(shape)
+        B = shape["B"]
+        q_rows = dsa_project.H * (dsa_project.DN + dsa_project.DR) + dsa_project.HI * dsa_project.DI
+        dom = q_rows * dsa_project.QL * 2 + B * dsa_project.QL * 2 + B * q_rows * 4
+        return total, dom, dsa_project.flops(shape)
     if opname == "prefix_paged":
         sl = None if inp_host.get("slens") is None else inp_host["slens"].numpy()
         total = prefix_paged.algorithmic_bytes(shape, sl)
@@ -152,9 +173,19 @@ def distinct_sets(opname, inp0, total_bytes, count=None):
     n = count or max(2, int(math.ceil((1 << 30) / max(total_bytes, 1))))
     sets = [inp0]
     big = {"prefix": ("q", "kp", "vp", "ks", "vs"), "spec": ("q", "k", "v"), "dsa": ("q", "kv", "iq", "ik"),
-           "decode": ("q", "k", "v"), "prefix_paged": ("q", "k_pages", "v_pages")}[opname]
+           "decode": ("q", "k", "v"), "prefix_paged": ("q", "k_pages", "v_pages"), "dsa_project": ()}[opname]
     g = torch.Generator(device="cuda")
     g.manual_seed(1234)
+    if opname == "dsa_project":                            # fresh weights (N(0, 1/fan_in)) and hidden states
+        from vmk.ops import dsa_project
+        for _ in range(n - 1):
+            s = dict(inp0, weights=dict(inp0["weights"]))
+            s["x"] = torch.randn(inp0["x"].shape, device="cuda", generator=g).to(inp0["x"].dtype)
+            for k, w in inp0["weights"].items():
+                if k not in dsa_project.NORMS:
+                    s["weights"][k] = (torch.randn(w.shape, device="cuda", generator=g) * w.shape[-1] ** -0.5).to(w.dtype)
+            sets.append(s)
+        return sets
     for _ in range(n - 1):
         s = dict(inp0)
         for k in big:
@@ -177,7 +208,11 @@ def cpu_baseline(opname, shape, dist, inp_host, total_bytes, runs=3):
         import contextlib
         ctx, cores, blas = contextlib.nullcontext(), host_cpus, []
     sl = lambda x, n: None if x is None else x[:n]
-    if opname == "prefix":
+    if opname == "dsa_project":
+        work = lambda: oracle.dsa_project.ref64(inp_host["x"], inp_host["pos"], inp_host["rope_cos"],
+                                                inp_host["rope_sin"], **inp_host["weights"])
+        scale, sample = 1, f"the whole call ({shape['B']} tokens)"
+    elif opname == "prefix":
         N = shape["N"]
         ns = min(N, 8)
         sub = {k: inp_host[k][:ns] for k in ("q", "ks", "vs")}
@@ -223,16 +258,17 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     import torch
     import vmk
     from vmk import lib
-    from vmk.ops import OPS
-    op = OPS[opname]
+    op = op_module(opname)
     log(f"[{name}] {opname} {shape} {dist}: generating inputs")
     host = op.make_inputs(shape, seed=0, dist=dist)
-    inp0 = {k: (v.cuda() if isinstance(v, torch.Tensor) else v) for k, v in host.items()}
+    to_gpu = lambda v: v.cuda() if isinstance(v, torch.Tensor) else ({k: to_gpu(x) for k, x in v.items()}
+                                                                     if isinstance(v, dict) else v)
+    inp0 = {k: to_gpu(v) for k, v in host.items()}
     if opname == "spec":
         inp0["words"] = op.mask_words(inp0["bits"], shape["k"]).contiguous()
     total_bytes, dom_bytes, flops = op_bytes_flops(opname, shape, host)
     # Output check on the benchmark inputs and input-mutation check (reference bench.py:180-192).
-    snap = {k: v.clone() for k, v in inp0.items() if isinstance(v, torch.Tensor)}
+    snap = {k: v.clone() for k, v in inp0.items() if isinstance(v, torch.Tensor) and k not in WRITES.get(opname, ())}
     out = call_op(opname, inp0)
     torch.cuda.synchronize()
     mutated = [k for k, v in snap.items() if not torch.equal(v.view(torch.uint8), inp0[k].view(torch.uint8))]  # bits
@@ -274,6 +310,9 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
                dominant=dict(kernel=DOMINANT[opname], us=round(dom_us, 2), bytes=int(dom_bytes),
                              gbs=round(dom_gbs, 1), frac=round(dom_gbs / PEAK_HBM_GBS, 4)),
                output_check="ok", distinct_input_sets=len(sets))
+    if opname not in AB_OPS:                               # no reference A/B for this op: its torch form, graph-timed
+        ts = graph_us_per_call(opname, sets, steps, fn=lambda s: std_op(opname, s), check=False)
+        row["vs_torch"] = dict(torch_us_per_call=round(ts["median"], 2), speedup=round(ts["median"] / us, 2))
     row["dominant"]["traffic"] = measured_traffic(name, row["dominant"])
     log(f"[{name}] {us:9.2f} us/call (p10 {gt['p10']:.2f}, p90 {gt['p90']:.2f})  {gbs:7.1f} GB/s "
         f"({row['pct_peak']:.1f}% of 8 TB/s)  [median of {gt['n']} replays of a HIP graph of {steps} calls; "
@@ -287,33 +326,34 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     return row
 
 
-def graph_us_per_call(opname, sets, steps, replays=15):
+def graph_us_per_call(opname, sets, steps, replays=15, fn=None, check=True):
     """µs per call of the K calls captured once in a HIP graph (torch.cuda.CUDAGraph over the calls' launches on the
     capture stream, rotating over the same input sets), each replay timed between two events and synchronised:
     the GPU time of K steps without the Python and launch overhead of an eager loop, which dominates ops of a few
     µs.  Returns the median, p10 and p90 over `replays` replays.  Before timing, the output of the last captured call
     after each of 3 replays (with eager work and synchronisation in between) must equal an eager call on the same
-    inputs bit for bit."""
+    inputs bit for bit.  `fn(set)` replaces the op's call (then `check` may turn the bit comparison off)."""
     import torch
+    call = fn or (lambda s: call_op(opname, s))
     n = steps
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for i in range(3):
-            call_op(opname, sets[i % len(sets)])
+            call(sets[i % len(sets)])
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        outs = [call_op(opname, sets[i % len(sets)]) for i in range(n)]
+        outs = [call(sets[i % len(sets)]) for i in range(n)]
     last = outs[-1]
-    ref = call_op(opname, sets[(n - 1) % len(sets)]).clone()
+    ref = call(sets[(n - 1) % len(sets)]).clone()
     for _ in range(3):
         g.replay()
         torch.cuda.synchronize()
-        if not torch.equal(last.view(torch.int16), ref.view(torch.int16)):
+        if check and not torch.equal(last.view(torch.int16), ref.view(torch.int16)):
             raise SystemExit(f"{opname}: a graph replay differs from the eager call")
-        call_op(opname, sets[0])                          # eager work between replays
+        call(sets[0])                                     # eager work between replays
         torch.cuda.synchronize()
     times = []
     for _ in range(replays):
@@ -485,7 +525,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2,C2b")
+    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2,C2b,DP")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle timings")
     ap.add_argument("--ab-rounds", type=int, default=10,
                     help="shuffled rounds of the A/B comparison with the torch standard ops (0: skip it)")

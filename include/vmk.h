@@ -13,7 +13,7 @@
  *     the last failure on this host thread is returned by vmk_last_error().
  *
  * Each entry point replaces the `kernel(**inputs)` function of one of the reference's kernel modules, called with
- * the keyword inputs listed in verify.py:35-37; the Python modules verified-metal-kernels_amd/kernels/*_mi355x.py
+ * the keyword inputs listed in verify.py:35-37; the Python modules verified-metal-kernels_amd/kernels/<op>_mi355x.py
  * keep that signature and call into this ABI.
  */
 #ifndef VMK_H
@@ -168,6 +168,45 @@ int vmk_dsa_topk(const void* scores, const void* lens, void* idx, void* cnt, int
 /* Sparse absorbed-MLA attention over given indices (the reference's attn_mpp/attn_float, dsa_opus55_v7.py:975). */
 int vmk_dsa_sparse_mla(const void* q, const void* kv, const void* idx, const void* cnt, void* out, int64_t B,
                        int64_t L, void* workspace, size_t ws_bytes, void* stream);
+/* ------------------------------------------------------------------------------------------------ DSA projections
+ * The per-token projections that produce the DSA op's inputs from a hidden state.  The reference leaves them outside
+ * its op (ops/dsa.py:8-9); this build defines them after DeepSeek-V3.2's attention block (absorbed MLA and the
+ * lightning indexer), for one new token per request:
+ *   cq   = rmsnorm(x Wq_a^T) * q_norm, rounded to the input type          (B, 1536)
+ *   q    = [nope_h W_uk[h]^T | rope(pe_h)] per head h of cq Wq_b^T = [nope (128) | pe (64)]
+ *   iq   = [rope(pe_j) | nope_j] per head j of cq Wiq_b^T = [pe (64) | nope (64)]
+ *   w    = (x Wiw^T) / sqrt(64 * 128)                                     (B, 64) fp32, the op's pre-scaled w
+ *   kv[b, pos[b]] = [rmsnorm(kv_c) * kv_norm | rope(k_pe)],  [kv_c (512) | k_pe (64)] = x Wkv_a^T
+ *   ik[b, pos[b]] = layernorm(x Wik^T) * ik_norm_w + ik_norm_b, RoPE on its first 64 dims
+ * RMSNorm/LayerNorm eps 1e-6; RoPE rotates interleaved pairs (v[2i], v[2i+1]) by rope_cos/rope_sin[pos[b], i]
+ * (tables of (rope_rows, 32) fp32; pos is clamped into them).  The indexer's Hadamard rotation of DeepSeek-V3.2 is
+ * orthonormal and leaves every iq . ik unchanged, so it is not applied.
+ * Matrices are row-major (out, in), 16-bit like x (fp16; bf16 for the _bf16 entry); W_uk is the absorbed key half of
+ * Wkv_b pre-transposed to (128 heads, 512 latent, 128 nope); norm weights are fp32.  The struct is read on the host
+ * (its fields are device pointers).
+ *   x (B, 7168), pos (B,) int32, q (B, 128, 576), iq (B, 64, 128), w (B, 64) fp32, kv (B, L, 576), ik (B, L, 128)
+ * Only row pos[b] of each request's kv and ik is written, and only when 0 <= pos[b] < L. */
+typedef struct vmk_dsa_project_weights {
+  const void* wq_a;       /* (1536, 7168) */
+  const void* q_norm;     /* (1536,) fp32 */
+  const void* wq_b;       /* (24576, 1536): head h rows [192 h, 192 h + 128) nope, then 64 pe */
+  const void* w_uk;       /* (128, 512, 128) */
+  const void* wkv_a;      /* (576, 7168) */
+  const void* kv_norm;    /* (512,) fp32 */
+  const void* iwq_b;      /* (8192, 1536): head j rows [128 j, 128 j + 64) pe, then 64 nope */
+  const void* iwk;        /* (128, 7168) */
+  const void* ik_norm_w;  /* (128,) fp32 */
+  const void* ik_norm_b;  /* (128,) fp32 */
+  const void* iw;         /* (64, 7168) */
+} vmk_dsa_project_weights;
+size_t vmk_dsa_project_workspace_size(int64_t B);
+int vmk_dsa_project(const void* x, const void* pos, const void* rope_cos, const void* rope_sin, int64_t rope_rows,
+                    const vmk_dsa_project_weights* weights, void* q, void* iq, void* w, void* kv, void* ik, int64_t B,
+                    int64_t L, void* workspace, size_t ws_bytes, void* stream);
+int vmk_dsa_project_bf16(const void* x, const void* pos, const void* rope_cos, const void* rope_sin,
+                         int64_t rope_rows, const vmk_dsa_project_weights* weights, void* q, void* iq, void* w,
+                         void* kv, void* ik, int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream);
+
 /* The whole decode step: vmk_dsa_indexer_select followed by vmk_dsa_sparse_mla (idx/cnt are written). */
 int vmk_dsa_decode(const void* q, const void* kv, const void* iq, const void* ik, const void* w, const void* lens,
                    void* out, void* idx, void* cnt, int64_t B, int64_t L, void* workspace, size_t ws_bytes,
@@ -177,7 +216,7 @@ int vmk_dsa_decode(const void* q, const void* kv, const void* iq, const void* ik
  * No reference counterpart (the reference times whole calls only, bench.py:61-96).  The next launch of kernel
  * `kernel_id` on this host thread is bracketed by hipEventRecord(before) and hipEventRecord(after) on its stream.
  * Ids: 0 spec_partial, 1 spec_combine, 2 prefix_partial, 3 prefix_combine, 4 dsa_indexer, 5 dsa_select (final),
- *      6 dsa_attn, 7 dsa_combine, 8 dsa_select_scan. */
+ *      6 dsa_attn, 7 dsa_combine, 8 dsa_select_scan, 9 the q products of vmk_dsa_project. */
 int vmk_profile_next(void* before_event, void* after_event, int kernel_id);
 
 /* ---------------------------------------------------------------------------------------------- test hooks

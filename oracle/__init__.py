@@ -12,4 +12,4 @@ Pinning (tests/test_oracle.py): float64 SDPA of PyTorch on the CPU as an indepen
 (q = 0 gives the mean of V over the allowed keys, constant V rows, a single allowed key), the cascade/LSE identity,
 brute-force sorting for the top-k, and planted mistakes that each of those checks must catch.
 """
-from . import prefix, prefix_paged, spec, dsa, decode  # noqa: F401
+from . import prefix, prefix_paged, spec, dsa, decode, dsa_project  # noqa: F401

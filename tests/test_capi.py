@@ -234,3 +234,40 @@ def test_noalloc_entry_point_refuses_oversized_shapes_without_a_gpu():
     assert rc == 1 and b"static scratch" in L.vmk_last_error()
     rc = L.vmk_spec_verify_noalloc(p, p, p, p, p, 2, 64, 32, 8, 128, 65536, 1, None)   # wrong word count
     assert rc == 1 and b"ceil(kd/32)" in L.vmk_last_error()
+
+
+def test_dsa_project_rejects_before_launch(lib):
+    """The projections' host checks (weights struct, sizes, workspace) return 1 before anything is launched."""
+    from vmk import lib as L
+    assert lib.vmk_dsa_project_workspace_size(0) == 0
+    assert lib.vmk_dsa_project_workspace_size(4) > (4 << 20)
+    fake = ctypes.c_void_p(1 << 20)
+    wts = L.DsaProjectWeights(*([1 << 20] * len(L.PROJECT_WEIGHT_FIELDS)))
+    ws = lib.vmk_dsa_project_workspace_size(4)
+    args = lambda wp, B, nbytes: (fake, fake, fake, fake, 64, wp, fake, fake, fake, fake, fake, B, 100, fake, nbytes,
+                                  None)
+    rc = lib.vmk_dsa_project(*args(None, 4, ws))
+    assert rc == 1 and b"null weights" in lib.vmk_last_error()
+    rc = lib.vmk_dsa_project(*args(ctypes.addressof(wts), 0, ws))
+    assert rc == 1 and b"out of range" in lib.vmk_last_error()
+    rc = lib.vmk_dsa_project(*args(ctypes.addressof(wts), 4, 1024))
+    assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
+    wts.iw = None
+    rc = lib.vmk_dsa_project_bf16(*args(ctypes.addressof(wts), 4, ws))
+    assert rc == 1 and b"null weight pointer" in lib.vmk_last_error()
+
+
+def test_dsa_project_wrapper_checks_shapes_without_gpu():
+    import torch
+    import vmk
+    from vmk.ops import dsa_project as op
+    pos = torch.zeros(2, dtype=torch.int32)
+    cs = torch.zeros(16, 32)
+    kv, ik = torch.zeros(2, 16, 576, dtype=torch.float16), torch.zeros(2, 16, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="7168"):
+        vmk.dsa_project(torch.zeros(2, 100, dtype=torch.float16), pos, cs, cs, {}, kv, ik)
+    x = torch.zeros(2, op.DIM, dtype=torch.float16)
+    with pytest.raises(ValueError, match="weights must be a dict"):
+        vmk.dsa_project(x, pos, cs, cs, {}, kv, ik)
+    with pytest.raises(ValueError, match="rope tables"):
+        vmk.dsa_project(x, pos, cs, torch.zeros(16, 31), {}, kv, ik)

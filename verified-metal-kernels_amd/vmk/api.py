@@ -11,6 +11,8 @@ current stream is capturing (`reserve_workspace` beforehand, or one eager call o
 After a failed call the buffer is set aside the same way and the next call starts from a fresh zeroed one, since a
 call that stops half-way can leave the workspace head (which must stay zero between calls) non-zero.
 """
+import ctypes
+
 import torch
 
 from . import lib
@@ -412,3 +414,53 @@ def dsa_decode(q, kv, iq, ik, w, lens=None, out=None, idx=None, cnt=None):
             0 if lens is None else lens.data_ptr(), out.data_ptr(), idx.data_ptr(), cnt.data_ptr(), B, L,
             ws.data_ptr(), ws.numel(), _stream(q))
     return out
+
+
+# ---------------------------------------------------------------------------------------------- DSA projections
+def dsa_project(x, pos, rope_cos, rope_sin, weights, kv, ik, q=None, iq=None, w=None):
+    """The projections that make the DSA op's inputs for one new token per request (include/vmk.h,
+    vmk_dsa_project): x (B, 7168) and the matrices of `weights` (a dict with the fields of vmk_dsa_project_weights)
+    fp16 or bf16, norm weights fp32, pos (B,) int32, rope_cos/rope_sin (rows, 32) fp32.  Writes row pos[b] of the
+    caches kv (B, L, 576) and ik (B, L, 128) (when 0 <= pos[b] < L) and returns q (B,128,576), iq (B,64,128) of x's
+    dtype and w (B,64) fp32."""
+    from .ops import dsa_project as op
+    dt, sfx = _elem(x)
+    _need(x, "x", dt, 2)
+    B = x.shape[0]
+    if x.shape[1] != op.DIM:
+        raise ValueError(f"x {tuple(x.shape)}: expected (B, {op.DIM})")
+    _need(pos, "pos", torch.int32, 1)
+    if pos.shape[0] != B:
+        raise ValueError(f"pos {tuple(pos.shape)}: expected ({B},)")
+    _need(rope_cos, "rope_cos", torch.float32, 2)
+    _need(rope_sin, "rope_sin", torch.float32, 2)
+    if rope_cos.shape != rope_sin.shape or rope_cos.shape[1] != op.DR // 2 or rope_cos.shape[0] < 1:
+        raise ValueError(f"rope tables {tuple(rope_cos.shape)}, {tuple(rope_sin.shape)}: expected (rows, 32) each")
+    if not isinstance(weights, dict) or set(weights) != set(lib.PROJECT_WEIGHT_FIELDS):
+        raise ValueError(f"weights must be a dict with exactly the keys {lib.PROJECT_WEIGHT_FIELDS}")
+    for name, shape in op.WEIGHT_SHAPES.items():
+        _need(weights[name], name, torch.float32 if name in op.NORMS else dt, len(shape))
+        if tuple(weights[name].shape) != shape:
+            raise ValueError(f"{name} {tuple(weights[name].shape)}: expected {shape}")
+    _need(kv, "kv", dt, 3)
+    _need(ik, "ik", dt, 3)
+    L = kv.shape[1]
+    if tuple(kv.shape) != (B, L, op.DC + op.DR) or tuple(ik.shape) != (B, L, op.DI):
+        raise ValueError(f"kv {tuple(kv.shape)}, ik {tuple(ik.shape)}: expected ({B}, L, 576), ({B}, L, 128)")
+    for name, t, shape, tdt in (("q", q, (B, op.H, op.DC + op.DR), dt), ("iq", iq, (B, op.HI, op.DI), dt),
+                                ("w", w, (B, op.HI), torch.float32)):
+        if t is not None:
+            _need(t, name, tdt, len(shape))
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{name} {tuple(t.shape)}: expected {shape}")
+    _resident(x=x, pos=pos, rope_cos=rope_cos, rope_sin=rope_sin, kv=kv, ik=ik, q=q, iq=iq, w=w, **weights)
+    dev = x.device
+    q = torch.empty(B, op.H, op.DC + op.DR, dtype=dt, device=dev) if q is None else q
+    iq = torch.empty(B, op.HI, op.DI, dtype=dt, device=dev) if iq is None else iq
+    w = torch.empty(B, op.HI, dtype=torch.float32, device=dev) if w is None else w
+    wts = lib.DsaProjectWeights(*[weights[name].data_ptr() for name in lib.PROJECT_WEIGHT_FIELDS])
+    ws = workspace(lib.load().vmk_dsa_project_workspace_size(B), dev)
+    _launch("vmk_dsa_project" + sfx, ws, x.data_ptr(), pos.data_ptr(), rope_cos.data_ptr(), rope_sin.data_ptr(),
+            rope_cos.shape[0], ctypes.addressof(wts), q.data_ptr(), iq.data_ptr(), w.data_ptr(), kv.data_ptr(),
+            ik.data_ptr(), B, L, ws.data_ptr(), ws.numel(), _stream(x))
+    return q, iq, w

@@ -6,6 +6,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(os.path.dirname(HERE), "csrc")
+INCLUDE = os.path.join(os.path.dirname(os.path.dirname(HERE)), "include")   # the C ABI header (vmk.h)
 LIB = os.path.join(HERE, "libvmk.so")
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
@@ -20,7 +21,7 @@ def sources():
 def build(verbose=False, extra=()):
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     tmp = LIB + ".tmp"
-    cmd = [hipcc, *FLAGS, *extra, "-I", CSRC, *sources(), "-o", tmp]
+    cmd = [hipcc, *FLAGS, *extra, "-I", CSRC, "-I", INCLUDE, *sources(), "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     p = subprocess.run(cmd, capture_output=True, text=True)

@@ -45,10 +45,22 @@ _SIGS = {
     "vmk_dsa_topk": [_c_vp] * 4 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_sparse_mla": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_decode": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_project_workspace_size": [_c_i64],
+    # x, pos, rope_cos, rope_sin, rope_rows, &weights (host struct), q, iq, w, kv, ik, B, L, workspace, bytes, stream
+    "vmk_dsa_project": [_c_vp] * 4 + [_c_i64, _c_vp] + [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_project_bf16": [_c_vp] * 4 + [_c_i64, _c_vp] + [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
 }
 _RET = {"vmk_last_error": ctypes.c_char_p, "vmk_spec_workspace_size": _c_sz, "vmk_spec_noalloc_max_bytes": _c_sz, "vmk_prefix_workspace_size": _c_sz,
         "vmk_prefix_paged_workspace_size": _c_sz,
-        "vmk_dsa_workspace_size": _c_sz, "vmk_decode_workspace_size": _c_sz}
+        "vmk_dsa_workspace_size": _c_sz, "vmk_decode_workspace_size": _c_sz, "vmk_dsa_project_workspace_size": _c_sz}
+
+# struct vmk_dsa_project_weights of include/vmk.h: device pointers of the projection weights, in its field order.
+PROJECT_WEIGHT_FIELDS = ("wq_a", "q_norm", "wq_b", "w_uk", "wkv_a", "kv_norm", "iwq_b", "iwk", "ik_norm_w",
+                         "ik_norm_b", "iw")
+
+
+class DsaProjectWeights(ctypes.Structure):
+    _fields_ = [(name, _c_vp) for name in PROJECT_WEIGHT_FIELDS]
 
 
 class VmkError(RuntimeError):
@@ -76,7 +88,7 @@ def load():
 # Kernel ids of vmk_profile_next (include/vmk.h).
 KERNEL_IDS = {"spec_partial": 0, "spec_combine": 1, "prefix_partial": 2, "prefix_combine": 3,
               "dsa_indexer": 4, "dsa_select": 5, "dsa_attn": 6, "dsa_combine": 7,
-              "dsa_select_scan": 8}
+              "dsa_select_scan": 8, "dsa_project_q": 9}
 
 
 def exported_symbols():

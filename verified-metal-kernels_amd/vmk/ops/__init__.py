@@ -1,6 +1,7 @@
 """Op contracts: shapes, case lists, seeded input generators and PyTorch standard ops: the reference's three ops and
 this build's single-token decode and paged shared-prefix decode."""
 from . import prefix, prefix_paged, spec, dsa, decode  # noqa: F401
+from . import dsa_project  # noqa: F401  (DSA's input projections; not a verifier op)
 
 OPS = {"prefix": prefix, "prefix_paged": prefix_paged, "spec": spec, "dsa": dsa, "decode": decode}
 
