@@ -5,7 +5,8 @@
 Prints human-readable progress on stderr and ONE JSON line on stdout.  A "step" is one call of the op on one batch
 of the headline configuration (BASELINE configs[1] = C2, shared-prefix decode at scale); `value` is its achieved
 HBM throughput (algorithmic bytes / time per call, inputs resident in HBM), `ops` holds the same figures for every
-configuration (C1..C5, and this build's D1-D3 decode, P2 paged prefix, C2b bf16, DP the DSA input projections).
+configuration (C1..C5, and this build's D1-D3 decode, P2/P2n paged prefix in HND/NHD pages, C2b bf16, DP the
+DSA input projections).
 Method:
   * the kernel's output on the timed inputs is checked against the PyTorch standard op first
     (allclose atol=rtol=1e-2, bench.py:180-192 of the reference), and the inputs are checked for modification;
@@ -67,6 +68,7 @@ def config_table():
             ("C5", "dsa", *dsa.CONFIGS["C5"]),
             ("D1", "decode", *decode.CONFIGS["D1"]), ("D2", "decode", *decode.CONFIGS["D2"]),
             ("D3", "decode", *decode.CONFIGS["D3"]), ("P2", "prefix_paged", *prefix_paged.CONFIGS["P2"]),
+            ("P2n", "prefix_paged", *prefix_paged.CONFIGS["P2n"]),
             ("C2b", "prefix", *prefix.CONFIGS["C2b"]), ("DP", "dsa_project", *dsa_project.CONFIGS["DP"])]
 
 
@@ -109,7 +111,7 @@ def call_op(opname, inp):
         return vmk.decode(inp["q"], inp["k"], inp["v"], inp.get("lens"))
     if opname == "prefix_paged":
         return vmk.prefix_decode_paged(inp["q"], inp["k_pages"], inp["v_pages"], inp["prefix_pages"],
-                                       inp["suffix_pages"], inp.get("slens"))
+                                       inp["suffix_pages"], inp.get("slens"), layout=inp.get("layout", "HND"))
     if opname == "dsa_project":                           # q stands for the three outputs in the checks
         return vmk.dsa_project(inp["x"], inp["pos"], inp["rope_cos"], inp["rope_sin"], inp["weights"], inp["kv"],
                                inp["ik"])[0]
@@ -525,7 +527,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2,C2b,DP")
+    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2,P2n,C2b,DP")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle timings")
     ap.add_argument("--ab-rounds", type=int, default=10,
                     help="shuffled rounds of the A/B comparison with the torch standard ops (0: skip it)")

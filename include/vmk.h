@@ -106,6 +106,13 @@ int vmk_prefix_decode_paged(const void* q, const void* k_pages, const void* v_pa
                             const void* suffix_pages, const void* slens, void* out, int64_t N, int64_t Hq,
                             int64_t Hkv, int64_t D, int64_t num_pages, int64_t page_size, int64_t P,
                             int64_t max_suffix_pages, void* workspace, size_t ws_bytes, void* stream);
+/* The same op over a page pool in the layout FlashInfer calls NHD: k_pages, v_pages (num_pages, page_size, Hkv, D),
+ * a page's rows of one head Hkv * D elements apart.  Same arguments, limits (also Hkv <= 4096), workspace size and
+ * plans as vmk_prefix_decode_paged; the output is bit-equal to it on the same logical cache. */
+int vmk_prefix_decode_paged_nhd(const void* q, const void* k_pages, const void* v_pages, const void* prefix_pages,
+                                const void* suffix_pages, const void* slens, void* out, int64_t N, int64_t Hq,
+                                int64_t Hkv, int64_t D, int64_t num_pages, int64_t page_size, int64_t P,
+                                int64_t max_suffix_pages, void* workspace, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------- bf16 inputs
  * The reference kernels read fp16 only (README.md:140: on bf16 inputs they produce invalid values).  These entry points
@@ -124,6 +131,11 @@ int vmk_prefix_decode_paged_bf16(const void* q, const void* k_pages, const void*
                                  const void* suffix_pages, const void* slens, void* out, int64_t N, int64_t Hq,
                                  int64_t Hkv, int64_t D, int64_t num_pages, int64_t page_size, int64_t P,
                                  int64_t max_suffix_pages, void* workspace, size_t ws_bytes, void* stream);
+int vmk_prefix_decode_paged_nhd_bf16(const void* q, const void* k_pages, const void* v_pages,
+                                     const void* prefix_pages, const void* suffix_pages, const void* slens, void* out,
+                                     int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t num_pages,
+                                     int64_t page_size, int64_t P, int64_t max_suffix_pages, void* workspace,
+                                     size_t ws_bytes, void* stream);
 int vmk_dsa_indexer_select_bf16(const void* iq, const void* ik, const void* w, const void* lens, void* idx, void* cnt,
                                 int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream);
 int vmk_dsa_indexer_bf16(const void* iq, const void* ik, const void* w, const void* lens, void* scores, int64_t B,

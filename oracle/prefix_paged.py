@@ -28,9 +28,12 @@ def gather_rows(kpool, vpool, pages, nrows):
     return np.concatenate(ks, 1), np.concatenate(vs, 1)
 
 
-def ref64(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None, **_):
-    """Returns (N, Hq, D) float64."""
+def ref64(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None, layout="HND", **_):
+    """Returns (N, Hq, D) float64.  The pools are (num_pages, Hkv, ps, D), or (num_pages, ps, Hkv, D) with
+    layout="NHD"."""
     q, kpool, vpool = to64(q), to64(k_pages), to64(v_pages)
+    if layout == "NHD":
+        kpool, vpool = kpool.transpose(0, 2, 1, 3), vpool.transpose(0, 2, 1, 3)
     pp, sp, sl = toint(prefix_pages), toint(suffix_pages), toint(slens)
     N, Hq, d = q.shape
     num_pages, Hkv, ps, _ = kpool.shape

@@ -82,6 +82,12 @@ def test_entry_points_reject_before_launch(lib):
     rc = lib.vmk_prefix_decode_paged(fake, fake, fake, fake, fake, None, fake, 4, 32, 8, 128, 100, 48, 96, 2, fake,
                                      1 << 30, None)
     assert rc == 1 and b"page_size" in lib.vmk_last_error()
+    rc = lib.vmk_prefix_decode_paged_nhd(fake, fake, fake, fake, fake, None, fake, 4, 32, 8, 128, 100, 48, 96, 2,
+                                         fake, 1 << 30, None)
+    assert rc == 1 and b"page_size" in lib.vmk_last_error()
+    rc = lib.vmk_prefix_decode_paged_nhd(fake, fake, fake, fake, fake, None, fake, 4, 8192, 8192, 128, 100, 64, 128,
+                                         2, fake, 1 << 30, None)
+    assert rc == 1 and b"at most 4096 KV heads" in lib.vmk_last_error()
     rc = lib.vmk_dsa_decode(fake, fake, fake, fake, fake, None, fake, fake, fake, 2, 5000, fake, 1024, None)
     assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
     rc = lib.vmk_dsa_decode(fake, fake, fake, fake, None, None, fake, fake, fake, 2, 5000, fake, 1 << 30, None)
@@ -105,6 +111,19 @@ def test_python_wrappers_validate_shapes_without_gpu():
                         torch.zeros(2, 8, 100, 128, dtype=torch.float16), torch.zeros(2, 8, 1, dtype=torch.int32))
     with pytest.raises(TypeError):
         vmk.spec_verify(q.float(), q, q, q)
+    # Paged prefix: the layout names the pool's shape, checked before the device.
+    qp = torch.zeros(2, 32, 128, dtype=torch.float16)
+    pool = torch.zeros(10, 8, 64, 128, dtype=torch.float16)                    # HND (num_pages, Hkv, ps, D)
+    pp, sp = torch.zeros(2, dtype=torch.int32), torch.zeros(2, 1, dtype=torch.int32)
+    with pytest.raises(ValueError, match="layout"):
+        vmk.prefix_decode_paged(qp, pool, pool, pp, sp, layout="HDN")
+    with pytest.raises(ValueError, match="expected"):
+        vmk.prefix_decode_paged(qp, pool, pool[:, :4].contiguous(), pp, sp)
+    nhd = pool.transpose(1, 2).contiguous()                                     # (num_pages, ps, Hkv, D)
+    with pytest.raises(ValueError, match="ROCm device"):
+        vmk.prefix_decode_paged(qp, nhd, nhd, pp, sp, layout="NHD")
+    with pytest.raises(ValueError, match="expected"):
+        vmk.prefix_decode_paged(qp, nhd, nhd[:, :32].contiguous(), pp, sp, layout="NHD")
 
 
 def test_bf16_reaches_the_bf16_entry_points():

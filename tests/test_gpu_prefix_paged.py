@@ -75,3 +75,39 @@ def test_paged_all_pages_absent_rows_are_nan_like_the_oracle():
     r = oracle.prefix_paged.ref64(**inp)
     o = out.float().cpu().numpy().astype(np.float64)
     assert same_pattern(o, r) and np.isnan(o[1]).all() and not np.isnan(o[[0, 2]]).any()
+
+
+# NHD pools: the HND pool transposed to (num_pages, ps, Hkv, D).  The plans and the arithmetic do not depend on the
+# layout, so the output must be the HND call's bits; absent pages, NaN spare pages and partial last tiles included.
+NHD = [SAME[0], SAME[1], SAME[3], SAME[4], SAME[5], SAME[8], SAME[9], ORACLE[0], ORACLE[2], ORACLE[4],
+       (dict(N=6, P=1024, S=300, ps=64, dtype="bf16", absent=1), "randn", 18)]
+
+
+@pytest.mark.parametrize("shape,dist,seed", NHD)
+def test_nhd_equals_hnd(shape, dist, seed):
+    import vmk
+    print(f"paged NHD vs HND {shape} {dist} seed={seed}", flush=True)
+    inp = prefix_paged.make_inputs(shape, seed=seed, dist=dist, device="cuda")
+    args = (inp["prefix_pages"], inp["suffix_pages"], inp["slens"])
+    a = vmk.prefix_decode_paged(inp["q"], inp["k_pages"], inp["v_pages"], *args)
+    kn, vn = prefix_paged.to_nhd(inp["k_pages"]), prefix_paged.to_nhd(inp["v_pages"])
+    b = vmk.prefix_decode_paged(inp["q"], kn, vn, *args, layout="NHD")
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_nhd_parity_vs_oracle():
+    """The NHD entry on its own against the float64 oracle (absent pages, ragged suffixes, NaN spare pages)."""
+    import prefix_paged_mi355x
+    shape = dict(N=9, P=2560, S=700, S_min=0, ps=128, absent=2)
+    print(f"paged NHD vs oracle {shape}", flush=True)
+    inp = prefix_paged.make_inputs(shape, seed=19, device="cuda")
+    nhd = dict(inp, k_pages=prefix_paged.to_nhd(inp["k_pages"]), v_pages=prefix_paged.to_nhd(inp["v_pages"]))
+    out = prefix_paged_mi355x.kernel(**nhd, layout="NHD")
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy().astype(np.float64)
+    r = oracle.prefix_paged.ref64(**inp)
+    assert same_pattern(o, r)
+    em, ea = nerr(o, r)
+    print(f"  err max {em:.3e} mean {ea:.3e}")
+    assert em <= 1e-2

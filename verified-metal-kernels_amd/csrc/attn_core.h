@@ -302,13 +302,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const f16* tile) {
 // lp = dma_lane(lane, i & 7): the rows of block j = i & 7 start 1024 j bytes into the tile half, which the load takes
 // as its scalar offset: a buffer load with the half's resource in scalar registers and lp as the only per-lane
 // operand, so a whole tile costs no per-lane address arithmetic.
+// A source whose tile rows are not contiguous (Src::kStrided) gives the bytes from one row to the next for the tile
+// at key0, uniform over the wave (src.row_bytes(key0), a multiple of 256): block j then starts 4 j rows in, lane
+// quarter q (lane / 16) reads row 4 j + q, and the resource spans the 32 rows.  The LDS layout does not change.
 template <class Src>
 __device__ __forceinline__ void issue_dma_full(char* __restrict__ stage, const Src& src, int key0, int i,
                                                uint32_t lp) {
   const int j = i & 7;
-  const __amdgpu_buffer_rsrc_t r = tile_rsrc(i < 8 ? src.ktile(key0) : src.vtile(key0));
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, VMK_LPTR(stage + (i < 8 ? 0 : 8192) + j * 1024), 16, lp, 1024 * j, 0,
-                                           0);
+  const f16* tile = i < 8 ? src.ktile(key0) : src.vtile(key0);
+  if constexpr (Src::kStrided) {
+    const uint32_t rb = src.row_bytes(key0);
+    const uint32_t lps = lp + (uint32_t)((threadIdx.x & 63) >> 4) * (rb - 256);
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(tile), 0, (int)(31 * rb + 256), 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, VMK_LPTR(stage + (i < 8 ? 0 : 8192) + j * 1024), 16, lps,
+                                             (int)(4 * j * rb), 0, 0);
+  } else {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(tile_rsrc(tile), VMK_LPTR(stage + (i < 8 ? 0 : 8192) + j * 1024), 16,
+                                             lp, 1024 * j, 0, 0);
+  }
 }
 
 template <class Src>
@@ -317,7 +329,12 @@ __device__ __forceinline__ void issue_dma_part(char* __restrict__ stage, const S
   const int j = i & 7;
   const f16* tile = i < 8 ? src.ktile(key0) : src.vtile(key0);
   const int row = 4 * j + (lane >> 4);
-  const char* gp = reinterpret_cast<const char*>(key0 + row < src.kend ? tile + row * 128 : g_zero_row) + (lp & 255);
+  const f16* rowp;
+  if constexpr (Src::kStrided)
+    rowp = reinterpret_cast<const f16*>(reinterpret_cast<const char*>(tile) + (size_t)row * src.row_bytes(key0));
+  else
+    rowp = tile + row * 128;
+  const char* gp = reinterpret_cast<const char*>(key0 + row < src.kend ? rowp : g_zero_row) + (lp & 255);
   __builtin_amdgcn_global_load_lds(VMK_GPTR(gp), VMK_LPTR(stage + (i < 8 ? 0 : 8192) + j * 1024), 16, 0, 0);
 }
 
@@ -434,9 +451,10 @@ __device__ __forceinline__ void ring_walk(char* ring, const Src& src, int kbeg, 
 // (NS - 1 tiles in flight while one is computed; NS <= 4 keeps the wait counts within vmcnt's range), unrolled by NS
 // so every stage offset is a compile-time constant.  ring is this wave's ring (DMA destinations); base is the LDS
 // address the read offsets of tl are relative to (they include the ring's offset from it).
-// The key source `src` provides: ktile(key0) / vtile(key0) (the 32 contiguous K / V rows of the tile starting at
-// key0, a multiple of 32 from the range start; rows at or past kend are not read), kend, scale (log2-domain softmax
-// scale) and mask(s, key0, g) (masked scores of the raw S^T tile -> -inf).
+// The key source `src` provides: ktile(key0) / vtile(key0) (the first of the 32 K / V rows of the tile starting at
+// key0, a multiple of 32 from the range start; rows at or past kend are not read; the rows are 256 bytes apart, or
+// src.row_bytes(key0) apart when Src::kStrided), kend, scale (log2-domain softmax scale) and mask(s, key0, g)
+// (masked scores of the raw S^T tile -> -inf).
 template <int NS, class Src, class V>
 __device__ __forceinline__ void wave_walk(RowState& st, const V (&qb)[8], char* __restrict__ ring,
                                           const char* __restrict__ base, const TileLanes& tl, const Src& src,

@@ -127,6 +127,7 @@ struct IkSrc {
   const f16* kbase;
   const f16* vbase;
   int kend;
+  static constexpr bool kStrided = false;   // rows 256 bytes apart
   __device__ const f16* ktile(int key0) const { return kbase + (size_t)key0 * kDI; }
   __device__ const f16* vtile(int key0) const { return ktile(key0); }
 };

@@ -51,6 +51,7 @@ struct RangeSrc {
   const f16* vbase;
   int kend;
   float scale;
+  static constexpr bool kStrided = false;   // rows 256 bytes apart
   __device__ const f16* ktile(int key0) const { return kbase + (size_t)key0 * 128; }
   __device__ const f16* vtile(int key0) const { return vbase + (size_t)key0 * 128; }
   __device__ void mask(floatx16& s, int key0, int g) const {
@@ -66,18 +67,23 @@ struct RangeSrc {
 };
 
 // Keys [kbeg, kend) of one KV head of a sequence in a paged cache: pages of ps rows (ps a multiple of 32, so a tile
-// never straddles two pages) laid out (num_pages, Hkv, ps, 128), the sequence's pages listed in `table`.  Lane t
-// holds the K and V row addresses of the range's tile t (keys kbeg + 32 t ..; kbeg is a multiple of 32 and a range
-// has at most 2048 keys, i.e. 64 tiles), worked out once per lane, so a tile finds its rows with readlanes only (no
-// division or multiply per tile).  An id outside [0, num_pages) is an absent page: its tiles read a zero tile and
-// its keys are masked out.
+// never straddles two pages) laid out (num_pages, Hkv, ps, 128) (HND: a page's rows of one head are contiguous) or,
+// with kNHD, (num_pages, ps, Hkv, 128) (a page's rows are Hkv * 256 bytes apart), the sequence's pages listed in
+// `table`.  Lane t holds the K and V row addresses of the range's tile t (keys kbeg + 32 t ..; kbeg is a multiple of
+// 32 and a range has at most 2048 keys, i.e. 64 tiles), worked out once per lane, so a tile finds its rows with
+// readlanes only (no division or multiply per tile).  An id outside [0, num_pages) is an absent page: its tiles read
+// a zero tile (contiguous rows in either layout) and its keys are masked out.
+template <bool kNHD>
 struct PagedSrc {
   const f16* kt;           // this lane's tile: K rows, or g_zero_tile when its page is absent
   const f16* vt;           //                   V rows
   int here;                // 1 when this lane's tile has a page
   int kbeg, kend;
   float scale;
+  uint32_t rb_page;        // NHD: bytes between the rows of a page (Hkv * 256)
+  static constexpr bool kStrided = kNHD;
   __device__ int tile(int key0) const { return (key0 - kbeg) >> 5; }
+  __device__ uint32_t row_bytes(int key0) const { return present(key0) ? rb_page : 256u; }
   __device__ static const f16* lane_ptr(const f16* p, int t) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, t), hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), t);
@@ -99,17 +105,21 @@ struct PagedSrc {
   }
 };
 
-__device__ __forceinline__ PagedSrc paged_src(const PrefixArgs& a, const int* table, int ntable, int h, int kbeg,
-                                              int kend) {
-  PagedSrc s;
+template <bool kNHD>
+__device__ __forceinline__ PagedSrc<kNHD> paged_src(const PrefixArgs& a, const int* table, int ntable, int h,
+                                                    int kbeg, int kend) {
+  PagedSrc<kNHD> s;
   s.kbeg = kbeg;
   s.kend = kend;
   s.scale = a.sl2;
+  s.rb_page = (uint32_t)a.Hkv * 256u;
   const int key = kbeg + kTile * (int)(threadIdx.x & 63);     // this lane's tile
   const int slot = key / a.ps;
   const int page = key < kend && slot < ntable ? table[slot] : -1;
   s.here = (unsigned)page < (unsigned)a.num_pages;
-  const size_t off = (((size_t)page * a.Hkv + h) * a.ps + (key - slot * a.ps)) * 128;
+  const size_t row = key - slot * a.ps;                      // the tile's first row within its page
+  const size_t off =
+      (kNHD ? ((size_t)page * a.ps + row) * a.Hkv + h : ((size_t)page * a.Hkv + h) * a.ps + row) * 128;
   s.kt = s.here ? a.kp + off : g_zero_tile;
   s.vt = s.here ? a.vp + off : g_zero_tile;
   return s;
@@ -254,9 +264,12 @@ __device__ __forceinline__ void suffix_walk(const PrefixArgs& a, char* smem, con
   }
 }
 
+// The kernels' key source, a template argument: contiguous caches, or a page pool in the HND or NHD layout.
+constexpr int kContig = 0, kPagedHND = 1, kPagedNHD = 2;
+
 // Suffix item `sitem` (request, KV head, suffix chunk) of 4 waves.  Fused: the prefix partials are finished (an
 // earlier launch) and the item writes its rows' outputs; otherwise it writes its partial to po_s / pml_s.
-template <bool kPaged, class V>
+template <int kPaged, class V>
 __device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int sitem) {
   const int split = sitem % a.nsplit_s;
   int nh = sitem / a.nsplit_s, sn = 0;
@@ -270,9 +283,9 @@ __device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int
   if (!a.order) sn = suffix_len(a, n);
   if (kbeg >= sn && !a.fuse && !a.merge) return;        // whole workgroup: nothing of this suffix is here
   const int kend = min(sn, kbeg + a.chunk_s);
-  if constexpr (kPaged) {
-    suffix_walk<V>(a, smem, paged_src(a, a.suffix_pages + (size_t)n * a.max_sp, a.max_sp, h, kbeg, kend), n, h, nh,
-                split, kbeg);
+  if constexpr (kPaged != kContig) {
+    const int* table = a.suffix_pages + (size_t)n * a.max_sp;
+    suffix_walk<V>(a, smem, paged_src<kPaged == kPagedNHD>(a, table, a.max_sp, h, kbeg, kend), n, h, nh, split, kbeg);
   } else {
     RangeSrc src;
     src.scale = a.sl2;
@@ -286,7 +299,7 @@ __device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int
 
 
 // Suffix items, after the prefix launch has written the prefix partials.
-template <bool kPaged, class V>
+template <int kPaged, class V>
 __global__ __launch_bounds__(256) void prefix_partial_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
   suffix_item<kPaged, V>(a, smem, blockIdx.x);
@@ -327,7 +340,7 @@ __device__ void build_suffix_order(const PrefixArgs& a, uint32_t* cnt /* LDS, 25
 
 // Prefix item (KV head h, row block rb, prefix chunk): NW waves own 32 of the N*G rows each and share one LDS ring,
 // so the prefix chunk is streamed from HBM once per 32*NW rows.
-template <int NW, bool kPaged, class V>
+template <int NW, int kPaged, class V>
 __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem, int item) {
   const int split = item % a.nsplit_p;
   const int rb = (item / a.nsplit_p) % a.nrb_p;
@@ -346,8 +359,8 @@ __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem
                        a.N * a.G - row0, kbeg, ntiles, a.po_p + (size_t)item * rows_wg * 128,
                        a.pml_p + (size_t)item * rows_wg * 2);
   };
-  if constexpr (kPaged) {
-    walk(paged_src(a, a.prefix_pages, a.P / a.ps, h, kbeg, kend));
+  if constexpr (kPaged != kContig) {
+    walk(paged_src<kPaged == kPagedNHD>(a, a.prefix_pages, a.P / a.ps, h, kbeg, kend));
   } else {
     RangeSrc src;
     src.scale = a.sl2;
@@ -359,7 +372,7 @@ __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem
   }
 }
 
-template <int NW, bool kPaged, class V>
+template <int NW, int kPaged, class V>
 __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kRowsSmemBytes];
   if (blockIdx.x == 0 && a.order) build_suffix_order<64 * NW>(a, reinterpret_cast<uint32_t*>(smem));
@@ -371,7 +384,7 @@ __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
 // arithmetic is that of a row-block wave (the same tiles in the same order through the same tile function), so the
 // output bits do not depend on which form ran; several units share a workgroup so that the grid stays within one
 // dispatch round when the row-block grid would not.
-template <int NS, bool kPaged, class V>
+template <int NS, int kPaged, class V>
 __device__ __forceinline__ void prefix_unit(const PrefixArgs& a, char* smem, int u, int w) {
   const int lane = threadIdx.x & 63;
   const int split = u % a.nsplit_p, h = u / a.nsplit_p;            // one row block (nrb_p == 1)
@@ -388,8 +401,8 @@ __device__ __forceinline__ void prefix_unit(const PrefixArgs& a, char* smem, int
   auto walk = [&](const auto& src) {
     wave_walk<NS>(st, qb, smem + ring_off, smem, tl, src, kbeg, 0, ntiles, 1, lane);
   };
-  if constexpr (kPaged) {
-    walk(paged_src(a, a.prefix_pages, a.P / a.ps, h, kbeg, kend));
+  if constexpr (kPaged != kContig) {
+    walk(paged_src<kPaged == kPagedNHD>(a, a.prefix_pages, a.P / a.ps, h, kbeg, kend));
   } else {
     RangeSrc src;
     src.scale = a.sl2;
@@ -407,7 +420,7 @@ __device__ __forceinline__ void prefix_unit(const PrefixArgs& a, char* smem, int
 // sharing a ring, or a.units single-wave units per workgroup), then suffix items writing their partials.  No item
 // depends on another.
 constexpr int kMixedSmemBytes = kRowsSmemBytes > kAttnSmemBytes ? kRowsSmemBytes : kAttnSmemBytes;
-template <bool kPaged, class V>
+template <int kPaged, class V>
 __global__ __launch_bounds__(256) void prefix_mixed_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kMixedSmemBytes];
   const int upw = a.units;
@@ -530,7 +543,7 @@ static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int
 }
 
 // Plan, workspace carve-up and launches of one prefix call (contiguous or paged; a's K/V pointers are set).
-template <bool kPaged, class V>
+template <int kPaged, class V>
 static int prefix_launch(PrefixArgs& a, const void* q, void* out, const void* slens, bool ragged, int64_t N,
                          int64_t Hq, int64_t Hkv, int64_t D, int64_t P, int64_t S, void* workspace, hipStream_t s) {
   PrefixPlan p = prefix_plan(N, Hq, Hkv, P, S);
@@ -615,7 +628,7 @@ static int prefix_decode(const void* q, const void* kp, const void* vp, const vo
   a.q = (const f16*)q; a.kp = (const f16*)kp; a.vp = (const f16*)vp; a.ks = (const f16*)ks; a.vs = (const f16*)vs;
   a.prefix_pages = a.suffix_pages = nullptr;
   a.ps = a.max_sp = a.num_pages = 0;
-  return prefix_launch<false, V>(a, q, out, slens, ragged != 0, N, Hq, Hkv, D, P, S, workspace, (hipStream_t)stream);
+  return prefix_launch<kContig, V>(a, q, out, slens, ragged != 0, N, Hq, Hkv, D, P, S, workspace, (hipStream_t)stream);
 }
 
 extern "C" int vmk_prefix_decode(const void* q, const void* kp, const void* vp, const void* ks, const void* vs,
@@ -641,7 +654,7 @@ extern "C" size_t vmk_prefix_paged_workspace_size(int64_t N, int64_t Hq, int64_t
   return vmk_prefix_workspace_size(N, Hq, Hkv, D, P, page_size * max_suffix_pages, 1);
 }
 
-template <class V>
+template <int kLayout, class V>
 static int prefix_decode_paged(const void* q, const void* k_pages, const void* v_pages, const void* prefix_pages,
                                const void* suffix_pages, const void* slens, void* out, int64_t N, int64_t Hq,
                                int64_t Hkv, int64_t D, int64_t num_pages, int64_t page_size, int64_t P,
@@ -660,6 +673,7 @@ static int prefix_decode_paged(const void* q, const void* k_pages, const void* v
             "sizes out of range");
   VMK_CHECK(aligned16(q) && aligned16(out) && aligned16(k_pages) && aligned16(v_pages),
             "tensors must be 16-byte aligned");
+  VMK_CHECK(kLayout != kPagedNHD || Hkv <= 4096, "NHD pages: at most 4096 KV heads");
   const int64_t S = page_size * max_suffix_pages;
   const size_t need = vmk_prefix_paged_workspace_size(N, Hq, Hkv, D, P, page_size, max_suffix_pages);
   VMK_CHECK(workspace && ws_bytes >= need, "workspace too small (query vmk_prefix_paged_workspace_size)");
@@ -668,7 +682,7 @@ static int prefix_decode_paged(const void* q, const void* k_pages, const void* v
   a.prefix_pages = (const int*)prefix_pages;
   a.suffix_pages = (const int*)suffix_pages;
   a.ps = (int)page_size; a.max_sp = (int)max_suffix_pages; a.num_pages = (int)num_pages;
-  return prefix_launch<true, V>(a, q, out, slens, slens != nullptr, N, Hq, Hkv, D, P, S, workspace,
+  return prefix_launch<kLayout, V>(a, q, out, slens, slens != nullptr, N, Hq, Hkv, D, P, S, workspace,
                                 (hipStream_t)stream);
 }
 
@@ -677,8 +691,9 @@ extern "C" int vmk_prefix_decode_paged(const void* q, const void* k_pages, const
                                        void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D, int64_t num_pages,
                                        int64_t page_size, int64_t P, int64_t max_suffix_pages, void* workspace,
                                        size_t ws_bytes, void* stream) {
-  return prefix_decode_paged<half8>(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, out, N, Hq, Hkv, D,
-                                    num_pages, page_size, P, max_suffix_pages, workspace, ws_bytes, stream);
+  return prefix_decode_paged<kPagedHND, half8>(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, out, N, Hq,
+                                               Hkv, D, num_pages, page_size, P, max_suffix_pages, workspace,
+                                               ws_bytes, stream);
 }
 
 extern "C" int vmk_prefix_decode_paged_bf16(const void* q, const void* k_pages, const void* v_pages,
@@ -686,6 +701,28 @@ extern "C" int vmk_prefix_decode_paged_bf16(const void* q, const void* k_pages, 
                                             void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D,
                                             int64_t num_pages, int64_t page_size, int64_t P, int64_t max_suffix_pages,
                                             void* workspace, size_t ws_bytes, void* stream) {
-  return prefix_decode_paged<bf16x8>(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, out, N, Hq, Hkv, D,
-                                     num_pages, page_size, P, max_suffix_pages, workspace, ws_bytes, stream);
+  return prefix_decode_paged<kPagedHND, bf16x8>(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, out, N, Hq,
+                                                Hkv, D, num_pages, page_size, P, max_suffix_pages, workspace,
+                                                ws_bytes, stream);
+}
+
+extern "C" int vmk_prefix_decode_paged_nhd(const void* q, const void* k_pages, const void* v_pages,
+                                           const void* prefix_pages, const void* suffix_pages, const void* slens,
+                                           void* out, int64_t N, int64_t Hq, int64_t Hkv, int64_t D,
+                                           int64_t num_pages, int64_t page_size, int64_t P, int64_t max_suffix_pages,
+                                           void* workspace, size_t ws_bytes, void* stream) {
+  return prefix_decode_paged<kPagedNHD, half8>(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, out, N, Hq,
+                                               Hkv, D, num_pages, page_size, P, max_suffix_pages, workspace,
+                                               ws_bytes, stream);
+}
+
+extern "C" int vmk_prefix_decode_paged_nhd_bf16(const void* q, const void* k_pages, const void* v_pages,
+                                                const void* prefix_pages, const void* suffix_pages,
+                                                const void* slens, void* out, int64_t N, int64_t Hq, int64_t Hkv,
+                                                int64_t D, int64_t num_pages, int64_t page_size, int64_t P,
+                                                int64_t max_suffix_pages, void* workspace, size_t ws_bytes,
+                                                void* stream) {
+  return prefix_decode_paged<kPagedNHD, bf16x8>(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, out, N, Hq,
+                                                Hkv, D, num_pages, page_size, P, max_suffix_pages, workspace,
+                                                ws_bytes, stream);
 }

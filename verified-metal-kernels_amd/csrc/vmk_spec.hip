@@ -38,6 +38,7 @@ struct SpecSrc {
   u32x8 mw;          // the row's mask words; words at or past nw are not used
   int nw, kend, tail0;
   float scale;
+  static constexpr bool kStrided = false;   // rows 256 bytes apart
   __device__ const f16* ktile(int key0) const { return kbase + (size_t)key0 * 128; }
   __device__ const f16* vtile(int key0) const { return vbase + (size_t)key0 * 128; }
   __device__ uint32_t bit(int j) const {          // bit j of the row's mask, 0 <= j < 32 * kMaskWords

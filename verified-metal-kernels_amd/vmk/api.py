@@ -228,11 +228,14 @@ def prefix_decode(q, kp, vp, ks, vs, slens=None, out=None):
     return out
 
 
-def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None, out=None):
+def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None, out=None, layout="HND"):
     """Shared-prefix decode over a paged cache.  q (N, Hq, 128); k_pages/v_pages (num_pages, Hkv, page_size, 128)
-    with page_size a multiple of 32, all fp16 or all bf16; prefix_pages (P / page_size,) int32; suffix_pages
-    (N, max_sp) int32; slens (N,) int32 or None (full suffixes).  Page ids outside [0, num_pages) are absent pages
-    (left out).  Returns out (N, Hq, 128) of q's dtype."""
+    for layout "HND" or (num_pages, page_size, Hkv, 128) for "NHD", with page_size a multiple of 32, all fp16 or
+    all bf16; prefix_pages (P / page_size,) int32; suffix_pages (N, max_sp) int32; slens (N,) int32 or None (full
+    suffixes).  Page ids outside [0, num_pages) are absent pages (left out).  Returns out (N, Hq, 128) of q's
+    dtype; both layouts give the same bits for the same logical cache."""
+    if layout not in ("HND", "NHD"):
+        raise ValueError(f"layout {layout!r}: expected 'HND' or 'NHD'")
     dt, sfx = _elem(q)
     _need(q, "q", dt, 3)
     for t, n in ((k_pages, "k_pages"), (v_pages, "v_pages")):
@@ -240,9 +243,14 @@ def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=N
     _need(prefix_pages, "prefix_pages", torch.int32, 1)
     _need(suffix_pages, "suffix_pages", torch.int32, 2)
     N, Hq, D = q.shape
-    num_pages, Hkv, ps = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
-    if tuple(k_pages.shape) != (num_pages, Hkv, ps, D) or tuple(v_pages.shape) != tuple(k_pages.shape):
-        raise ValueError("k_pages/v_pages shapes do not match")
+    if layout == "HND":
+        num_pages, Hkv, ps = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
+        want = (num_pages, Hkv, ps, D)
+    else:
+        num_pages, ps, Hkv = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
+        want = (num_pages, ps, Hkv, D)
+    if tuple(k_pages.shape) != want or tuple(v_pages.shape) != tuple(k_pages.shape):
+        raise ValueError(f"k_pages {tuple(k_pages.shape)} / v_pages {tuple(v_pages.shape)}: expected {want} ({layout})")
     if suffix_pages.shape[0] != N:
         raise ValueError("suffix_pages must have N rows")
     if slens is not None:
@@ -259,7 +267,8 @@ def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=N
         raise lib.VmkError(f"unsupported paged prefix shape N={N} Hq={Hq} Hkv={Hkv} D={D} P={P} page_size={ps} "
                            f"max_suffix_pages={max_sp}")
     ws = workspace(ws_n, q.device)
-    _launch("vmk_prefix_decode_paged" + sfx, ws, q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
+    entry = "vmk_prefix_decode_paged" + ("_nhd" if layout == "NHD" else "") + sfx
+    _launch(entry, ws, q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
             prefix_pages.data_ptr() if P else 0, suffix_pages.data_ptr() if max_sp else 0,
             0 if slens is None else slens.data_ptr(), out.data_ptr(), N, Hq, Hkv, D, num_pages, ps, P, max_sp,
             ws.data_ptr(), ws.numel(), _stream(q))

@@ -35,6 +35,8 @@ _SIGS = {
     "vmk_decode_bf16": [_c_vp] * 5 + [_c_i64] * 5 + [_c_vp, _c_sz, _c_vp],
     "vmk_prefix_decode_bf16": [_c_vp] * 7 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
     "vmk_prefix_decode_paged_bf16": [_c_vp] * 7 + [_c_i64] * 8 + [_c_vp, _c_sz, _c_vp],
+    "vmk_prefix_decode_paged_nhd": [_c_vp] * 7 + [_c_i64] * 8 + [_c_vp, _c_sz, _c_vp],
+    "vmk_prefix_decode_paged_nhd_bf16": [_c_vp] * 7 + [_c_i64] * 8 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_indexer_select_bf16": [_c_vp] * 6 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_sparse_mla_bf16": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_decode_bf16": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],

@@ -22,7 +22,8 @@ HQ, HKV, D = prefix.HQ, prefix.HKV, prefix.D
 PS = 64                                                   # default page size
 L1_SHAPE = dict(N=4, P=2048, S=256, ps=64)
 BENCH_SHAPES = [dict(N=64, P=16384, S=2048, S_min=128, ps=64), dict(N=8, P=2048, S=256, ps=32)]
-CONFIGS = {"P2": (dict(N=64, P=16384, S=2048, S_min=128, ps=64), "outlier")}
+CONFIGS = {"P2": (dict(N=64, P=16384, S=2048, S_min=128, ps=64), "outlier"),
+           "P2n": (dict(N=64, P=16384, S=2048, S_min=128, ps=64, layout="NHD"), "outlier")}   # P2 in NHD pages
 FUZZ = [(dict(N=1, P=32, S=1, ps=32), "randn"), (dict(N=3, P=1024, S=77, ps=64), "randn"),
         (dict(N=5, P=4096, S=33, ps=128), "randn"), (dict(N=2, P=96, S=200, ps=96), "randn"),
         (dict(N=7, P=8192, S=700, S_min=1, ps=32), "randn"), (dict(N=4, P=2048, S=256, ps=256), "large"),
@@ -46,12 +47,13 @@ def make_inputs(shape, seed=0, dist="randn", device="cpu"):
         absent (-1).
     The pool holds 1/8 more pages than used; the spare pages are NaN, so a read of any page the tables do not name
     shows in the output.  Table entries past a request's rows in use are -1.  When S is not a whole number of pages,
-    slens = S is passed even without S_min (a suffix without slens fills all its pages)."""
+    slens = S is passed even without S_min (a suffix without slens fills all its pages).  With shape["layout"] =
+    "NHD" the pools are returned as (num_pages, ps, Hkv, D) (to_nhd) and the dict carries layout="NHD"."""
     ps = shape.get("ps", PS)
     N, P, S = shape["N"], shape["P"], shape["S"]
     if P % ps:
         raise ValueError(f"P={P} is not a whole number of pages of {ps}")
-    base = {k: v for k, v in shape.items() if k not in ("ps", "absent")}
+    base = {k: v for k, v in shape.items() if k not in ("ps", "absent", "layout")}
     c = prefix.make_inputs(base, seed=seed, dist=dist)
     kp, vp, ks, vs = (c[k] for k in ("kp", "vp", "ks", "vs"))          # CPU tensors of the op's dtype
     slens = None if c["slens"] is None else c["slens"].numpy()
@@ -89,8 +91,16 @@ def make_inputs(shape, seed=0, dist="randn", device="cpu"):
             if live.size:
                 sp[n, int(rng.choice(live))] = -1
     t = lambda a: torch.from_numpy(a).to(device)
-    return dict(q=c["q"].to(device), k_pages=kpool.to(device), v_pages=vpool.to(device), prefix_pages=t(pp),
-                suffix_pages=t(sp), slens=None if slens is None else t(slens))
+    out = dict(q=c["q"].to(device), k_pages=kpool.to(device), v_pages=vpool.to(device), prefix_pages=t(pp),
+               suffix_pages=t(sp), slens=None if slens is None else t(slens))
+    if shape.get("layout", "HND") == "NHD":
+        out.update(k_pages=to_nhd(out["k_pages"]), v_pages=to_nhd(out["v_pages"]), layout="NHD")
+    return out
+
+
+def to_nhd(pages):
+    """The same page pool in the layout FlashInfer calls NHD: (num_pages, Hkv, ps, D) -> (num_pages, ps, Hkv, D)."""
+    return pages.transpose(1, 2).contiguous()
 
 
 def gather(k_pages, v_pages, prefix_pages, suffix_pages, slens=None):
@@ -130,9 +140,11 @@ def row_inputs(inp, i):
 
 
 # ---------------------------------------------------------------- PyTorch standard op
-def torch_naive(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None, **_):
+def torch_naive(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None, layout="HND", **_):
     """Gather the pages into a dense per-request cache, then SDPA with the presence mask (prefix.torch_naive)."""
     import torch.nn.functional as F
+    if layout == "NHD":
+        k_pages, v_pages = k_pages.transpose(1, 2), v_pages.transpose(1, 2)
     kf, vf, m = gather(k_pages, v_pages, prefix_pages, suffix_pages, slens)
     return F.scaled_dot_product_attention(q[:, :, None, :], kf, vf, attn_mask=m, enable_gqa=True)[:, :, 0, :]
 
