@@ -137,12 +137,13 @@ def std_op(opname, inp):
 
 def op_bytes_flops(opname, shape, inp_host):
     from vmk.ops import decode, dsa, dsa_project, prefix, prefix_paged, spec
-    if opname == "dsa_project":                            # dominant: the q products (Wq_b and Wiq_b) and cq
-        total = dsa_project.algorithmic_bytes(shape)
+    if opname == "dsa_project":   # dominant: the heads launch (Wq_b, Wiq_b, W_uk against cq; q and iq out)
+        m = dsa_project
+        total = m.algorithmic_bytes(shape)
         B = shape["B"]
-        q_rows = dsa_project.H * (dsa_project.DN + dsa_project.DR) + dsa_project.HI * dsa_project.DI
-        dom = q_rows * dsa_project.QL * 2 + B * dsa_project.QL * 2 + B * q_rows * 4
-        return total, dom, dsa_project.flops(shape)
+        q_rows = m.H * (m.DN + m.DR) + m.HI * m.DI
+        dom = (q_rows * m.QL + m.H * m.DC * m.DN) * 2 + B * m.QL * 2 + B * (m.H * (m.DC + m.DR) + m.HI * m.DI) * 2
+        return total, dom, m.flops(shape)
     if opname == "prefix_paged":
         sl = None if inp_host.get("slens") is None else inp_host["slens"].numpy()
         total = prefix_paged.algorithmic_bytes(shape, sl)

@@ -228,7 +228,7 @@ int vmk_dsa_decode(const void* q, const void* kv, const void* iq, const void* ik
  * No reference counterpart (the reference times whole calls only, bench.py:61-96).  The next launch of kernel
  * `kernel_id` on this host thread is bracketed by hipEventRecord(before) and hipEventRecord(after) on its stream.
  * Ids: 0 spec_partial, 1 spec_combine, 2 prefix_partial, 3 prefix_combine, 4 dsa_indexer, 5 dsa_select (final),
- *      6 dsa_attn, 7 dsa_combine, 8 dsa_select_scan, 9 the q products of vmk_dsa_project. */
+ *      6 dsa_attn, 7 dsa_combine, 8 dsa_select_scan, 9 the heads launch of vmk_dsa_project (its q, iq products and the absorbed product). */
 int vmk_profile_next(void* before_event, void* after_event, int kernel_id);
 
 /* ---------------------------------------------------------------------------------------------- test hooks

@@ -6,15 +6,15 @@
 // (B tokens against up to 100 MB of weights), so the bound is HBM: 150 MB of weights per call.
 //
 // Launch 1 (proj_x_kernel): the x-side rows (Wq_a 1536, Wkv_a 576, Wik 128, Wiw 64 = 2304 rows of 7168) in row blocks
-//   of 32 and eight K parts of 896; partial sums per K part.
-// Launch 2 (proj_fin_kernel): per request, sums the K parts in order, RMSNorms cq (kept as the 16-bit operand of
-//   launch 3) and kv_c, LayerNorms ik, applies RoPE, writes the cache rows and w.
-// Launch 3 (proj_q_kernel): Wq_b (24576 rows) and Wiq_b (8192 rows) against cq, two row blocks of 32 per workgroup.
-// Launch 4 (proj_absorb_kernel): per head and quarter of its 512 latent dims, the absorbed product of the 16-bit nope
-//   part with W_uk[h] (512 x 128), RoPE of the pe parts, the q and iq outputs.
+//   of 64 and seven K parts of 1024: 252 workgroups of 8 waves, one dispatch round; partial sums per K part.
+// Launch 2 (proj_heads_kernel): 256 workgroups of 8 waves, each 128 rows of Wq_b or Wiq_b against cq.  Workgroup h
+//   (< 128) takes MLA head h's nope rows and then the absorbed product with W_uk[h] (512 x 128); workgroups 128 + p
+//   take the pe rows of heads 2p and 2p + 1 (RoPE) and finish token p's cache rows and w; workgroups 192 + j take
+//   indexer head j's rows (RoPE on the first 64).  Every workgroup first sums cq's K parts and RMSNorms it itself
+//   (the same arithmetic in each), so no launch runs between the two.
 // GEMV tiles use the 32x32x16 MFMA with weight rows as A and the batch (up to 32 tokens per tile) as B; every wave
 // issues all its weight loads before its first MFMA, and the K split inside a workgroup is summed through LDS in
-// wave order, so results do not depend on scheduling.
+// K order, so results do not depend on scheduling.
 #include "vmk.h"
 #include "vmk_common.h"
 #include "vmk_internal.h"
@@ -26,12 +26,15 @@ constexpr int kPQRows = kPH * (kPDn + kPDr);                 // 24576 rows of Wq
 constexpr int kPIRows = kPHi * kPDi;                         // 8192 rows of Wiq_b
 constexpr int kPXRows = kPQl + kPDc + kPDr + kPDi + kPHi;    // 2304 rows from x
 constexpr int kPXKv = kPQl, kPXIk = kPQl + kPDc + kPDr, kPXIw = kPXIk + kPDi;   // row offsets inside the x rows
-constexpr int kPKs = 8;                                      // K parts of launch 1
-constexpr int kPKPart = kPDim / kPKs;                        // 896
+constexpr int kPKs = 7;                                      // K parts of launch 1
+constexpr int kPKPart = kPDim / kPKs;                        // 1024
+constexpr int kPXBlock = 64;                                 // rows per workgroup of launch 1
 constexpr int kPCols = 32;                                   // tokens per GEMV tile
 constexpr float kPEps = 1e-6f;
-static_assert(kPKPart % (4 * 16) == 0 && kPQl % (4 * 16) == 0, "K splits of whole MFMA steps");
-constexpr int kPQBlocks = 2;                                 // row blocks per workgroup of launch 3
+constexpr int kPHeadsWG = kPH + kPH / 2 + kPHi;              // workgroups of launch 2 per token block: 128 + 64 + 64
+static_assert(kPDim % kPKs == 0 && kPKPart % (4 * 16) == 0 && kPQl % (4 * 16) == 0, "K splits of whole MFMA steps");
+static_assert(kPQl % 64 == 0 && (kPDc + kPDr) % 64 == 0 && kPDi % 64 == 0 && kPHi % 64 == 0,
+              "a row block of launch 1 never straddles two matrices");
 
 struct ProjArgs {
   const f16* x;            // (B, 7168)
@@ -48,8 +51,6 @@ struct ProjArgs {
   f16* ik;                 // (B, L, 128)
   int B, L;
   float* yx;               // (kPKs, B, kPXRows)
-  f16* cqn;                // (B, 1536)
-  float* yq;               // (B, kPQRows + kPIRows)
 };
 
 // A GEMV tile: acc (32 weight rows x 32 token columns, the mfma32 D layout) += W[r0 + r][k] * X[col][k] over NS
@@ -84,22 +85,23 @@ __device__ __forceinline__ void stage_rows(f16* xs, const f16* src, size_t ldsrc
   }
 }
 
-// The four waves' accumulators (same tile, different k ranges) summed in wave order: wave w then holds, in
-// out[0..3], rows 8 w + 4 g + c (c < 4) of column lane % 32.  slots: 4 x 4 KB of LDS.
-__device__ __forceinline__ void sum_waves(const floatx16& acc, float* slots, int w, int lane, float (&out)[4]) {
+// The accumulators of four waves (the same tile over K quarters q = 0..3) summed in K order: the wave of quarter q
+// then holds, in out[0..3], rows 8 q + 4 g + c (c < 4) of column lane % 32.  slots: the four waves' 16 KB of LDS.
+// Every thread of the workgroup calls it (it holds a workgroup barrier).
+__device__ __forceinline__ void sum_quarters(const floatx16& acc, float* slots, int q, int lane, float (&out)[4]) {
   floatx4* sl = reinterpret_cast<floatx4*>(slots);
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk)
-    sl[(w * 4 + blk) * 64 + lane] = floatx4{acc[4 * blk], acc[4 * blk + 1], acc[4 * blk + 2], acc[4 * blk + 3]};
+    sl[(q * 4 + blk) * 64 + lane] = floatx4{acc[4 * blk], acc[4 * blk + 1], acc[4 * blk + 2], acc[4 * blk + 3]};
   __syncthreads();
-  floatx4 t = sl[(0 * 4 + w) * 64 + lane];
+  floatx4 t = sl[(0 * 4 + q) * 64 + lane];
 #pragma unroll
-  for (int k = 1; k < 4; ++k) t += sl[(k * 4 + w) * 64 + lane];
+  for (int k = 1; k < 4; ++k) t += sl[(k * 4 + q) * 64 + lane];
 #pragma unroll
   for (int c = 0; c < 4; ++c) out[c] = t[c];
 }
 
-// x-side rows of row block rb (of 72) as (matrix, first row, rows of that matrix, row offset in yx).
+// x-side rows from `row` on as (matrix, its first row, rows of that matrix).
 __device__ __forceinline__ const f16* x_rows(const ProjArgs& a, int row, int& local, int& nrows) {
   if (row < kPXKv) { local = row; nrows = kPQl; return a.wq_a; }
   if (row < kPXIk) { local = row - kPXKv; nrows = kPDc + kPDr; return a.wkv_a; }
@@ -107,46 +109,51 @@ __device__ __forceinline__ const f16* x_rows(const ProjArgs& a, int row, int& lo
   local = row - kPXIw; nrows = kPHi; return a.iw;
 }
 
-// Launch 1: grid (72 row blocks * kPKs, token blocks), 256 threads; dynamic LDS max(ncol * kPKPart * 2, 16 KB).
+// Launch 1: grid (36 row blocks * kPKs, token blocks), 512 threads; dynamic LDS max(ncol * kPKPart * 2, 32 KB).
+// Wave w takes the 32-row tile w & 1 of the block over K quarter w >> 1 of the part.
 template <class V>
-__global__ __launch_bounds__(256) void proj_x_kernel(ProjArgs a) {
+__global__ __launch_bounds__(512) void proj_x_kernel(ProjArgs a) {
   extern __shared__ __attribute__((aligned(16))) char pl[];
   f16* xs = reinterpret_cast<f16*>(pl);
   const int rb = blockIdx.x / kPKs, ks = blockIdx.x % kPKs;
   const int c0 = blockIdx.y * kPCols, ncol = min(kPCols, a.B - c0);
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rt = w & 1, kq = w >> 1;
   int local, nrows;
-  const f16* W = x_rows(a, rb * 32, local, nrows);           // a row block never straddles two matrices
-  const int kw = ks * kPKPart + w * (kPKPart / 4);
+  const f16* W = x_rows(a, rb * kPXBlock, local, nrows);
+  const int kw = ks * kPKPart + kq * (kPKPart / 4);
   constexpr int NS = kPKPart / 4 / 16;
   u32x4 wv[NS];
-  gemv_issue(wv, W, kPDim, local, nrows, kw, lane);          // the weights fly while x is staged
+  gemv_issue(wv, W, kPDim, local + 32 * rt, nrows, kw, lane);     // the weights fly while x is staged
   stage_rows(xs, a.x, kPDim, c0, ncol, ks * kPKPart, kPKPart);
   __syncthreads();
   floatx16 acc = {};
   gemv_mma<V>(acc, wv, kw, xs, kPKPart, ks * kPKPart, ncol, lane);
-  __syncthreads();                                            // every wave is done with xs: it becomes the slots
+  __syncthreads();                                                // every wave is done with xs: it becomes the slots
   float out[4];
-  sum_waves(acc, reinterpret_cast<float*>(pl), w, lane, out);
+  sum_quarters(acc, reinterpret_cast<float*>(pl) + rt * 4096, kq, lane, out);
   const int col = lane & 31, g = lane >> 5;
   if (col < ncol) {
-    float* y = a.yx + ((size_t)ks * a.B + c0 + col) * kPXRows + rb * 32;
+    float* y = a.yx + ((size_t)ks * a.B + c0 + col) * kPXRows + rb * kPXBlock + 32 * rt;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) y[8 * w + 4 * g + c] = out[c];
+    for (int c = 0; c < 4; ++c) y[8 * kq + 4 * g + c] = out[c];
   }
 }
-static_assert(kPQl % 32 == 0 && (kPDc + kPDr) % 32 == 0 && kPDi % 32 == 0 && kPHi % 32 == 0, "whole row blocks");
 
-// Block sum of one value per thread (256 threads), returned to every thread.
-__device__ __forceinline__ float block_sum256(float v, float* red) {
+// Block sum of one value per thread (512 threads), returned to every thread; red: 8 floats of LDS.
+__device__ __forceinline__ float block_sum512(float v, float* red) {
   v = wave_sum(v);
   const int w = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[w] = v;
   __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
+  float s = red[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) s += red[i];
+  return s;
 }
 
+// x-side row `row` of token b: its K parts summed in part order.
 __device__ __forceinline__ float yx_sum(const ProjArgs& a, int b, int row) {
   float s = a.yx[(size_t)b * kPXRows + row];
 #pragma unroll
@@ -154,170 +161,192 @@ __device__ __forceinline__ float yx_sum(const ProjArgs& a, int b, int row) {
   return s;
 }
 
-// Launch 2: one workgroup of 256 threads per request.
-template <class V>
-__global__ __launch_bounds__(256) void proj_fin_kernel(ProjArgs a) {
-  typedef elem_t<V> E;
-  __shared__ float red[4];
-  const int b = blockIdx.x, t = threadIdx.x;
-  const int p = a.pos[b];
-  const int pr = min(max(p, 0), a.rope_rows - 1);            // the table row (clamped into the table)
-  const bool store = p >= 0 && p < a.L;                       // cache rows are written only inside the cache
-  // cq: 6 values per thread.
-  float cq[kPQl / 256], ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < kPQl / 256; ++i) {
-    cq[i] = yx_sum(a, b, t + 256 * i);
-    ss += cq[i] * cq[i];
-  }
-  const float rq = 1.f / sqrtf(block_sum256(ss, red) / kPQl + kPEps);
-  E* cqn = reinterpret_cast<E*>(a.cqn) + (size_t)b * kPQl;
-#pragma unroll
-  for (int i = 0; i < kPQl / 256; ++i) cqn[t + 256 * i] = (E)(cq[i] * rq * a.q_norm[t + 256 * i]);
-  // kv_c: 2 values per thread; k_pe: pairs on threads 0..31.
-  float kc[2];
-  ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    kc[i] = yx_sum(a, b, kPXKv + t + 256 * i);
-    ss += kc[i] * kc[i];
-  }
-  const float rk = 1.f / sqrtf(block_sum256(ss, red) / kPDc + kPEps);
+__device__ __forceinline__ int rope_row(const ProjArgs& a, int b) { return min(max(a.pos[b], 0), a.rope_rows - 1); }
+
+// Token b's cache rows (kv: RMSNorm of kv_c, RoPE of k_pe; ik: LayerNorm, RoPE of its first 64) and w, by 512 threads.
+// Rows are written only for a position inside the cache.
+template <class E>
+__device__ void finish_token(const ProjArgs& a, int b, float* red, float* ikn) {
+  const int t = threadIdx.x;
+  const int p = a.pos[b], pr = rope_row(a, b);
+  const bool store = p >= 0 && p < a.L;
+  const float kc = yx_sum(a, b, kPXKv + t);                   // kv_c: one value per thread
+  const float rk = 1.f / sqrtf(block_sum512(kc * kc, red) / kPDc + kPEps);
   E* kvr = reinterpret_cast<E*>(a.kv) + ((size_t)b * a.L + (store ? p : 0)) * (kPDc + kPDr);
-  if (store) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) kvr[t + 256 * i] = (E)(kc[i] * rk * a.kv_norm[t + 256 * i]);
-  }
-  const float cs = a.rcos[(size_t)pr * 32 + (t & 31)], sn = a.rsin[(size_t)pr * 32 + (t & 31)];
-  if (t < 32 && store) {
+  if (store) kvr[t] = (E)(kc * rk * a.kv_norm[t]);
+  if (t < 32 && store) {                                      // k_pe: pair t
+    const float cs = a.rcos[(size_t)pr * 32 + t], sn = a.rsin[(size_t)pr * 32 + t];
     const float x0 = yx_sum(a, b, kPXKv + kPDc + 2 * t), x1 = yx_sum(a, b, kPXKv + kPDc + 2 * t + 1);
     kvr[kPDc + 2 * t] = (E)(x0 * cs - x1 * sn);
     kvr[kPDc + 2 * t + 1] = (E)(x0 * sn + x1 * cs);
   }
-  // ik: LayerNorm over 128 values (threads 0..127), then RoPE on its first 64 (pairs on threads 0..31).
-  const float v = t < kPDi ? yx_sum(a, b, kPXIk + t) : 0.f;
-  const float mean = block_sum256(v, red) / kPDi;
+  const float v = t < kPDi ? yx_sum(a, b, kPXIk + t) : 0.f;   // ik: LayerNorm over 128 values
+  const float mean = block_sum512(v, red) / kPDi;
   const float d = t < kPDi ? v - mean : 0.f;
-  const float ri = 1.f / sqrtf(block_sum256(d * d, red) / kPDi + kPEps);
-  __shared__ float ikn[kPDi];
+  const float ri = 1.f / sqrtf(block_sum512(d * d, red) / kPDi + kPEps);
   if (t < kPDi) ikn[t] = d * ri * a.ik_w[t] + a.ik_b[t];
   __syncthreads();
-  E* ikr = reinterpret_cast<E*>(a.ik) + ((size_t)b * a.L + (store ? p : 0)) * kPDi;
   if (store && t < kPDi) {
-    float o;
+    E* ikr = reinterpret_cast<E*>(a.ik) + ((size_t)b * a.L + p) * kPDi;
+    float o = ikn[t];
     if (t < kPDr) {
       const int i = t >> 1;
       const float c2 = a.rcos[(size_t)pr * 32 + i], s2 = a.rsin[(size_t)pr * 32 + i];
       const float x0 = ikn[2 * i], x1 = ikn[2 * i + 1];
       o = (t & 1) ? x0 * s2 + x1 * c2 : x0 * c2 - x1 * s2;
-    } else {
-      o = ikn[t];
     }
     ikr[t] = (E)o;
   }
-  // w: 64 values.
   if (t < kPHi) a.w[(size_t)b * kPHi + t] = yx_sum(a, b, kPXIw + t) * (0.125f * 0.08838834764831845f);
 }
 
-// Launch 3: grid ((kPQRows + kPIRows) / (32 * kPQBlocks), token blocks), 256 threads; dynamic LDS
-// max(ncol * 1536 * 2, 16 KB) + 16 KB (the reduction slots).  Every wave issues the weights of all kPQBlocks row
-// blocks before the first MFMA.
+// Launch 2: grid (kPHeadsWG, token blocks), 512 threads; dynamic LDS max(ncol * 1536 * 2, 64 KB + ncol * 256).
+// Wave w takes row blocks 2 (w >> 2) and 2 (w >> 2) + 1 of the workgroup's four over K quarter w & 3.
 template <class V>
-__global__ __launch_bounds__(256) void proj_q_kernel(ProjArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char pl[];
-  f16* xs = reinterpret_cast<f16*>(pl);
-  // The reduction slots follow the staged tokens, at the offset the host sized the LDS with.
-  float* slots = reinterpret_cast<float*>(pl + max(min(kPCols, a.B) * kPQl * 2, 16384));
-  const int c0 = blockIdx.y * kPCols, ncol = min(kPCols, a.B - c0);
-  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  constexpr int NS = kPQl / 4 / 16;
-  u32x4 wv[kPQBlocks][NS];
-#pragma unroll
-  for (int j = 0; j < kPQBlocks; ++j) {
-    const int row0 = (blockIdx.x * kPQBlocks + j) * 32;
-    const bool qrows = row0 < kPQRows;                      // the q rows end on a block boundary
-    gemv_issue(wv[j], qrows ? a.wq_b : a.iwq_b, kPQl, qrows ? row0 : row0 - kPQRows, qrows ? kPQRows : kPIRows,
-               w * (kPQl / 4), lane);
-  }
-  stage_rows(xs, a.cqn, kPQl, c0, ncol, 0, kPQl);
-  __syncthreads();
-  const int col = lane & 31, g = lane >> 5;
-#pragma unroll
-  for (int j = 0; j < kPQBlocks; ++j) {
-    floatx16 acc = {};
-    gemv_mma<V>(acc, wv[j], w * (kPQl / 4), xs, kPQl, 0, ncol, lane);
-    float out[4];
-    sum_waves(acc, slots, w, lane, out);
-    if (col < ncol) {
-      float* y = a.yq + (size_t)(c0 + col) * (kPQRows + kPIRows) + (blockIdx.x * kPQBlocks + j) * 32;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) y[8 * w + 4 * g + c] = out[c];
-    }
-    __syncthreads();                                          // the slots are reused by the next block
-  }
-}
-static_assert(kPQRows % (32 * kPQBlocks) == 0 && kPIRows % (32 * kPQBlocks) == 0, "whole row blocks");
-
-// Launch 4: grid (128 heads * 4 quarters, token blocks), 256 threads.  Wave w of quarter qt computes rows (latent
-// dims) [128 qt + 32 w, + 32) of head h over K = 128 (8 steps); quarter 0 also applies RoPE to the pe parts.
-template <class V>
-__global__ __launch_bounds__(256) void proj_absorb_kernel(ProjArgs a) {
+__global__ __launch_bounds__(512) void proj_heads_kernel(ProjArgs a) {
   typedef elem_t<V> E;
-  __shared__ __attribute__((aligned(16))) E xs[kPCols * kPDn];  // the tokens' 16-bit nope parts of head h
-  const int h = blockIdx.x >> 2, qt = blockIdx.x & 3;
+  extern __shared__ __attribute__((aligned(16))) char pl[];
+  __shared__ float red[8], ikn[kPDi];
+  E* xs = reinterpret_cast<E*>(pl);                           // cq of the token block (ncol x 1536)
   const int c0 = blockIdx.y * kPCols, ncol = min(kPCols, a.B - c0);
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const size_t ldy = kPQRows + kPIRows;
-  const f16* W = a.w_uk + (size_t)h * kPDc * kPDn;
-  constexpr int NS = kPDn / 16;
-  const int r0 = 128 * qt + 32 * w;
-  u32x4 wv[NS];
-  gemv_issue(wv, W, kPDn, r0, kPDc, 0, lane);
-  for (int i = threadIdx.x; i < ncol * kPDn; i += 256) {
-    const int c = i / kPDn, d = i % kPDn;
-    xs[i] = (E)a.yq[(size_t)(c0 + c) * ldy + h * (kPDn + kPDr) + d];
-  }
-  __syncthreads();
-  const int col = lane & 31, g = lane >> 5;
-  floatx16 acc = {};
-  gemv_mma<V>(acc, wv, 0, reinterpret_cast<const f16*>(xs), kPDn, 0, ncol, lane);
-  if (col < ncol) {
-    E* qo = reinterpret_cast<E*>(a.q) + ((size_t)(c0 + col) * kPH + h) * (kPDc + kPDr) + r0;
+  const int kq = w & 3, bp = w >> 2;
+  const int wg = blockIdx.x;
+  // The workgroup's four row blocks: rows of Wq_b (nope of head wg, or pe of heads 2p, 2p + 1) or of Wiq_b.
+  auto block_rows = [&](int i, const f16*& W, int& nrows) -> int {
+    if (wg < kPH) { W = a.wq_b; nrows = kPQRows; return wg * (kPDn + kPDr) + 32 * i; }
+    if (wg < kPH + kPH / 2) {
+      const int hp = 2 * (wg - kPH) + (i >> 1);
+      W = a.wq_b; nrows = kPQRows; return hp * (kPDn + kPDr) + kPDn + 32 * (i & 1);
+    }
+    W = a.iwq_b; nrows = kPIRows; return (wg - kPH - kPH / 2) * kPDi + 32 * i;
+  };
+  constexpr int NS = kPQl / 4 / 16;
+  u32x4 wv[2][NS];
+  // cq first (its loads need most of the registers the weights take): wave w takes tokens w, w + 8, ...; lane l the
+  // rows [24 l, 24 l + 24), its K parts summed in part order.
+  for (int c = w; c < ncol; c += 8) {
+    const int b = c0 + c;
+    float v[24];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) qo[8 * (i / 4) + 4 * g + (i % 4)] = (E)acc[i];
+    for (int i = 0; i < 6; ++i) {
+      floatx4 s = *reinterpret_cast<const floatx4*>(a.yx + (size_t)b * kPXRows + 24 * lane + 4 * i);
+#pragma unroll
+      for (int ks = 1; ks < kPKs; ++ks)
+        s += *reinterpret_cast<const floatx4*>(a.yx + ((size_t)ks * a.B + b) * kPXRows + 24 * lane + 4 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * i + e] = s[e];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 24; ++k) ss += v[k] * v[k];
+    const float rq = 1.f / sqrtf(wave_sum(ss) / kPQl + kPEps);
+#pragma unroll
+    for (int k = 0; k < 24; ++k) xs[c * kPQl + 24 * lane + k] = (E)(v[k] * rq * a.q_norm[24 * lane + k]);
   }
-  if (qt != 0) return;
-  // RoPE of q's pe part (and, for h < 64, the indexer head h): thread t -> token t / 32, pair t % 32.
-  for (int i = threadIdx.x; i < ncol * 32; i += 256) {
-    const int c = i / 32, pi = i % 32, b = c0 + c;
-    const int pr = min(max(a.pos[b], 0), a.rope_rows - 1);
-    const float cs = a.rcos[(size_t)pr * 32 + pi], sn = a.rsin[(size_t)pr * 32 + pi];
-    const float* yb = a.yq + (size_t)b * ldy;
-    const float x0 = yb[h * (kPDn + kPDr) + kPDn + 2 * pi], x1 = yb[h * (kPDn + kPDr) + kPDn + 2 * pi + 1];
-    E* qo = reinterpret_cast<E*>(a.q) + ((size_t)b * kPH + h) * (kPDc + kPDr) + kPDc;
-    qo[2 * pi] = (E)(x0 * cs - x1 * sn);
-    qo[2 * pi + 1] = (E)(x0 * sn + x1 * cs);
-    if (h < kPHi) {
-      const float* yi = yb + kPQRows + h * kPDi;
-      E* io = reinterpret_cast<E*>(a.iq) + ((size_t)b * kPHi + h) * kPDi;
-      const float y0 = yi[2 * pi], y1 = yi[2 * pi + 1];
-      io[2 * pi] = (E)(y0 * cs - y1 * sn);
-      io[2 * pi + 1] = (E)(y0 * sn + y1 * cs);
-      io[kPDr + 2 * pi] = (E)yi[kPDr + 2 * pi];
-      io[kPDr + 2 * pi + 1] = (E)yi[kPDr + 2 * pi + 1];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const f16* W;
+    int nrows;
+    const int r0 = block_rows(2 * bp + j, W, nrows);
+    gemv_issue(wv[j], W, kPQl, r0, nrows, kq * (kPQl / 4), lane);
+  }
+  __syncthreads();                                            // cq staged
+  floatx16 acc[2] = {};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) gemv_mma<V>(acc[j], wv[j], kq * (kPQl / 4), reinterpret_cast<const f16*>(xs), kPQl, 0,
+                                          ncol, lane);
+  // MLA head workgroups: W_uk[h] rows [64 w, 64 w + 64) fly while the K quarters are summed.
+  constexpr int NU = kPDn / 16;
+  u32x4 wu[2][NU];
+  if (wg < kPH) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) gemv_issue(wu[j], a.w_uk + (size_t)wg * kPDc * kPDn, kPDn, 64 * w + 32 * j, kPDc, 0,
+                                           lane);
+  }
+  __syncthreads();                                            // every wave is done with xs: it becomes the slots
+  float out[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) sum_quarters(acc[j], reinterpret_cast<float*>(pl) + (bp * 2 + j) * 4096, kq, lane,
+                                           out[j]);
+  // This wave now holds rows 8 kq + 4 g + c (c < 4) of blocks 2 bp + j for token column col.
+  const int col = lane & 31, g = lane >> 5, b = c0 + col;
+  const bool live = col < ncol;
+  if (wg < kPH) {
+    // The nope part, rounded to the operand type, is the absorbed product's B operand (ncol x 128 after the slots).
+    E* xn = reinterpret_cast<E*>(pl + 65536);
+    if (live) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xn[col * kPDn + 32 * (2 * bp + j) + 8 * kq + 4 * g + c] = (E)out[j][c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      floatx16 qa = {};
+      gemv_mma<V>(qa, wu[j], 0, reinterpret_cast<const f16*>(xn), kPDn, 0, ncol, lane);
+      if (live) {
+        E* qo = reinterpret_cast<E*>(a.q) + ((size_t)b * kPH + wg) * (kPDc + kPDr) + 64 * w + 32 * j;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) qo[8 * (i / 4) + 4 * g + (i % 4)] = (E)qa[i];
+      }
+    }
+    return;
+  }
+  // RoPE pairs (rows 2m, 2m + 1 are c = 0, 1 and c = 2, 3 of one lane), with token b's table row.
+  const int pr = live ? rope_row(a, b) : 0;
+  if (wg < kPH + kPH / 2) {
+    if (live) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int i = 2 * bp + j, hp = 2 * (wg - kPH) + (i >> 1);
+        E* qo = reinterpret_cast<E*>(a.q) + ((size_t)b * kPH + hp) * (kPDc + kPDr) + kPDc;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const int e = 32 * (i & 1) + 8 * kq + 4 * g + 2 * m, pi = e >> 1;
+          const float cs = a.rcos[(size_t)pr * 32 + pi], sn = a.rsin[(size_t)pr * 32 + pi];
+          const float x0 = out[j][2 * m], x1 = out[j][2 * m + 1];
+          qo[e] = (E)(x0 * cs - x1 * sn);
+          qo[e + 1] = (E)(x0 * sn + x1 * cs);
+        }
+      }
+    }
+    const int tok = wg - kPH;                                 // token of the block whose cache rows this finishes
+    if (tok < ncol) finish_token<E>(a, c0 + tok, red, ikn);
+    return;
+  }
+  if (live) {
+    const int hj = wg - kPH - kPH / 2;
+    E* io = reinterpret_cast<E*>(a.iq) + ((size_t)b * kPHi + hj) * kPDi;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = 2 * bp + j;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int e = 32 * i + 8 * kq + 4 * g + 2 * m;
+        const float x0 = out[j][2 * m], x1 = out[j][2 * m + 1];
+        if (e < kPDr) {
+          const int pi = e >> 1;
+          const float cs = a.rcos[(size_t)pr * 32 + pi], sn = a.rsin[(size_t)pr * 32 + pi];
+          io[e] = (E)(x0 * cs - x1 * sn);
+          io[e + 1] = (E)(x0 * sn + x1 * cs);
+        } else {
+          io[e] = (E)x0;
+          io[e + 1] = (E)x1;
+        }
+      }
     }
   }
 }
 
 struct ProjPlan {
-  size_t yx, cqn, yq;      // bytes of each workspace region
+  size_t yx;               // bytes of the workspace's partial sums
 };
 
 static ProjPlan proj_plan(int64_t B) {
   ProjPlan p;
   p.yx = (size_t)kPKs * B * kPXRows * sizeof(float);
-  p.cqn = (size_t)B * kPQl * 2;
-  p.yq = (size_t)B * (kPQRows + kPIRows) * sizeof(float);
   return p;
 }
 
@@ -347,22 +376,16 @@ static int dsa_project(const void* x, const void* pos, const void* rope_cos, con
   a.q = (f16*)q; a.iq = (f16*)iq; a.w = (float*)w; a.kv = (f16*)kv; a.ik = (f16*)ik;
   a.B = (int)B; a.L = (int)L;
   a.yx = (float*)align_up((char*)workspace + kWsHead, 256);
-  a.cqn = (f16*)align_up((char*)a.yx + p.yx, 256);
-  a.yq = (float*)align_up((char*)a.cqn + p.cqn, 256);
   hipStream_t s = (hipStream_t)stream;
   const unsigned nbb = (unsigned)((B + kPCols - 1) / kPCols);
   const int ncol = (int)std::min<int64_t>(B, kPCols);
-  const size_t lds_x = std::max<size_t>((size_t)ncol * kPKPart * 2, 16384);
-  const size_t lds_q = std::max<size_t>((size_t)ncol * kPQl * 2, 16384) + 16384;
-  hipLaunchKernelGGL(proj_x_kernel<V>, dim3(kPXRows / 32 * kPKs, nbb), dim3(256), lds_x, s, a);
-  VMK_CHECK_HIP(hipGetLastError());
-  hipLaunchKernelGGL(proj_fin_kernel<V>, dim3((unsigned)B), dim3(256), 0, s, a);
+  const size_t lds_x = std::max<size_t>((size_t)ncol * kPKPart * 2, 32768);
+  const size_t lds_h = std::max<size_t>((size_t)ncol * kPQl * 2, 65536 + (size_t)ncol * kPDn * 2);
+  hipLaunchKernelGGL(proj_x_kernel<V>, dim3(kPXRows / kPXBlock * kPKs, nbb), dim3(512), lds_x, s, a);
   VMK_CHECK_HIP(hipGetLastError());
   prof_before(kKDsaProjectQ, s);
-  hipLaunchKernelGGL(proj_q_kernel<V>, dim3((kPQRows + kPIRows) / (32 * kPQBlocks), nbb), dim3(256), lds_q, s, a);
+  hipLaunchKernelGGL(proj_heads_kernel<V>, dim3(kPHeadsWG, nbb), dim3(512), lds_h, s, a);
   prof_after(kKDsaProjectQ, s);
-  VMK_CHECK_HIP(hipGetLastError());
-  hipLaunchKernelGGL(proj_absorb_kernel<V>, dim3(kPH * 4, nbb), dim3(256), 0, s, a);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
 }
@@ -374,7 +397,7 @@ using namespace vmk;
 extern "C" size_t vmk_dsa_project_workspace_size(int64_t B) {
   if (B < 1 || B > (1 << 20)) return 0;
   const ProjPlan p = proj_plan(B);
-  return kWsHead + p.yx + p.cqn + p.yq + 3 * 256;
+  return kWsHead + p.yx + 256;
 }
 
 extern "C" int vmk_dsa_project(const void* x, const void* pos, const void* rope_cos, const void* rope_sin,

@@ -34,9 +34,11 @@ L3_CASES = [(dict(N=8, P=1024, S=128, ps=64), "randn"), (dict(N=8, P=32768, S=10
             (dict(N=16, P=4096, S=512, S_min=1, ps=32), "randn"), (dict(N=4, P=8192, S=512, ps=64), "needle_suffix"),
             (dict(N=64, P=16384, S=2048, S_min=128, ps=64), "outlier")]
 EXTRA = [(dict(N=33, P=640, S=40, ps=32, absent=2), "randn"), (dict(N=20, P=40960, S=3000, S_min=1, ps=256), "randn"),
-         (dict(N=6, P=1024, S=300, ps=64, dtype="bf16"), "randn")]
+         (dict(N=6, P=1024, S=300, ps=64, dtype="bf16"), "randn"),
+         (dict(N=7, P=2048, S=500, S_min=1, ps=128, absent=1, layout="NHD"), "randn")]
 L4_CASES = [(dict(N=64, P=16384, S=2048, S_min=128, ps=64), "outlier"), (dict(N=8, P=2048, S=256, ps=32), "randn"),
-            (dict(N=12, P=3072, S=2500, S_min=1, ps=128, absent=2), "randn")]
+            (dict(N=12, P=3072, S=2500, S_min=1, ps=128, absent=2), "randn"),
+            (dict(N=16, P=4096, S=700, S_min=1, ps=64, layout="NHD"), "randn")]
 
 
 def make_inputs(shape, seed=0, dist="randn", device="cpu"):
