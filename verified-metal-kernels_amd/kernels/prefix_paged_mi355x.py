@@ -15,4 +15,4 @@ def kernel(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=None, layout="
     suffix_pages = suffix_pages.to(device=q.device, dtype=torch.int32).contiguous()
     if slens is not None:
         slens = slens.to(device=q.device, dtype=torch.int32).contiguous()
-    return vmk.prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, layout=layout)
+    return vmk.prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens, layout=layout or "HND")

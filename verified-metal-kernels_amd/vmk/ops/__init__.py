@@ -11,7 +11,7 @@ KEYS = {"prefix": ["q", "kp", "vp", "ks", "vs", "slens"],
         "spec": ["q", "k", "v", "bits"],
         "dsa": ["q", "kv", "iq", "ik", "w", "lens"],
         "decode": ["q", "k", "v", "lens"],
-        "prefix_paged": ["q", "k_pages", "v_pages", "prefix_pages", "suffix_pages", "slens"]}
+        "prefix_paged": ["q", "k_pages", "v_pages", "prefix_pages", "suffix_pages", "slens", "layout"]}
 
 
 def load_op(name):

@@ -8,6 +8,7 @@ pool, in the layout FlashInfer calls HND:
     prefix_pages: (P / ps,) int32                   the shared prefix's pages, in order
     suffix_pages: (N, max_sp) int32                 each request's suffix pages, in order
     slens: (N,) int32 or None                       suffix rows in use (None: all max_sp * ps)
+    layout: "HND", "NHD" or None (HND)              NHD pools are (num_pages, ps, Hkv, D)
 A page id outside [0, num_pages) is an absent page: its rows take no part in the softmax.
 """
 import math
