@@ -538,7 +538,7 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py measures one MI355X: the three ops run on a single GPU and this build has no multi-GPU path "
-            "(the sharding design is in DESIGN.md).  Run with --gpus 1.")
+            "(how the ops would shard over several GPUs is a design only).  Run with --gpus 1.")
         sys.exit(2)
     import torch
     import vmk
