@@ -80,7 +80,11 @@ def test_paged_all_pages_absent_rows_are_nan_like_the_oracle():
 # NHD pools: the HND pool transposed to (num_pages, ps, Hkv, D).  The plans and the arithmetic do not depend on the
 # layout, so the output must be the HND call's bits; absent pages, NaN spare pages and partial last tiles included.
 NHD = [SAME[0], SAME[1], SAME[3], SAME[4], SAME[5], SAME[8], SAME[9], ORACLE[0], ORACLE[2], ORACLE[4],
-       (dict(N=6, P=1024, S=300, ps=64, dtype="bf16", absent=1), "randn", 18)]
+       (dict(N=6, P=1024, S=300, ps=64, dtype="bf16", absent=1), "randn", 18),
+       # other head counts: rows 512 and 768 bytes apart, and Hkv = 1 (the two layouts coincide)
+       (dict(N=2, P=1024, S=200, ps=64, Hq=32, Hkv=2), "randn", 20),
+       (dict(N=5, P=384, S=130, S_min=1, ps=96, Hq=12, Hkv=3, absent=1), "randn", 21),
+       (dict(N=3, P=512, S=100, ps=32, Hq=16, Hkv=1), "randn", 22)]
 
 
 @pytest.mark.parametrize("shape,dist,seed", NHD)
