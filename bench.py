@@ -5,8 +5,8 @@
 Prints human-readable progress on stderr and ONE JSON line on stdout.  A "step" is one call of the op on one batch
 of the headline configuration (BASELINE configs[1] = C2, shared-prefix decode at scale); `value` is its achieved
 HBM throughput (algorithmic bytes / time per call, inputs resident in HBM), `ops` holds the same figures for every
-configuration (C1..C5, and this build's D1-D3 decode, P2/P2n paged prefix in HND/NHD pages, C2b bf16, DP the
-DSA input projections).
+configuration (C1..C5, and this build's D1-D3 decode, P2/P2n paged prefix in HND/NHD pages, D1p/D2n paged decode
+in HND/NHD pages, C2b bf16, DP the DSA input projections).
 Method:
   * the kernel's output on the timed inputs is checked against the PyTorch standard op first
     (allclose atol=rtol=1e-2, bench.py:180-192 of the reference), and the inputs are checked for modification;
@@ -46,7 +46,7 @@ PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16 MFMA
 METRIC = "µs/call per op + achieved HBM GB/s (% of MI355X peak) at bench shapes"
 HEADLINE = "C2"
 DOMINANT = {"prefix": "prefix_partial", "spec": "spec_partial", "dsa": "dsa_indexer", "decode": "spec_partial",
-            "prefix_paged": "prefix_partial", "dsa_project": "dsa_project_q"}
+            "prefix_paged": "prefix_partial", "dsa_project": "dsa_project_q", "decode_paged": "spec_partial"}
 # Inputs the ops write by contract (the projections append the new token's cache rows), left out of the
 # input-mutation check.
 WRITES = {"dsa_project": ("kv", "ik")}
@@ -62,13 +62,14 @@ def op_module(opname):
 
 
 def config_table():
-    from vmk.ops import decode, dsa, dsa_project, prefix, prefix_paged, spec
+    from vmk.ops import decode, decode_paged, dsa, dsa_project, prefix, prefix_paged, spec
     return [("C1", "prefix", *prefix.CONFIGS["C1"]), ("C2", "prefix", *prefix.CONFIGS["C2"]),
             ("C3", "spec", *spec.CONFIGS["C3"]), ("C4", "spec", *spec.CONFIGS["C4"]),
             ("C5", "dsa", *dsa.CONFIGS["C5"]),
             ("D1", "decode", *decode.CONFIGS["D1"]), ("D2", "decode", *decode.CONFIGS["D2"]),
             ("D3", "decode", *decode.CONFIGS["D3"]), ("P2", "prefix_paged", *prefix_paged.CONFIGS["P2"]),
             ("P2n", "prefix_paged", *prefix_paged.CONFIGS["P2n"]),
+            ("D1p", "decode_paged", *decode_paged.CONFIGS["D1p"]), ("D2n", "decode_paged", *decode_paged.CONFIGS["D2n"]),
             ("C2b", "prefix", *prefix.CONFIGS["C2b"]), ("DP", "dsa_project", *dsa_project.CONFIGS["DP"])]
 
 
@@ -109,6 +110,9 @@ def call_op(opname, inp):
         return vmk.spec_verify(inp["q"], inp["k"], inp["v"], inp["words"])
     if opname == "decode":
         return vmk.decode(inp["q"], inp["k"], inp["v"], inp.get("lens"))
+    if opname == "decode_paged":
+        return vmk.decode_paged(inp["q"], inp["k_pages"], inp["v_pages"], inp["page_table"], inp.get("lens"),
+                                layout=inp.get("layout", "HND"))
     if opname == "prefix_paged":
         return vmk.prefix_decode_paged(inp["q"], inp["k_pages"], inp["v_pages"], inp["prefix_pages"],
                                        inp["suffix_pages"], inp.get("slens"), layout=inp.get("layout", "HND"))
@@ -129,6 +133,9 @@ def std_op(opname, inp):
         return spec.torch_sdpa(inp["q"], inp["k"], inp["v"], inp["bits"])
     if opname == "decode":
         return decode.torch_sdpa(inp["q"], inp["k"], inp["v"], inp.get("lens"))
+    if opname == "decode_paged":
+        from vmk.ops import decode_paged
+        return decode_paged.torch_sdpa(**inp)
     if opname == "dsa_project":
         from vmk.ops import dsa_project
         return dsa_project.torch_ref(inp["x"], inp["pos"], inp["rope_cos"], inp["rope_sin"], inp["weights"])[0]
@@ -136,7 +143,7 @@ def std_op(opname, inp):
 
 
 def op_bytes_flops(opname, shape, inp_host):
-    from vmk.ops import decode, dsa, dsa_project, prefix, prefix_paged, spec
+    from vmk.ops import decode, decode_paged, dsa, dsa_project, prefix, prefix_paged, spec
     if opname == "dsa_project":   # dominant: the heads launch (Wq_b, Wiq_b, W_uk against cq; q and iq out)
         m = dsa_project
         total = m.algorithmic_bytes(shape)
@@ -158,11 +165,12 @@ def op_bytes_flops(opname, shape, inp_host):
         total = spec.algorithmic_bytes(shape)
         out = shape["B"] * shape["k"] * spec.HQ * spec.D * 2
         return total, total - out, spec.flops(shape)
-    if opname == "decode":
+    if opname in ("decode", "decode_paged"):
+        m = decode if opname == "decode" else decode_paged
         ln = None if inp_host.get("lens") is None else inp_host["lens"].numpy()
-        total = decode.algorithmic_bytes(shape, ln)
+        total = m.algorithmic_bytes(shape, ln)
         out = shape["B"] * decode.HQ * decode.D * 2
-        return total, total - out, decode.flops(shape, ln)
+        return total, total - out, m.flops(shape, ln)
     total = dsa.algorithmic_bytes(shape)
     B, L = shape["B"], shape["L"]
     indexer = B * L * dsa.DI * 2 + B * dsa.HI * dsa.DI * 2 + B * dsa.HI * 4    # ik + iq + w
@@ -176,7 +184,8 @@ def distinct_sets(opname, inp0, total_bytes, count=None):
     n = count or max(2, int(math.ceil((1 << 30) / max(total_bytes, 1))))
     sets = [inp0]
     big = {"prefix": ("q", "kp", "vp", "ks", "vs"), "spec": ("q", "k", "v"), "dsa": ("q", "kv", "iq", "ik"),
-           "decode": ("q", "k", "v"), "prefix_paged": ("q", "k_pages", "v_pages"), "dsa_project": ()}[opname]
+           "decode": ("q", "k", "v"), "prefix_paged": ("q", "k_pages", "v_pages"), "dsa_project": (),
+           "decode_paged": ("q", "k_pages", "v_pages")}[opname]
     g = torch.Generator(device="cuda")
     g.manual_seed(1234)
     if opname == "dsa_project":                            # fresh weights (N(0, 1/fan_in)) and hidden states
@@ -238,6 +247,12 @@ def cpu_baseline(opname, shape, dist, inp_host, total_bytes, runs=3):
         work = lambda: oracle.decode.ref64(inp_host["q"][:1], inp_host["k"][:1], inp_host["v"][:1],
                                            sl(inp_host.get("lens"), 1))
         scale, sample = B, f"request 0 of {B}, time scaled x{B}"
+    elif opname == "decode_paged":
+        B = shape["B"]
+        sub = dict(inp_host, q=inp_host["q"][:1], page_table=inp_host["page_table"][:1],
+                   lens=sl(inp_host.get("lens"), 1))
+        work, scale = (lambda: oracle.decode_paged.ref64(**sub)), B
+        sample = f"request 0 of {B}, time scaled x{B}"
     else:
         B = shape["B"]
         work = lambda: oracle.dsa.ref64(inp_host["q"][:1], inp_host["kv"][:1], inp_host["iq"][:1],
@@ -528,7 +543,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2,P2n,C2b,DP")
+    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2,P2n,D1p,D2n,C2b,DP")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle timings")
     ap.add_argument("--ab-rounds", type=int, default=10,
                     help="shuffled rounds of the A/B comparison with the torch standard ops (0: skip it)")

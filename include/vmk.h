@@ -74,6 +74,33 @@ size_t vmk_decode_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, 
 int vmk_decode(const void* q, const void* k, const void* v, const void* lens, void* out, int64_t B, int64_t Hq,
                int64_t Hkv, int64_t D, int64_t L, void* workspace, size_t ws_bytes, void* stream);
 
+/* Paged single-token decode: vmk_decode over a page pool, as serving engines keep their caches.  No reference kernel
+ * covers it (the reference's paged variant is the shared-prefix one it leaves out, README.md:141-142); it joins this
+ * decode op with the page pools of vmk_prefix_decode_paged.
+ *   k_pages, v_pages  (num_pages, Hkv, page_size, D)  (HND; _nhd: (num_pages, page_size, Hkv, D))  page pool
+ *   page_table        (B, max_pages)  int32   each request's pages, in order; ids outside [0, num_pages) are absent
+ *                                             pages, left out of the softmax (no memory is read for them)
+ *   lens              (B,)            int32   positions in use (clamped to [1, page_size * max_pages]), or NULL
+ * page_size a multiple of 32, Hq / Hkv <= 16.  With every page of the rows in use present, the output is bit-equal to
+ * vmk_decode on the gathered cache (L = page_size * max_pages).  _bf16: bf16 q, pages and output. */
+size_t vmk_decode_paged_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
+                                       int64_t max_pages);
+int vmk_decode_paged(const void* q, const void* k_pages, const void* v_pages, const void* page_table,
+                     const void* lens, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t num_pages,
+                     int64_t page_size, int64_t max_pages, void* workspace, size_t ws_bytes, void* stream);
+int vmk_decode_paged_bf16(const void* q, const void* k_pages, const void* v_pages, const void* page_table,
+                          const void* lens, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                          int64_t num_pages, int64_t page_size, int64_t max_pages, void* workspace, size_t ws_bytes,
+                          void* stream);
+int vmk_decode_paged_nhd(const void* q, const void* k_pages, const void* v_pages, const void* page_table,
+                         const void* lens, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                         int64_t num_pages, int64_t page_size, int64_t max_pages, void* workspace, size_t ws_bytes,
+                         void* stream);
+int vmk_decode_paged_nhd_bf16(const void* q, const void* k_pages, const void* v_pages, const void* page_table,
+                              const void* lens, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                              int64_t num_pages, int64_t page_size, int64_t max_pages, void* workspace,
+                              size_t ws_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------------------------- shared-prefix decode
  * Replaces kernel(q, kp, vp, ks, vs) of kernels/prefix_opus55_v8.py:282-355 (op contract ops/prefix.py:1-4, 57-70).
  *   q       (N, Hq, D)        fp16   one decode token per request

@@ -88,6 +88,18 @@ def test_entry_points_reject_before_launch(lib):
     rc = lib.vmk_prefix_decode_paged_nhd(fake, fake, fake, fake, fake, None, fake, 4, 8192, 8192, 128, 100, 64, 128,
                                          2, fake, 1 << 30, None)
     assert rc == 1 and b"at most 4096 KV heads" in lib.vmk_last_error()
+    # Paged decode: page size, heads per KV head and the workspace are checked before any launch.
+    assert lib.vmk_decode_paged_workspace_size(4, 32, 8, 128, 48, 10) == 0
+    assert lib.vmk_decode_paged_workspace_size(4, 32, 8, 128, 64, 10) > 0
+    rc = lib.vmk_decode_paged(fake, fake, fake, fake, None, fake, 4, 32, 8, 128, 100, 48, 10, fake, 1 << 30, None)
+    assert rc == 1 and b"page_size" in lib.vmk_last_error()
+    rc = lib.vmk_decode_paged_nhd(fake, fake, fake, fake, None, fake, 4, 64, 2, 128, 100, 64, 10, fake, 1 << 30, None)
+    assert rc == 1 and b"at most 16 query heads" in lib.vmk_last_error()
+    rc = lib.vmk_decode_paged_bf16(fake, fake, fake, None, None, fake, 4, 32, 8, 128, 100, 64, 10, fake, 1 << 30,
+                                   None)
+    assert rc == 1 and b"null pointer" in lib.vmk_last_error()
+    rc = lib.vmk_decode_paged(fake, fake, fake, fake, None, fake, 4, 32, 8, 128, 100, 64, 10, fake, 64, None)
+    assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
     rc = lib.vmk_dsa_decode(fake, fake, fake, fake, fake, None, fake, fake, fake, 2, 5000, fake, 1024, None)
     assert rc == 1 and b"workspace too small" in lib.vmk_last_error()
     rc = lib.vmk_dsa_decode(fake, fake, fake, fake, None, None, fake, fake, fake, 2, 5000, fake, 1 << 30, None)
@@ -124,6 +136,14 @@ def test_python_wrappers_validate_shapes_without_gpu():
         vmk.prefix_decode_paged(qp, nhd, nhd, pp, sp, layout="NHD")
     with pytest.raises(ValueError, match="expected"):
         vmk.prefix_decode_paged(qp, nhd, nhd[:, :32].contiguous(), pp, sp, layout="NHD")
+    # Paged decode: the same layout rules.
+    qd, table = torch.zeros(2, 32, 128, dtype=torch.float16), torch.zeros(2, 3, dtype=torch.int32)
+    with pytest.raises(ValueError, match="layout"):
+        vmk.decode_paged(qd, pool, pool, table, layout="nhd")
+    with pytest.raises(ValueError, match="B rows"):
+        vmk.decode_paged(qd, pool, pool, table[:1].contiguous())
+    with pytest.raises(ValueError, match="ROCm device"):
+        vmk.decode_paged(qd, nhd, nhd, table, layout="NHD")
 
 
 def test_bf16_reaches_the_bf16_entry_points():

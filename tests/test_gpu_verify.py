@@ -31,7 +31,8 @@ def counts(rep, layer):
 @pytest.mark.timeout(1500)
 @pytest.mark.parametrize("name,configs", [("spec_mi355x.py", {"C3", "C4"}), ("prefix_mi355x.py", {"C1", "C2", "C2b"}),
                                           ("dsa_mi355x.py", {"C5"}), ("decode_mi355x.py", {"D1", "D2", "D3"}),
-                                          ("prefix_paged_mi355x.py", {"P2", "P2n"})])
+                                          ("prefix_paged_mi355x.py", {"P2", "P2n"}),
+                                          ("decode_paged_mi355x.py", {"D1p", "D2n"})])
 def test_kernel_module_is_correct(name, configs, tmp_path):
     rc, rep = run_verify(os.path.join(KDIR, name), tmp_path)
     assert rep["verdict"] == "CORRECT" and rc == 0

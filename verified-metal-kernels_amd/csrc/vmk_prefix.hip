@@ -66,63 +66,10 @@ struct RangeSrc {
   }
 };
 
-// Keys [kbeg, kend) of one KV head of a sequence in a paged cache: pages of ps rows (ps a multiple of 32, so a tile
-// never straddles two pages) laid out (num_pages, Hkv, ps, 128) (HND: a page's rows of one head are contiguous) or,
-// with kNHD, (num_pages, ps, Hkv, 128) (a page's rows are Hkv * 256 bytes apart), the sequence's pages listed in
-// `table`.  Lane t holds the K and V row addresses of the range's tile t (keys kbeg + 32 t ..; kbeg is a multiple of
-// 32 and a range has at most 2048 keys, i.e. 64 tiles), worked out once per lane, so a tile finds its rows with
-// readlanes only (no division or multiply per tile).  An id outside [0, num_pages) is an absent page: its tiles read
-// a zero tile (contiguous rows in either layout) and its keys are masked out.
-template <bool kNHD>
-struct PagedSrc {
-  const f16* kt;           // this lane's tile: K rows, or g_zero_tile when its page is absent
-  const f16* vt;           //                   V rows
-  int here;                // 1 when this lane's tile has a page
-  int kbeg, kend;
-  float scale;
-  uint32_t rb_page;        // NHD: bytes between the rows of a page (Hkv * 256)
-  static constexpr bool kStrided = kNHD;
-  __device__ int tile(int key0) const { return (key0 - kbeg) >> 5; }
-  __device__ uint32_t row_bytes(int key0) const { return present(key0) ? rb_page : 256u; }
-  __device__ static const f16* lane_ptr(const f16* p, int t) {
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, t), hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), t);
-    return reinterpret_cast<const f16*>(((uint64_t)hi << 32) | lo);
-  }
-  __device__ bool present(int key0) const { return __builtin_amdgcn_readlane(here, tile(key0)) != 0; }
-  __device__ const f16* ktile(int key0) const { return lane_ptr(kt, tile(key0)); }
-  __device__ const f16* vtile(int key0) const { return lane_ptr(vt, tile(key0)); }
-  __device__ void mask(floatx16& s, int key0, int g) const {
-    const bool here = present(key0);
-    if (here && key0 + kTile <= kend) return;              // whole tile inside (same for the whole wave)
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int key = key0 + 8 * blk + 4 * g + c;
-        s[4 * blk + c] = here && key < kend ? s[4 * blk + c] : kNegInf;
-      }
-  }
-};
-
 template <bool kNHD>
 __device__ __forceinline__ PagedSrc<kNHD> paged_src(const PrefixArgs& a, const int* table, int ntable, int h,
                                                     int kbeg, int kend) {
-  PagedSrc<kNHD> s;
-  s.kbeg = kbeg;
-  s.kend = kend;
-  s.scale = a.sl2;
-  s.rb_page = (uint32_t)a.Hkv * 256u;
-  const int key = kbeg + kTile * (int)(threadIdx.x & 63);     // this lane's tile
-  const int slot = key / a.ps;
-  const int page = key < kend && slot < ntable ? table[slot] : -1;
-  s.here = (unsigned)page < (unsigned)a.num_pages;
-  const size_t row = key - slot * a.ps;                      // the tile's first row within its page
-  const size_t off =
-      (kNHD ? ((size_t)page * a.ps + row) * a.Hkv + h : ((size_t)page * a.Hkv + h) * a.ps + row) * 128;
-  s.kt = s.here ? a.kp + off : g_zero_tile;
-  s.vt = s.here ? a.vp + off : g_zero_tile;
-  return s;
+  return paged_src<kNHD>(a.kp, a.vp, a.ps, a.Hkv, a.num_pages, a.sl2, table, ntable, h, kbeg, kend);
 }
 
 // Suffix length of request n, clamped to [0, S] so that a bad length can never read past its own rows.

@@ -22,6 +22,9 @@ struct SpecArgs {
   int B, kd, Hq, Hkv, G, L, W;
   int WR, WK, nrb, nsplit, chunk;
   float sl2;               // softmax scale * log2(e)
+  // Paged decode: k, v are the page pools (num_pages pages of ps rows, HND or NHD), pages the (B, max_pages) table.
+  const int* pages;
+  int ps, max_pages, num_pages;
 };
 
 // Keys of one (batch, KV head) for one split: rows of k/v, and the draft mask of this lane's row on the last kd
@@ -117,6 +120,29 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
     attend_wg<1, 4, 2, V>(smem, src, qrow, R - row0, kbeg, ntiles, po, pml);
   else
     attend_wg<2, 2, 2, V>(smem, src, qrow, R - row0, kbeg, ntiles, po, pml);
+}
+
+// Paged single-token decode: the key-split kernel with request b's keys [0, lens[b]) read through its page table
+// (paged_src; a split holds at most 2048 keys, the decode split size up to 16 query heads per KV head).  Absent
+// pages are left out of the softmax.  With every page present the partials are those of spec_partial_kernel on the
+// gathered cache, so the output is bit-equal to vmk_decode's.
+template <bool kNHD, class V>
+__global__ __launch_bounds__(256) void decode_paged_kernel(SpecArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kAttnSmemBytes];
+  const int item = blockIdx.x;
+  const int split = item % a.nsplit;
+  const int grp = item / a.nsplit;                         // one row block: G <= 16 rows
+  const int b = grp / a.Hkv, h = grp % a.Hkv;
+  const int Lb = batch_len(a, b);
+  const int kbeg = split * a.chunk;
+  const int kend = min(Lb, kbeg + a.chunk);
+  const int ntiles = max(0, (kend - kbeg + kTile - 1) / kTile);
+  const PagedSrc<kNHD> src = paged_src<kNHD>(a.k, a.v, a.ps, a.Hkv, a.num_pages, a.sl2,
+                                             a.pages + (size_t)b * a.max_pages, a.max_pages, h, kbeg, kend);
+  auto qrow = [&](int r) { return a.q + ((size_t)b * a.Hq + h * a.G + r) * 128; };
+  float* po = a.part_o + (size_t)item * 32 * 128;
+  float* pml = a.part_ml + (size_t)item * 32 * 2;
+  attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, po, pml);
 }
 
 // Row-split variant for kd*G > 64 rows: NW waves own 32 rows each and share one LDS ring, so every K/V tile of the
@@ -324,6 +350,72 @@ extern "C" int vmk_decode_bf16(const void* q, const void* k, const void* v, cons
                                void* stream) {
   return decode<bf16x8>(q, k, v, lens, out, B, Hq, Hkv, D, L, workspace, ws_bytes, stream);
 }
+
+// Paged single-token decode (HND or NHD page pools).
+extern "C" size_t vmk_decode_paged_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t page_size,
+                                                  int64_t max_pages) {
+  if (page_size < 32 || page_size % 32 || page_size > (1 << 20) || max_pages < 1 || max_pages > (1 << 20)) return 0;
+  return vmk_decode_workspace_size(B, Hq, Hkv, D, page_size * max_pages);
+}
+
+template <bool kNHD, class V>
+static int decode_paged(const void* q, const void* k_pages, const void* v_pages, const void* page_table,
+                        const void* lens, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t num_pages,
+                        int64_t page_size, int64_t max_pages, void* workspace, size_t ws_bytes, void* stream) {
+  VMK_CHECK(q && k_pages && v_pages && page_table && out, "null pointer argument");
+  VMK_CHECK(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "bad head/batch sizes");
+  VMK_CHECK(D == 128, "only head_dim 128 is supported");
+  VMK_CHECK(Hq / Hkv <= 16, "at most 16 query heads per KV head");
+  VMK_CHECK(!kNHD || Hkv <= 4096, "NHD pages: at most 4096 KV heads");
+  VMK_CHECK(page_size >= 32 && page_size % 32 == 0 && page_size <= (1 << 20), "page_size must be a multiple of 32");
+  VMK_CHECK(max_pages >= 1 && page_size * max_pages < (1 << 30) && B * max_pages < ((int64_t)1 << 31),
+            "max_pages out of range");
+  VMK_CHECK(num_pages > 0 && num_pages < (1 << 30) && num_pages * Hkv * page_size <= ((int64_t)1 << 34),
+            "num_pages out of range");
+  VMK_CHECK(B * Hkv * page_size * max_pages <= (int64_t)1 << 40, "sizes out of range");
+  VMK_CHECK(aligned16(q) && aligned16(k_pages) && aligned16(v_pages) && aligned16(out),
+            "tensors must be 16-byte aligned");
+  const int64_t L = page_size * max_pages;
+  const size_t need = vmk_decode_paged_workspace_size(B, Hq, Hkv, D, page_size, max_pages);
+  VMK_CHECK(workspace && ws_bytes >= need, "workspace too small (query vmk_decode_paged_workspace_size)");
+  SpecPlan p = spec_plan(B, 1, Hq, Hkv, L);
+  VMK_CHECK(!p.rows_mode && p.WR == 1 && p.WK == 4 && p.nrb == 1 && p.chunk <= 2048, "unsupported decode plan");
+  SpecArgs a;
+  a.q = (const f16*)q; a.k = (const f16*)k_pages; a.v = (const f16*)v_pages; a.bits = nullptr;
+  a.lens = (const int*)lens;
+  a.out = (f16*)out;
+  a.B = (int)B; a.kd = 1; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = 1;
+  a.pages = (const int*)page_table;
+  a.ps = (int)page_size; a.max_pages = (int)max_pages; a.num_pages = (int)num_pages;
+  a.part_o = (float*)align_up((char*)workspace + kWsHead, 256);
+  a.part_ml = a.part_o + p.po_floats;
+  a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;
+  a.sl2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  prof_before(kKSpecPartial, s);
+  hipLaunchKernelGGL((decode_paged_kernel<kNHD, V>), dim3((unsigned)(B * Hkv * p.nsplit)), dim3(256), 0, s, a);
+  prof_after(kKSpecPartial, s);
+  VMK_CHECK_HIP(hipGetLastError());
+  prof_before(kKSpecCombine, s);
+  hipLaunchKernelGGL(spec_combine_kernel<elem_t<V>>, dim3((unsigned)(B * Hq)), dim3(128), 0, s, a);
+  prof_after(kKSpecCombine, s);
+  VMK_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
+#define VMK_DECODE_PAGED_ENTRY(name, nhd, V)                                                                      \
+  extern "C" int name(const void* q, const void* k_pages, const void* v_pages, const void* page_table,           \
+                      const void* lens, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,               \
+                      int64_t num_pages, int64_t page_size, int64_t max_pages, void* workspace, size_t ws_bytes,  \
+                      void* stream) {                                                                            \
+    return decode_paged<nhd, V>(q, k_pages, v_pages, page_table, lens, out, B, Hq, Hkv, D, num_pages, page_size, \
+                                max_pages, workspace, ws_bytes, stream);                                          \
+  }
+VMK_DECODE_PAGED_ENTRY(vmk_decode_paged, false, half8)
+VMK_DECODE_PAGED_ENTRY(vmk_decode_paged_bf16, false, bf16x8)
+VMK_DECODE_PAGED_ENTRY(vmk_decode_paged_nhd, true, half8)
+VMK_DECODE_PAGED_ENTRY(vmk_decode_paged_nhd_bf16, true, bf16x8)
+#undef VMK_DECODE_PAGED_ENTRY
 
 // ---------------------------------------------------------------------------------------------- allocation-free
 // vmk_spec_verify without a workspace argument, for callers that cannot allocate device memory.  The partials go to

@@ -195,6 +195,49 @@ def decode(q, k, v, lens=None, out=None):
     return out
 
 
+def decode_paged(q, k_pages, v_pages, page_table, lens=None, out=None, layout="HND"):
+    """Single-token decode over a page pool: q (B, Hq, 128); k_pages/v_pages (num_pages, Hkv, page_size, 128) for
+    layout "HND" or (num_pages, page_size, Hkv, 128) for "NHD", page_size a multiple of 32, all fp16 or all bf16;
+    page_table (B, max_pages) int32; lens (B,) int32 or None (all max_pages * page_size).  Page ids outside
+    [0, num_pages) are absent pages (left out).  Returns out (B, Hq, 128) of q's dtype."""
+    if layout not in ("HND", "NHD"):
+        raise ValueError(f"layout {layout!r}: expected 'HND' or 'NHD'")
+    dt, sfx = _elem(q)
+    _need(q, "q", dt, 3)
+    for t, n in ((k_pages, "k_pages"), (v_pages, "v_pages")):
+        _need(t, n, dt, 4)
+    _need(page_table, "page_table", torch.int32, 2)
+    B, Hq, D = q.shape
+    if layout == "HND":
+        num_pages, Hkv, ps = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
+        want = (num_pages, Hkv, ps, D)
+    else:
+        num_pages, ps, Hkv = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
+        want = (num_pages, ps, Hkv, D)
+    if tuple(k_pages.shape) != want or tuple(v_pages.shape) != tuple(k_pages.shape):
+        raise ValueError(f"k_pages {tuple(k_pages.shape)} / v_pages {tuple(v_pages.shape)}: expected {want} ({layout})")
+    if page_table.shape[0] != B:
+        raise ValueError("page_table must have B rows")
+    if lens is not None:
+        _need(lens, "lens", torch.int32, 1)
+        if lens.shape[0] != B:
+            raise ValueError("lens must have B entries")
+    mp = page_table.shape[1]
+    _resident(q=q, k_pages=k_pages, v_pages=v_pages, page_table=page_table, lens=lens, out=out)
+    if out is None:
+        out = torch.empty_like(q)
+    ws_n = lib.load().vmk_decode_paged_workspace_size(B, Hq, Hkv, D, ps, mp)
+    if ws_n == 0:
+        raise lib.VmkError(f"unsupported paged decode shape B={B} Hq={Hq} Hkv={Hkv} D={D} page_size={ps} "
+                           f"max_pages={mp}")
+    ws = workspace(ws_n, q.device)
+    entry = "vmk_decode_paged" + ("_nhd" if layout == "NHD" else "") + sfx
+    _launch(entry, ws, q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), page_table.data_ptr(),
+            0 if lens is None else lens.data_ptr(), out.data_ptr(), B, Hq, Hkv, D, num_pages, ps, mp,
+            ws.data_ptr(), ws.numel(), _stream(q))
+    return out
+
+
 def prefix_decode(q, kp, vp, ks, vs, slens=None, out=None):
     """q (N, Hq, 128), kp/vp (Hkv, P, 128), ks/vs (N, Hkv, S, 128), all fp16 or all bf16; slens (N,) int32 or
     None.  Returns out (N, Hq, 128) of q's dtype."""

@@ -37,6 +37,11 @@ _SIGS = {
     "vmk_prefix_decode_paged_bf16": [_c_vp] * 7 + [_c_i64] * 8 + [_c_vp, _c_sz, _c_vp],
     "vmk_prefix_decode_paged_nhd": [_c_vp] * 7 + [_c_i64] * 8 + [_c_vp, _c_sz, _c_vp],
     "vmk_prefix_decode_paged_nhd_bf16": [_c_vp] * 7 + [_c_i64] * 8 + [_c_vp, _c_sz, _c_vp],
+    "vmk_decode_paged_workspace_size": [_c_i64] * 6,
+    "vmk_decode_paged": [_c_vp] * 6 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
+    "vmk_decode_paged_bf16": [_c_vp] * 6 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
+    "vmk_decode_paged_nhd": [_c_vp] * 6 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
+    "vmk_decode_paged_nhd_bf16": [_c_vp] * 6 + [_c_i64] * 7 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_indexer_select_bf16": [_c_vp] * 6 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_sparse_mla_bf16": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_decode_bf16": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
@@ -54,6 +59,7 @@ _SIGS = {
 }
 _RET = {"vmk_last_error": ctypes.c_char_p, "vmk_spec_workspace_size": _c_sz, "vmk_spec_noalloc_max_bytes": _c_sz, "vmk_prefix_workspace_size": _c_sz,
         "vmk_prefix_paged_workspace_size": _c_sz,
+        "vmk_decode_paged_workspace_size": _c_sz,
         "vmk_dsa_workspace_size": _c_sz, "vmk_decode_workspace_size": _c_sz, "vmk_dsa_project_workspace_size": _c_sz}
 
 # struct vmk_dsa_project_weights of include/vmk.h: device pointers of the projection weights, in its field order.
