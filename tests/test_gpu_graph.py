@@ -4,12 +4,13 @@ synchronisation between the replays; every replay must reproduce the eager outpu
 import pytest
 import torch
 
-from vmk.ops import KEYS, decode, dsa, prefix, prefix_paged, spec
+from vmk.ops import KEYS, decode, decode_paged, dsa, prefix, prefix_paged, spec
 
 pytestmark = pytest.mark.gpu
 
 CASES = [("spec", spec, dict(B=3, L=5000, k=8), "chain"), ("spec", spec, dict(B=2, L=8192, k=64), "tree_bd"),
          ("decode", decode, dict(B=4, L=9000, L_min=1), "randn"),
+         ("decode_paged", decode_paged, dict(B=4, L=9000, L_min=1, ps=64, absent=1, layout="NHD"), "randn"),
          ("prefix", prefix, dict(N=8, P=2048, S=256, S_min=1), "randn"),               # mixed launch + merge
          ("prefix", prefix, dict(N=64, P=4096, S=1024, S_min=128), "outlier"),        # prefix launch, fused suffix
          ("prefix", prefix, dict(N=20, P=3000, S=2500, S_min=1), "randn"),            # combine launch
