@@ -113,7 +113,7 @@ def traffic(fetch_db, write_db, copy_bytes):
     for name in sorted(f):
         if name not in w or "FETCH_SIZE" not in f[name] or ck == name:
             continue
-        if not any(s in name for s in ("prefix", "spec", "dsa", "proj_")):
+        if not any(s in name for s in ("prefix", "spec", "dsa", "proj_", "decode")):
             continue
         fv, wv = f[name]["FETCH_SIZE"], w[name]["WRITE_SIZE"]
         rd = sum(fv) / len(fv) * 1024.0 / kf
