@@ -14,6 +14,7 @@ CASES = [(dict(B=1, L=1), "randn", 1), (dict(B=1, L=31), "randn", 2), (dict(B=3,
          (dict(B=5, L=300), "large", 7), (dict(B=2, L=3000), "needle", 8), (dict(B=2, L=3000), "nan_inf", 9),
          (dict(B=2, L=3000), "tiny", 10), (dict(B=4, L=1000, Hq=8, Hkv=8), "randn", 11),
          (dict(B=2, L=2048, Hq=64, Hkv=2), "randn", 12), (dict(B=6, L=5000, L_min=1), "randn", 13),
+         (dict(B=3, L=3000, L_min=1, Hq=24, Hkv=8), "randn", 21), (dict(B=2, L=4000, Hq=20, Hkv=4), "needle", 22),
          (dict(B=8, L=2048, L_min=1), "needle", 14), (dict(B=3, L=40000, L_min=30000), "randn", 15),
          (dict(B=4, L=16384), "randn", 16)]
 

@@ -17,6 +17,11 @@ CASES = [(dict(B=1, L=8, k=8), "randn", 7), (dict(B=1, L=9, k=1), "randn", 8), (
          (dict(B=8, L=2049, k=4), "randn", 19), (dict(B=1, L=31, k=31), "needle_masked", 20),
          (dict(B=2, L=4096, k=64), "tree_bd", 0), (dict(B=1, L=70, k=64), "needle_masked", 1),
          (dict(B=1, L=5000, k=33), "randn", 2), (dict(B=2, L=3000, k=64), "chain", 3),
+         # other head counts: G = 8 (64 rows, two row blocks of two waves), G = 1, G = 5 (15 rows), G = 3 in the
+         # row split (120 rows, drafts straddling the 32-row blocks) and G = 16 (256 rows)
+         (dict(B=2, L=3000, k=8, Hq=16, Hkv=2), "randn", 21), (dict(B=2, L=2500, k=4, Hq=8, Hkv=8), "randn", 22),
+         (dict(B=2, L=2000, k=3, Hq=40, Hkv=8), "chain", 24), (dict(B=1, L=4100, k=40, Hq=24, Hkv=8), "randn", 25),
+         (dict(B=1, L=3000, k=16, Hq=64, Hkv=4), "chain", 23),
          # the benchmark configurations at full size (seed 0, as bench.py draws them): C3 is the key-split walk with
          # 8 splits per row group, C4 the row-split walk with 16 splits merged by the combine launch
          (dict(B=4, L=32768, k=8), "chain", 0), (dict(B=2, L=65536, k=64), "tree_bd", 0)]
