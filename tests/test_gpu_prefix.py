@@ -44,6 +44,14 @@ ROWS_CASES = [
     (dict(N=40, P=65536, S=100, S_min=1), "randn", 116),                   # 64 prefix chunks: the general merge
 ]
 
+# Other head counts, in the row-block path and the mixed launch.
+HEADS_CASES = [
+    (dict(N=10, P=3000, S=400, S_min=1, Hq=32, Hkv=1), "randn", 117),      # G = 32: two row blocks of 256 rows
+    (dict(N=20, P=2500, S=300, Hq=32, Hkv=16), "randn", 118),              # G = 2, 40 rows (mixed launch)
+    (dict(N=9, P=2048, S=300, S_min=1, Hq=8, Hkv=8), "randn", 119),        # G = 1, 9 rows
+    (dict(N=3, P=4096, S=200, S_min=1, Hq=64, Hkv=4), "randn", 126),       # G = 16, 48 rows
+]
+
 
 # At most 32 rows per KV head and more mixed-launch items than CUs: the prefix runs as single-wave units, 2 or 4 per
 # workgroup (the mixed launch's row blocks give the same bits; see the invariance test below).
@@ -70,6 +78,12 @@ def _head_is_zero():
 
 @pytest.mark.parametrize("shape,dist,seed", ROWS_CASES)
 def test_prefix_rows_parity(shape, dist, seed):
+    test_prefix_parity(shape, dist, seed)
+    assert _head_is_zero(), "the workspace head must be zero after every call"
+
+
+@pytest.mark.parametrize("shape,dist,seed", HEADS_CASES)
+def test_prefix_head_counts_parity(shape, dist, seed):
     test_prefix_parity(shape, dist, seed)
     assert _head_is_zero(), "the workspace head must be zero after every call"
 
