@@ -144,6 +144,20 @@ def test_python_wrappers_validate_shapes_without_gpu():
         vmk.decode_paged(qd, pool, pool, table[:1].contiguous())
     with pytest.raises(ValueError, match="ROCm device"):
         vmk.decode_paged(qd, nhd, nhd, table, layout="NHD")
+    # A caller's out must have q's shape and dtype: the kernels write exactly that many rows.
+    short, wrong = torch.zeros(1, 32, 128, dtype=torch.float16), torch.zeros(2, 32, 128, dtype=torch.bfloat16)
+    kv = torch.zeros(2, 8, 100, 128, dtype=torch.float16)
+    for bad, err in ((short, ValueError), (wrong, TypeError)):
+        with pytest.raises(err, match="out"):
+            vmk.decode(qd, kv, kv, out=bad)
+        with pytest.raises(err, match="out"):
+            vmk.decode_paged(qd, pool, pool, table, out=bad)
+        with pytest.raises(err, match="out"):
+            vmk.prefix_decode_paged(qp, pool, pool, pp, sp, out=bad)
+        with pytest.raises(err, match="out"):
+            vmk.prefix_decode(qp, kv[0], kv[0], kv, kv, out=bad)
+    with pytest.raises(ValueError, match="out"):
+        vmk.spec_verify(q, kv, kv, torch.zeros(2, 8, 1, dtype=torch.int32), out=q[:1].contiguous())
 
 
 def test_bf16_reaches_the_bf16_entry_points():

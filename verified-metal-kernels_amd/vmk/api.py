@@ -92,6 +92,15 @@ def _need(t, name, dtype, ndim):
         raise ValueError(f"{name} must be contiguous")
 
 
+def _need_out(out, like):
+    """A caller's output tensor must have the dtype and shape of `like` (the kernels write exactly that many rows)."""
+    if out is None:
+        return
+    _need(out, "out", like.dtype, like.dim())
+    if tuple(out.shape) != tuple(like.shape):
+        raise ValueError(f"out {tuple(out.shape)}: expected {tuple(like.shape)}")
+
+
 def _resident(**tensors):
     """Every given tensor (None skipped) is on the same ROCm device; then that device is checked once."""
     dev = None
@@ -133,6 +142,7 @@ def spec_verify(q, k, v, words, out=None):
         raise ValueError(f"k/v shape {tuple(k.shape)}/{tuple(v.shape)} do not match q {tuple(q.shape)}")
     if tuple(words.shape) != (B, kd, (kd + 31) // 32):
         raise ValueError(f"bits shape {tuple(words.shape)} is not (B, kd, ceil(kd/32)) = {(B, kd, (kd + 31) // 32)}")
+    _need_out(out, q)
     _resident(q=q, k=k, v=v, bits=words, out=out)
     if out is None:
         out = torch.empty_like(q)
@@ -183,6 +193,7 @@ def decode(q, k, v, lens=None, out=None):
         _need(lens, "lens", torch.int32, 1)
         if lens.shape[0] != B:
             raise ValueError("lens must have B entries")
+    _need_out(out, q)
     _resident(q=q, k=k, v=v, lens=lens, out=out)
     if out is None:
         out = torch.empty_like(q)
@@ -223,6 +234,7 @@ def decode_paged(q, k_pages, v_pages, page_table, lens=None, out=None, layout="H
         if lens.shape[0] != B:
             raise ValueError("lens must have B entries")
     mp = page_table.shape[1]
+    _need_out(out, q)
     _resident(q=q, k_pages=k_pages, v_pages=v_pages, page_table=page_table, lens=lens, out=out)
     if out is None:
         out = torch.empty_like(q)
@@ -258,6 +270,7 @@ def prefix_decode(q, kp, vp, ks, vs, slens=None, out=None):
         _need(slens, "slens", torch.int32, 1)
         if slens.shape[0] != N:
             raise ValueError("slens must have N entries")
+    _need_out(out, q)
     _resident(q=q, kp=kp, vp=vp, ks=ks, vs=vs, slens=slens, out=out)
     if out is None:
         out = torch.empty_like(q)
@@ -301,6 +314,7 @@ def prefix_decode_paged(q, k_pages, v_pages, prefix_pages, suffix_pages, slens=N
         if slens.shape[0] != N:
             raise ValueError("slens must have N entries")
     P, max_sp = prefix_pages.shape[0] * ps, suffix_pages.shape[1]
+    _need_out(out, q)
     _resident(q=q, k_pages=k_pages, v_pages=v_pages, prefix_pages=prefix_pages, suffix_pages=suffix_pages,
               slens=slens, out=out)
     if out is None:
