@@ -31,6 +31,35 @@ def test_header_declares_the_binding_table():
     assert declared() == sorted(L.exported_symbols())
 
 
+def prototypes():
+    """name -> (return type, [parameter types]) of every function include/vmk.h declares."""
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    src = re.sub(r"//[^\n]*", "", src)
+    out = {}
+    for ret, name, args in re.findall(r"([A-Za-z_][\w\s\*]*?)\b(vmk_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", src):
+        params = [a.strip() for a in args.split(",")]
+        params = [] if params == ["void"] else [re.sub(r"\s*\b\w+$", "", a) if not a.endswith("*") else a
+                                                 for a in params]
+        out[name] = (" ".join(ret.split()), params)
+    return out
+
+
+def test_binding_table_matches_the_header_prototypes():
+    """Every ctypes signature in vmk/lib.py has the header's parameter count and types, and its return type, so a
+    change on one side of the ABI cannot go unnoticed."""
+    import ctypes as C
+    from vmk import lib as L
+    ctype = {"int64_t": C.c_int64, "size_t": C.c_size_t, "int": C.c_int, "float": C.c_float, "uint32_t": C.c_uint32}
+    protos = prototypes()
+    assert sorted(protos) == sorted(L.exported_symbols())
+    for name, (ret, params) in protos.items():
+        want = [C.c_void_p if "*" in t else ctype[t.replace("const ", "").strip()] for t in params]
+        assert L._SIGS[name] == want, (name, params)
+        want_ret = {"int": C.c_int, "size_t": C.c_size_t, "const char*": C.c_char_p}[ret]
+        assert L._RET.get(name, C.c_int) == want_ret, (name, ret)
+
+
 def test_library_exports_every_declared_symbol(lib):
     out = subprocess.run(["nm", "-D", "--defined-only", lib._name], capture_output=True, text=True).stdout
     exported = set(re.findall(r"\bT (vmk_[a-z0-9_]+)\b", out))
