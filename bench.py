@@ -1,12 +1,18 @@
 """Benchmark of the attention ops on one MI355X, in the driver's contract.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs C1,C2,...] [--no-cpu] [--ab-rounds R]
+                    [--results DIR]
 
-Prints human-readable progress on stderr and ONE JSON line on stdout.  A "step" is one call of the op on one batch
-of the headline configuration (BASELINE configs[1] = C2, shared-prefix decode at scale); `value` is its achieved
-HBM throughput (algorithmic bytes / time per call, inputs resident in HBM), `ops` holds the same figures for every
-configuration (C1..C5, and this build's D1-D3 decode, P2/P2n paged prefix in HND/NHD pages, D1p/D2n paged decode
-in HND/NHD pages, C2b bf16, DP the DSA input projections).
+Prints human-readable progress on stderr and ONE short JSON line (a few KB) on stdout.  A "step" is one call of the
+op on one batch of the headline configuration, C4 (tree verification, B=2, k=64, L=65536): BASELINE.json's metric
+names no configuration, so the headline is the largest configuration that fits one GPU (C4, 539 MB and 137 GFLOP
+per call).  `value` is its achieved HBM throughput (algorithmic bytes / time per call, inputs resident in HBM);
+`roofline` is the dominant kernel's HBM fraction, with its MFMA fraction beside it since C4 sits near the ridge;
+`ops` maps every configuration to [us/call, GB/s, % of 8 TB/s] (C1..C5, and this build's D1-D3 decode, P2/P2n
+paged prefix in HND/NHD pages, D1p/D2n paged decode in HND/NHD pages, C2b bf16, DP the DSA input projections);
+`ab` holds the per-op geomean speedups over the torch standard ops.  The full per-configuration rows and every A/B
+sample go to DIR/bench_full.json and DIR/bench_<op>.json (DIR defaults to ./results), as the reference keeps its
+per-shape detail in results/bench_<op>.json.
 Method:
   * the kernel's output on the timed inputs is checked against the PyTorch standard op first
     (allclose atol=rtol=1e-2, bench.py:180-192 of the reference), and the inputs are checked for modification;
@@ -18,11 +24,13 @@ Method:
     launched one by one from Python, which adds the host's per-call overhead;
   * the dominant kernel of each op is bracketed by its own pair of HIP events on its launch stream inside the eager
     loop (libvmk's vmk_profile_next hook), which gives the roofline figure;
-  * A/B against the torch standard ops (the reference's headline form, bench.py:99-126, 157-236): on the
-    reference's BENCH_SHAPES and on this build's configurations, the kernel module and every TORCH_REFS op each
-    time a 16-call chain (each call's query is the previous call's output; DSA: [output | rope part of q]) after
-    a 1 GiB cache flush, in R shuffled rounds; reported: medians with p10/p90, and the median over rounds of
-    t(strongest op) / t(kernel), with its p10/p90, and the geomean over BENCH_SHAPES.
+  * A/B against the torch standard ops (the reference's headline form, bench.py:99-126, 157-236): each kernel
+    module is screened by the verifier's static gate before it is imported (reference bench.py:159-161); on the
+    reference's BENCH_SHAPES and on this build's configurations, the output is checked against the standard op
+    and the inputs for modification (reference bench.py:180-192), then the kernel module and every TORCH_REFS op
+    each time a 16-call chain (each call's query is the previous call's output; DSA: [output | rope part of q])
+    after a 1 GiB cache flush, in R shuffled rounds; reported: medians with p10/p90, and the median over rounds
+    of t(strongest op) / t(kernel), with its p10/p90, and the geomean over BENCH_SHAPES.
 The CPU baseline is the float64 NumPy oracle (oracle/) on the host, on a bounded sample of the same workload, the
 median of 3 runs.
 """
@@ -44,7 +52,7 @@ import numpy as np  # noqa: E402
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16 MFMA
 METRIC = "µs/call per op + achieved HBM GB/s (% of MI355X peak) at bench shapes"
-HEADLINE = "C2"
+HEADLINE = "C4"
 DOMINANT = {"prefix": "prefix_partial", "spec": "spec_partial", "dsa": "dsa_indexer", "decode": "spec_partial",
             "prefix_paged": "prefix_partial", "dsa_project": "dsa_project_q", "decode_paged": "spec_partial"}
 # Inputs the ops write by contract (the projections append the new token's cache rows), left out of the
@@ -285,6 +293,9 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     if opname == "spec":
         inp0["words"] = op.mask_words(inp0["bits"], shape["k"]).contiguous()
     total_bytes, dom_bytes, flops = op_bytes_flops(opname, shape, host)
+    # FLOPs inside the dominant bracket: all of them for the attention ops, the score GEMM for DSA's indexer.
+    dom_flops = {"dsa": lambda: 2 * shape["B"] * shape["L"] * op.HI * op.DI, "dsa_project": lambda: None}.get(
+        opname, lambda: flops)()
     # Output check on the benchmark inputs and input-mutation check (reference bench.py:180-192).
     snap = {k: v.clone() for k, v in inp0.items() if isinstance(v, torch.Tensor) and k not in WRITES.get(opname, ())}
     out = call_op(opname, inp0)
@@ -326,7 +337,9 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
                tflops=round(flops / us / 1e6, 2), mfma_pct=round(100 * flops / us / 1e6 / PEAK_FP16_TFLOPS, 2),
                eager=dict(us_per_call=round(eager_us, 2), gbs=round(total_bytes / eager_us / 1e3, 1)),
                dominant=dict(kernel=DOMINANT[opname], us=round(dom_us, 2), bytes=int(dom_bytes),
-                             gbs=round(dom_gbs, 1), frac=round(dom_gbs / PEAK_HBM_GBS, 4)),
+                             gbs=round(dom_gbs, 1), frac=round(dom_gbs / PEAK_HBM_GBS, 4),
+                             tflops=round(dom_flops / dom_us / 1e6, 2) if dom_flops else None,
+                             sq=measured_mfma(name, DOMINANT[opname])),
                output_check="ok", distinct_input_sets=len(sets))
     if opname not in AB_OPS:                               # no reference A/B for this op: its torch form, graph-timed
         ts = graph_us_per_call(opname, sets, steps, fn=lambda s: std_op(opname, s), check=False)
@@ -455,22 +468,47 @@ def ab_runner(fn, layers, chain, flush):
     return run
 
 
+def screened_module(opname):
+    """The op's kernel module, imported only after its source passes the verifier's static gate (the reference
+    screens a module before importing it, bench.py:159-161); a refused module ends the benchmark."""
+    import importlib
+    tests = os.path.join(ROOT, "tests")
+    if tests not in sys.path:
+        sys.path.insert(0, tests)
+    from verify import screen
+    path = os.path.join(PKG, "kernels", f"{opname}_mi355x.py")
+    with open(path) as f:
+        problems = screen(f.read())
+    if problems:
+        raise SystemExit(f"A/B {opname}: {path} fails the static gate: " + "; ".join(problems))
+    return importlib.import_module(f"{opname}_mi355x")
+
+
 def ab_shape(op, shape, dist, rounds, flush, seed):
-    """One shape: output check, then `rounds` shuffled rounds of the kernel module and every standard op."""
+    """One shape: output and input-mutation check, then `rounds` shuffled rounds of the kernel module and every
+    standard op."""
     import random
     import torch
     from vmk.ops import KEYS
-    mod = __import__(f"{op.NAME}_mi355x")
+    mod = screened_module(op.NAME)
     keys = KEYS[op.NAME]
     kernel = lambda **kw: mod.kernel(**{k: kw.get(k) for k in keys})
     sets = ab_inputs(op, shape, dist, keys)
     n = len(sets)
     layers = [sets[i % n] for i in range(max(16, n))]
     std = getattr(op, op.L1_REF)
-    out, ref = kernel(**sets[0]), std(**sets[0])
+    snap = {k: v.clone() for k, v in sets[0].items() if k in keys and isinstance(v, torch.Tensor)}
+    out = kernel(**sets[0])
+    torch.cuda.synchronize()
+    mutated = [k for k, v in snap.items() if not torch.equal(v.view(torch.uint8), sets[0][k].view(torch.uint8))]
+    del snap
+    if mutated:
+        raise SystemExit(f"A/B {op.NAME} {shape}: the kernel modified its inputs {mutated}")
+    ref = std(**sets[0])
     torch.cuda.synchronize()
     if not torch.allclose(out.float(), ref.float(), atol=1e-2, rtol=1e-2, equal_nan=True):
         raise SystemExit(f"A/B {op.NAME} {shape}: the kernel differs from {op.L1_REF} on the benchmark inputs")
+    del out, ref
     chain = ab_chain(op.NAME)
     runners = {"kernel": ab_runner(kernel, layers, chain, flush)}
     runners.update({name: ab_runner(f, layers, chain, flush) for name, f in op.TORCH_REFS.items()})
@@ -489,13 +527,14 @@ def ab_shape(op, shape, dist, rounds, flush, seed):
     ratios = {k: spread([b / a for a, b in zip(times["kernel"], times[k])]) for k in refs}
     del sets, layers, runners
     torch.cuda.empty_cache()
-    return dict(shape=shape, dist=dist, distinct_sets=n, chain=max(16, n),
+    return dict(shape=shape, dist=dist, distinct_sets=n, chain=max(16, n), input_check="unmodified",
                 median_us={k: round(v["median"], 2) for k, v in med.items()},
                 p10_us={k: round(v["p10"], 2) for k, v in med.items()},
                 p90_us={k: round(v["p90"], 2) for k, v in med.items()},
                 strongest_ref=strongest, speedup_vs_strongest_ref=round(ratios[strongest]["median"], 3),
                 speedup_p10=round(ratios[strongest]["p10"], 3), speedup_p90=round(ratios[strongest]["p90"], 3),
-                speedup_vs_each_ref={k: round(v["median"], 3) for k, v in ratios.items()})
+                speedup_vs_each_ref={k: round(v["median"], 3) for k, v in ratios.items()},
+                samples_us={k: [round(t, 3) for t in v] for k, v in times.items()})
 
 
 def ab_bench(rounds, configs):
@@ -538,6 +577,68 @@ def measured_traffic(name, dom):
     return int(t["read_bytes"] + t["write_bytes"])
 
 
+def measured_mfma(name, kernel):
+    """The dominant kernel's MFMA-busy share from the committed SQ counter summary of this configuration
+    (profiles/<config>_mfma.json: SQ_VALU_MFMA_BUSY_CYCLES over the kernel's active cycles), else None."""
+    path = os.path.join(ROOT, "profiles", f"{name}_mfma.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    if t.get("kernel") != kernel:
+        return None
+    return {k: t[k] for k in ("mfma_busy", "coexec", "valu_per_mfma") if k in t}
+
+
+def write_results(outdir, rows, ab, device):
+    """Every configuration's full row and every A/B sample, to outdir/bench_full.json and one
+    outdir/bench_<op>.json per A/B op (reference bench.py:276-284 keeps its per-shape samples the same way);
+    returns the path of the full file, or None when outdir is empty."""
+    if not outdir:
+        return None
+    os.makedirs(outdir, exist_ok=True)
+    full = os.path.join(outdir, "bench_full.json")
+    with open(full, "w") as f:
+        json.dump(dict(device=device, ops=rows, ab_vs_torch=ab), f, indent=1)
+    for opname, r in (ab or {}).items():
+        with open(os.path.join(outdir, f"bench_{opname}.json"), "w") as f:
+            json.dump(dict(device=device, op=opname, **r), f, indent=1)
+    return full
+
+
+def summary_line(rows, ab, steps, warmup, results=None):
+    """The one stdout line: the headline configuration's figures, its roofline and CPU baseline, and a compact
+    map of every configuration to [us/call, GB/s, % of peak HBM]; a few KB whatever the number of rows."""
+    head_name = HEADLINE if HEADLINE in rows else next(iter(rows))
+    head = rows[head_name]
+    dom = head["dominant"]
+    cpu = head.get("cpu_baseline") or {}
+    roof = dict(bound="hbm", achieved=dom["gbs"], peak=PEAK_HBM_GBS, unit="GB/s", frac=dom["frac"],
+                traffic=dom.get("traffic"), kernel=dom["kernel"], kernel_us=dom["us"],
+                algorithmic_bytes=dom["bytes"])
+    if dom.get("tflops") is not None:
+        roof["mfma"] = dict(achieved=dom["tflops"], peak=PEAK_FP16_TFLOPS, unit="TFLOP/s",
+                            frac=round(dom["tflops"] / PEAK_FP16_TFLOPS, 4), sq=dom.get("sq"))
+    return dict(
+        metric=METRIC, value=head["gbs"], unit="GB/s", n_gpus=1, steps=steps, warmup=warmup,
+        ms_per_step=round(head["us_per_call"] / 1e3, 5), higher_is_better=True, scaling="weak", vs_baseline=None,
+        dtype="fp16 (fp32 accumulate)", data="synthetic (seeded N(0,1) inputs of the BASELINE configuration)",
+        config=dict(workload=f"{head_name}: {head['op']} " + ", ".join(f"{k}={v}" for k, v in head["shape"].items())
+                    + f", dist={head['dist']}",
+                    us_per_call=head["us_per_call"], pct_peak=head["pct_peak"], tflops=head.get("tflops"),
+                    timing=f"median of {head['us_spread']['replays']} replays of a HIP graph of {steps} calls "
+                           f"(p10 {head['us_spread']['p10']}, p90 {head['us_spread']['p90']}); eager loop "
+                           f"{head['eager']['us_per_call']} us/call"),
+        roofline=roof,
+        cpu_baseline=None if not cpu else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample",
+                                                               "us_per_call") if k in cpu},
+        ops={name: [r["us_per_call"], r["gbs"], r["pct_peak"]] for name, r in rows.items()},
+        ops_fields=["us_per_call", "GB/s", "pct_of_8TB/s"],
+        ab=None if ab is None else {op: dict(geomean=r["geomean_bench_shapes"], min=r["min_bench_shapes"],
+                                             max=r["max_bench_shapes"], rounds=r["rounds"]) for op, r in ab.items()},
+        results=None if results is None else os.path.relpath(results, ROOT))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -550,6 +651,8 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="first run a plain streaming kernel that reads BYTES and writes BYTES (torch.bitwise_not "
                          "on int32), the calibration of the PMC traffic counters")
+    ap.add_argument("--results", default=os.path.join(ROOT, "results"), metavar="DIR",
+                    help="where the full rows and A/B samples are written ('' to skip)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py measures one MI355X: the three ops run on a single GPU and this build has no multi-GPU path "
@@ -575,32 +678,9 @@ def main():
             rows[name] = bench_config(name, opname, shape, dist, a.steps, a.warmup,
                                       do_cpu=not a.no_cpu)
     ab = ab_bench(a.ab_rounds, want) if a.ab_rounds > 0 else None
-    if ab:
-        for opname, r in ab.items():
-            for sh in r["shapes"]:
-                if sh["config"] in rows:
-                    rows[sh["config"]]["ab"] = {k: sh[k] for k in ("strongest_ref", "speedup_vs_strongest_ref",
-                                                                    "speedup_p10", "speedup_p90", "median_us")}
-    head = rows.get(HEADLINE) or next(iter(rows.values()))
-    head_name = HEADLINE if HEADLINE in rows else next(iter(rows))
-    dom = head["dominant"]
-    line = dict(
-        metric=METRIC, value=head["gbs"], unit="GB/s", n_gpus=1, steps=a.steps, warmup=a.warmup,
-        ms_per_step=round(head["us_per_call"] / 1e3, 5), higher_is_better=True, scaling="weak", vs_baseline=None,
-        dtype="fp16 (fp32 accumulate)", data="synthetic (seeded N(0,1) inputs of the BASELINE configuration)",
-        config=dict(workload=f"{head_name}: {head['op']} {head['shape']} dist={head['dist']}",
-                    us_per_call=head["us_per_call"], pct_peak=head["pct_peak"],
-                    timing=f"{a.steps} calls replayed from one HIP graph; eager loop {head['eager']['us_per_call']} "
-                           f"us/call"),
-        roofline=dict(bound="hbm", achieved=dom["gbs"], peak=PEAK_HBM_GBS, unit="GB/s", frac=dom["frac"],
-                      kernel=dom["kernel"], kernel_us=dom["us"], traffic=dom.get("traffic")),
-        cpu_baseline={k: v for k, v in head.get("cpu_baseline", {}).items()} or None,
-        ops=rows,
-        ab_vs_torch=None if ab is None else {
-            op: dict(geomean_bench_shapes=r["geomean_bench_shapes"], min=r["min_bench_shapes"],
-                     max=r["max_bench_shapes"], rounds=r["rounds"], shapes=r["shapes"]) for op, r in ab.items()},
-        device=torch.cuda.get_device_name(0),
-    )
+    results = write_results(a.results, rows, ab, device=torch.cuda.get_device_name(0))
+    log(f"full rows and A/B samples: {results}")
+    line = summary_line(rows, ab, a.steps, a.warmup, results)
     print(json.dumps(line), flush=True)
 
 

@@ -213,12 +213,14 @@ int vmk_dsa_sparse_mla(const void* q, const void* kv, const void* idx, const voi
  * lightning indexer), for one new token per request:
  *   cq   = rmsnorm(x Wq_a^T) * q_norm, rounded to the input type          (B, 1536)
  *   q    = [nope_h W_uk[h]^T | rope(pe_h)] per head h of cq Wq_b^T = [nope (128) | pe (64)]
- *   iq   = [rope(pe_j) | nope_j] per head j of cq Wiq_b^T = [pe (64) | nope (64)]
+ *   iq   = [rope_half(pe_j) | nope_j] per head j of cq Wiq_b^T = [pe (64) | nope (64)]
  *   w    = (x Wiw^T) / sqrt(64 * 128)                                     (B, 64) fp32, the op's pre-scaled w
  *   kv[b, pos[b]] = [rmsnorm(kv_c) * kv_norm | rope(k_pe)],  [kv_c (512) | k_pe (64)] = x Wkv_a^T
- *   ik[b, pos[b]] = layernorm(x Wik^T) * ik_norm_w + ik_norm_b, RoPE on its first 64 dims
- * RMSNorm/LayerNorm eps 1e-6; RoPE rotates interleaved pairs (v[2i], v[2i+1]) by rope_cos/rope_sin[pos[b], i]
- * (tables of (rope_rows, 32) fp32; pos is clamped into them).  The indexer's Hadamard rotation of DeepSeek-V3.2 is
+ *   ik[b, pos[b]] = layernorm(x Wik^T) * ik_norm_w + ik_norm_b, rope_half on its first 64 dims
+ * RMSNorm/LayerNorm eps 1e-6.  Both RoPE forms rotate pair i by rope_cos/rope_sin[pos[b], i] (tables of
+ * (rope_rows, 32) fp32; pos is clamped into them): MLA's `rope` (q's and kv's rope parts) pairs interleaved
+ * neighbours (v[2i], v[2i+1]); the indexer's `rope_half` (iq, ik) pairs the halves (v[i], v[i+32]), as
+ * DeepSeek-V3.2's indexer applies it (not interleaved).  The indexer's Hadamard rotation of DeepSeek-V3.2 is
  * orthonormal and leaves every iq . ik unchanged, so it is not applied.
  * Matrices are row-major (out, in), 16-bit like x (fp16; bf16 for the _bf16 entry); W_uk is the absorbed key half of
  * Wkv_b pre-transposed to (128 heads, 512 latent, 128 nope); norm weights are fp32.  The struct is read on the host

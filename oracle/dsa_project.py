@@ -11,11 +11,13 @@ Per request b, hidden state x (7168), position p:
   q_h = cq Wq_b^T, head h = [nope (128) | pe (64)]   (128 heads x 192)
   q   = [round16(nope_h) W_uk[h]^T (512) | rope(pe_h, p) (64)]      W_uk given as (128, 512, 128): [h][c][d]
   kv row p = [rmsnorm(kv_c) * kv_norm (512) | rope(k_pe, p) (64)],  [kv_c | k_pe] = x Wkv_a^T
-  iq_j = cq Wiq_b^T, head j = [rope(pe_j, p) (64) | nope_j (64)]   (64 heads x 128)
-  ik row p = layernorm(x Wik^T) * ik_w + ik_b, then rope on its first 64 dims
+  iq_j = cq Wiq_b^T, head j = [rope_half(pe_j, p) (64) | nope_j (64)]   (64 heads x 128)
+  ik row p = layernorm(x Wik^T) * ik_w + ik_b, then rope_half on its first 64 dims
   w   = (x Wiw^T) * 64^-1/2 * 128^-1/2                 (the op's "pre-scaled" w, ops/dsa.py:7, 28)
-RMSNorm and LayerNorm use eps = 1e-6.  RoPE rotates interleaved pairs (x[2i], x[2i+1]) by the table row p:
-(x0 c - x1 s, x0 s + x1 c) with c = cos[p, i], s = sin[p, i].  DeepSeek's indexer also applies a Hadamard rotation
+RMSNorm and LayerNorm use eps = 1e-6.  MLA's RoPE (q's and the kv row's rope parts) rotates interleaved pairs
+(x[2i], x[2i+1]) by the table row p: (x0 c - x1 s, x0 s + x1 c) with c = cos[p, i], s = sin[p, i].  The indexer's
+RoPE (iq's and the ik row's first 64 dims) is not interleaved: it rotates the pairs (x[i], x[i+32]) by the same
+entries, as DeepSeek-V3.2's inference code applies it in the indexer (apply_rotary_emb with interleaved=False).  DeepSeek's indexer also applies a Hadamard rotation
 to iq and ik before quantising them to fp8; the rotation is orthonormal, so it leaves every iq . ik product (and the
 op's scores) unchanged, and this fp16/bf16 contract has no quantisation, so it is left out.
 """
@@ -55,6 +57,13 @@ def rope(v, c, s):
     return out
 
 
+def rope_half(v, c, s):
+    """Rotate the pairs (v[i], v[i + n]) of v (..., 2n), the two halves, by per-pair cos/sin c, s (..., n)."""
+    n = v.shape[-1] // 2
+    x0, x1 = v[..., :n], v[..., n:]
+    return np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], axis=-1)
+
+
 W_SCALE = HI ** -0.5 * DI ** -0.5
 
 
@@ -87,8 +96,8 @@ def ref64(x, pos, cos, sin, wq_a, q_norm, wq_b, w_uk, wkv_a, kv_norm, iwq_b, iwk
     kvx = x @ to64(wkv_a).T
     kv_row = np.concatenate([rmsnorm(kvx[:, :DC], to64(kv_norm)), rope(kvx[:, DC:], c, s)], axis=-1)
     ipe, inope = split_iq((cq @ to64(iwq_b).T).reshape(-1, HI, DI))
-    iq = np.concatenate([rope(ipe, c[:, None], s[:, None]), inope], axis=-1)
+    iq = np.concatenate([rope_half(ipe, c[:, None], s[:, None]), inope], axis=-1)
     ikv = layernorm(x @ to64(iwk).T, to64(ik_norm_w), to64(ik_norm_b))
-    ik_row = np.concatenate([rope(ikv[:, :DR], c, s), ikv[:, DR:]], axis=-1)
+    ik_row = np.concatenate([rope_half(ikv[:, :DR], c, s), ikv[:, DR:]], axis=-1)
     w = (x @ to64(iw).T) * W_SCALE
     return dict(q=q, iq=iq, w=w, kv_row=kv_row, ik_row=ik_row)

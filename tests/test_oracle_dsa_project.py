@@ -1,7 +1,9 @@
 """Pins the float64 oracle of the DSA projections (oracle/dsa_project.py) without the reference (which has none).
 
-Independent checks: PyTorch's float64 rms_norm and layer_norm (library routines); RoPE against complex
-multiplication of the interleaved pairs (DeepSeek's formulation); two closed forms of the whole op (a zero hidden
+Independent checks: PyTorch's float64 rms_norm and layer_norm (library routines); both RoPE forms against complex
+multiplication as DeepSeek-V3.2's apply_rotary_emb states them (MLA: the interleaved pairs viewed as complex
+numbers; the indexer, interleaved=False: the 64 dims viewed as (2, 32), transposed into pairs, rotated, and the real
+and imaginary parts written back as the two halves); two closed forms of the whole op (a zero hidden
 state, where only the LayerNorm bias survives, and 0/1 selection weights, where every output is a known coordinate of
 x, so the head layouts, the absorbed product's orientation, the normed and rotated slices and the w scale are all
 fixed); and the scale structure (RMSNorm/LayerNorm outputs do not change when x doubles, the raw k_pe and w do).
@@ -23,6 +25,17 @@ def rope_complex(v, c, s):
     z = torch.view_as_complex(torch.from_numpy(np.ascontiguousarray(v, dtype=np.float64)).reshape(*v.shape[:-1], -1, 2))
     r = torch.complex(torch.from_numpy(np.asarray(c, np.float64)), torch.from_numpy(np.asarray(s, np.float64)))
     return torch.view_as_real(z * r).reshape(v.shape).numpy()
+
+
+def rope_complex_halves(v, c, s):
+    """Non-interleaved RoPE the way DeepSeek-V3.2 writes it: view (..., 2, n), transpose to (..., n, 2), rotate as
+    complex numbers, then [real parts | imaginary parts]."""
+    t = torch.from_numpy(np.ascontiguousarray(v, dtype=np.float64))
+    n = v.shape[-1] // 2
+    z = torch.view_as_complex(t.reshape(*v.shape[:-1], 2, n).transpose(-1, -2).contiguous())
+    r = torch.complex(torch.from_numpy(np.asarray(c, np.float64)), torch.from_numpy(np.asarray(s, np.float64)))
+    y = torch.view_as_real(z * r).reshape(v.shape)
+    return torch.cat([y[..., 0::2], y[..., 1::2]], -1).numpy()
 
 
 def tables(rows):
@@ -47,7 +60,20 @@ def rope_vs_complex(o):
     v = rng.standard_normal((5, 64))
     theta = rng.uniform(-4, 4, (5, 32))
     c, s = np.cos(theta), np.sin(theta)
-    return np.allclose(o.rope(v, c, s), rope_complex(v, c, s), atol=1e-12)
+    return np.allclose(o.rope(v, c, s), rope_complex(v, c, s), atol=1e-12) and \
+        np.allclose(o.rope_half(v, c, s), rope_complex_halves(v, c, s), atol=1e-12)
+
+
+def rope_forms_differ(o):
+    """A closed form that tells the two pairings apart: v = e_1 (the second dim) rotated by a quarter turn of pair 0
+    and no turn elsewhere.  Interleaved pairs (v0, v1) give -e_0; halves leave e_1 in place (its pair is (v1, v33),
+    not turned)."""
+    v = np.zeros((1, 64))
+    v[0, 1] = 1.0
+    c, s = np.ones((1, 32)), np.zeros((1, 32))
+    c[0, 0], s[0, 0] = 0.0, 1.0
+    e0, e1 = np.eye(64)[0:1], np.eye(64)[1:2]
+    return np.allclose(o.rope(v, c, s), -e0, atol=1e-15) and np.allclose(o.rope_half(v, c, s), e1, atol=1e-15)
 
 
 _RANDOM = {}
@@ -73,8 +99,8 @@ def zero_input(o):
     r = run(o, np.zeros((2, DIM), dtype=np.float32), pos, W)
     _, cos, sin = tables(64)
     bias = W["ik_norm_b"].double().numpy()
-    want_ik = np.concatenate([rope_complex(np.tile(bias[:DR], (2, 1)), cos[pos], sin[pos]), np.tile(bias[DR:], (2, 1))],
-                             -1)
+    want_ik = np.concatenate([rope_complex_halves(np.tile(bias[:DR], (2, 1)), cos[pos], sin[pos]),
+                              np.tile(bias[DR:], (2, 1))], -1)
     zero = all(np.array_equal(r[k], np.zeros_like(r[k])) for k in ("q", "iq", "w", "kv_row"))
     return zero and np.allclose(r["ik_row"], want_ik, atol=1e-12)
 
@@ -141,17 +167,17 @@ def selection_closed_form(o):
     kv = np.concatenate([kvc / np.sqrt((kvc ** 2).mean(-1, keepdims=True) + eps),
                          rope_complex(x[:, QL + DC:QL + DC + DR], c, s)], -1)
     yi = cq[:, (3 * np.arange(HI * DI)) % QL].reshape(2, HI, DI)
-    iq = np.concatenate([rope_complex(yi[..., :DR], ci, si), yi[..., DR:]], -1)
+    iq = np.concatenate([rope_complex_halves(yi[..., :DR], ci, si), yi[..., DR:]], -1)
     v = x[:, 2112:2112 + DI]
     ln = (v - v.mean(-1, keepdims=True)) / np.sqrt(v.var(-1, keepdims=True) + eps) + 0.25
-    ik = np.concatenate([rope_complex(ln[:, :DR], c, s), ln[:, DR:]], -1)
+    ik = np.concatenate([rope_complex_halves(ln[:, :DR], c, s), ln[:, DR:]], -1)
     w = x[:, 3000:3000 + HI] / np.sqrt(HI * DI)
     close = lambda a, b: np.allclose(a, b, rtol=1e-9, atol=1e-9)
     return close(r["q"], q) and close(r["kv_row"], kv) and close(r["iq"], iq) and close(r["ik_row"], ik) and \
         close(r["w"], w)
 
 
-CHECKS = [norms_vs_torch, rope_vs_complex, zero_input, scale_structure, selection_closed_form]
+CHECKS = [norms_vs_torch, rope_vs_complex, rope_forms_differ, zero_input, scale_structure, selection_closed_form]
 
 
 @pytest.mark.parametrize("check", CHECKS, ids=lambda c: c.__name__)
@@ -169,7 +195,8 @@ def _rope_halves(v, c, s):
 
 
 MUTANTS = {
-    "rope on halves, not interleaved pairs": dict(rope=_rope_halves),
+    "MLA rope on halves, not interleaved pairs": dict(rope=_rope_halves),
+    "indexer rope on interleaved pairs, not halves": dict(rope_half=odp.rope),
     "rmsnorm without eps": dict(rmsnorm=lambda v, w, eps=0.0: v / np.sqrt(np.mean(v * v, -1, keepdims=True)) * w),
     "layernorm without bias": dict(layernorm=lambda v, w, b, eps=odp.EPS: _layernorm(v, w, 0 * b, eps)),
     "layernorm with the unbiased variance": dict(

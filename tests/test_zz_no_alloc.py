@@ -46,3 +46,20 @@ def test_noalloc_refuses_shapes_beyond_its_scratch():
     with pytest.raises(lib.VmkError, match="static scratch"):
         lib.call("vmk_spec_verify_noalloc", x.data_ptr(), x.data_ptr(), x.data_ptr(), words.data_ptr(), x.data_ptr(),
                  8, 64, 32, 8, 128, L, 2, torch.cuda.current_stream().cuda_stream)
+
+
+def test_noalloc_on_a_side_stream():
+    """The scratch is looked up for the device of the stream the call is launched on (here a non-default stream
+    of the current GPU), through the Python wrapper, and gives the same bits as the workspace entry point."""
+    import vmk
+    inp = spec.make_inputs(dict(B=2, L=5000, k=8), seed=4, dist="chain", device="cuda")
+    words = spec.mask_words(inp["bits"], 8).contiguous()
+    want = call_workspace(inp)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out = torch.full_like(inp["q"], float("nan"))
+        vmk.spec_verify_noalloc(inp["q"], inp["k"], inp["v"], words, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))

@@ -10,7 +10,7 @@
 // Launch 2 (proj_heads_kernel): 256 workgroups of 8 waves, each 128 rows of Wq_b or Wiq_b against cq.  Workgroup h
 //   (< 128) takes MLA head h's nope rows and then the absorbed product with W_uk[h] (512 x 128); workgroups 128 + p
 //   take the pe rows of heads 2p and 2p + 1 (RoPE) and finish token p's cache rows and w; workgroups 192 + j take
-//   indexer head j's rows (RoPE on the first 64).  Every workgroup first sums cq's K parts and RMSNorms it itself
+//   indexer head j's rows (RoPE on the first 64, pairs (i, i + 32)).  Every workgroup first sums cq's K parts and RMSNorms it itself
 //   (the same arithmetic in each), so no launch runs between the two.
 // GEMV tiles use the 32x32x16 MFMA with weight rows as A and the batch (up to 32 tokens per tile) as B; every wave
 // issues all its weight loads before its first MFMA, and the K split inside a workgroup is summed through LDS in
@@ -163,7 +163,8 @@ __device__ __forceinline__ float yx_sum(const ProjArgs& a, int b, int row) {
 
 __device__ __forceinline__ int rope_row(const ProjArgs& a, int b) { return min(max(a.pos[b], 0), a.rope_rows - 1); }
 
-// Token b's cache rows (kv: RMSNorm of kv_c, RoPE of k_pe; ik: LayerNorm, RoPE of its first 64) and w, by 512 threads.
+// Token b's cache rows (kv: RMSNorm of kv_c, interleaved RoPE of k_pe; ik: LayerNorm, RoPE of its first 64 on the
+// pairs (i, i + 32)) and w, by 512 threads.
 // Rows are written only for a position inside the cache.
 template <class E>
 __device__ void finish_token(const ProjArgs& a, int b, float* red, float* ikn) {
@@ -189,11 +190,11 @@ __device__ void finish_token(const ProjArgs& a, int b, float* red, float* ikn) {
   if (store && t < kPDi) {
     E* ikr = reinterpret_cast<E*>(a.ik) + ((size_t)b * a.L + p) * kPDi;
     float o = ikn[t];
-    if (t < kPDr) {
-      const int i = t >> 1;
+    if (t < kPDr) {                                           // indexer RoPE: pairs (i, i + 32), not interleaved
+      const int i = t & 31;
       const float c2 = a.rcos[(size_t)pr * 32 + i], s2 = a.rsin[(size_t)pr * 32 + i];
-      const float x0 = ikn[2 * i], x1 = ikn[2 * i + 1];
-      o = (t & 1) ? x0 * s2 + x1 * c2 : x0 * c2 - x1 * s2;
+      const float x0 = ikn[i], x1 = ikn[i + 32];
+      o = (t & 32) ? x0 * s2 + x1 * c2 : x0 * c2 - x1 * s2;
     }
     ikr[t] = (E)o;
   }
@@ -319,23 +320,22 @@ __global__ __launch_bounds__(512) void proj_heads_kernel(ProjArgs a) {
   if (live) {
     const int hj = wg - kPH - kPH / 2;
     E* io = reinterpret_cast<E*>(a.iq) + ((size_t)b * kPHi + hj) * kPDi;
+    if (bp == 0) {
+      // Blocks 0 and 1 are the 64 pe dims: this lane holds dims r and r + 32 of each rotated pair (the indexer's
+      // RoPE pairs the halves, not interleaved neighbours), rotated by table entry r.
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = 2 * bp + j;
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int e = 32 * i + 8 * kq + 4 * g + 2 * m;
-        const float x0 = out[j][2 * m], x1 = out[j][2 * m + 1];
-        if (e < kPDr) {
-          const int pi = e >> 1;
-          const float cs = a.rcos[(size_t)pr * 32 + pi], sn = a.rsin[(size_t)pr * 32 + pi];
-          io[e] = (E)(x0 * cs - x1 * sn);
-          io[e + 1] = (E)(x0 * sn + x1 * cs);
-        } else {
-          io[e] = (E)x0;
-          io[e + 1] = (E)x1;
-        }
+      for (int c = 0; c < 4; ++c) {
+        const int r = 8 * kq + 4 * g + c;
+        const float cs = a.rcos[(size_t)pr * 32 + r], sn = a.rsin[(size_t)pr * 32 + r];
+        const float x0 = out[0][c], x1 = out[1][c];
+        io[r] = (E)(x0 * cs - x1 * sn);
+        io[r + 32] = (E)(x0 * sn + x1 * cs);
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) io[32 * (2 + j) + 8 * kq + 4 * g + c] = (E)out[j][c];
     }
   }
 }

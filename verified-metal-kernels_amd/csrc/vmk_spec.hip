@@ -432,15 +432,25 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 static void* g_scratch_ptr[kScratchDevices];
 static std::mutex g_scratch_mu;
 
-// Device address of the current device's `scratch` (looked up on the first call on that device); 0 on success.
-static int scratch_address(void** ptr) {
+// Device address of `scratch` on the device that `stream` belongs to (the current device for the null stream),
+// looked up on the first call on that device with that device made current, and kept per device; 0 on success.
+static int scratch_address(hipStream_t stream, void** ptr) {
   int dev = -1;
-  VMK_CHECK_HIP(hipGetDevice(&dev));
+  if (stream) {
+    VMK_CHECK_HIP(hipStreamGetDevice(stream, &dev));
+  } else {
+    VMK_CHECK_HIP(hipGetDevice(&dev));
+  }
   VMK_CHECK(dev >= 0 && dev < kScratchDevices, "device index beyond the per-device scratch table");
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    VMK_CHECK_HIP(hipGetDevice(&cur));
+    if (cur != dev) VMK_CHECK_HIP(hipSetDevice(dev));
     void* p = nullptr;
-    VMK_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) VMK_CHECK_HIP(hipSetDevice(cur));
+    VMK_CHECK_HIP(e);
     VMK_CHECK(p != nullptr && ((uintptr_t)p & 255u) == 0, "scratch symbol address missing or misaligned");
     g_scratch_ptr[dev] = p;
   }
@@ -464,7 +474,7 @@ extern "C" int vmk_spec_verify_noalloc(const void* q, const void* k, const void*
     return 1;
   }
   void* partials = nullptr;
-  if (int rc = scratch_address(&partials)) return rc;
+  if (int rc = scratch_address((hipStream_t)stream, &partials)) return rc;
   SpecArgs a;
   a.q = (const f16*)q; a.k = (const f16*)k; a.v = (const f16*)v; a.bits = (const uint32_t*)mask_words;
   a.lens = nullptr;

@@ -5,11 +5,13 @@ Arguments are checked in this order: types, dtypes and ranks, then shapes agains
 tensor is on a ROCm device, so a wrongly shaped tensor is refused before any GPU work.
 
 Workspaces come from one cached byte buffer per device.  Calls that overlap on two streams of one device would
-share it, so they must be ordered by the caller.  The buffer only grows; a buffer it outgrows is kept alive until
-the process ends, because a HIP graph captured before the growth still addresses it.  Growth is refused while the
-current stream is capturing (`reserve_workspace` beforehand, or one eager call of the largest shape, avoids it).
-After a failed call the buffer is set aside the same way and the next call starts from a fresh zeroed one, since a
-call that stops half-way can leave the workspace head (which must stay zero between calls) non-zero.
+share it, so they must be ordered by the caller.  The buffer only grows, at least doubling each time, so a growing
+workload reallocates O(log) times.  A buffer it outgrows is freed (after the device's queued work) unless a HIP graph
+was captured while it was current: such a graph still addresses it, so it is kept alive until the process ends.
+Growth is refused while the current stream is capturing (`reserve_workspace` beforehand, or one eager call of the
+largest shape, avoids it).  After a call that failed at launch (return code 2) the buffer is set aside the same
+way and the next call starts from a fresh zeroed one, since a call that stops half-way can leave the workspace head
+(which must stay zero between calls) non-zero; a call refused on the host (code 1) launched nothing and keeps it.
 """
 import ctypes
 
@@ -18,9 +20,23 @@ import torch
 from . import lib
 
 _ws = {}
-_retired = []          # outgrown or possibly dirty workspaces, kept alive for graphs captured over them
+_captured = set()      # devices whose current workspace was handed out during a HIP graph capture
+_retired = []          # workspaces a captured graph may still address, kept alive until the process ends
 _dev_ok = {}
 HEAD_BYTES = 4 << 20   # VMK_WORKSPACE_HEAD of include/vmk.h: must be zero before a call, is zero after it
+MIN_WORKSPACE = 1 << 20
+
+
+def _alloc(nbytes, key):
+    return torch.zeros(nbytes, dtype=torch.uint8, device=torch.device("cuda", key))
+
+
+def _capturing():
+    return torch.cuda.is_current_stream_capturing()
+
+
+def _drain(key):
+    torch.cuda.synchronize(key)
 
 
 def device_ok(device):
@@ -45,15 +61,34 @@ def workspace(nbytes, device):
     """A cached uint8 buffer of at least `nbytes` on `device`, allocated zeroed (the head must start at zero)."""
     key = _dev_index(device)
     buf = _ws.get(key)
+    capturing = _capturing()
     if buf is None or buf.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
+        if capturing:
             raise lib.VmkError(f"the libvmk workspace would have to grow to {int(nbytes)} bytes during HIP graph "
                                "capture; call vmk.reserve_workspace (or the op once, eagerly) before capturing")
+        size = max(int(nbytes), MIN_WORKSPACE)
         if buf is not None:
-            _retired.append(buf)
-        buf = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=torch.device("cuda", key))
+            size = max(size, 2 * buf.numel())
+            _set_aside(key)
+        buf = _alloc(size, key)
         _ws[key] = buf
+    if capturing:
+        _captured.add(key)
     return buf
+
+
+def _set_aside(key):
+    """Takes device `key`'s workspace out of use: kept alive until the process ends when a graph was captured over
+    it, else released to torch's allocator once the work queued on the device (any stream) has finished."""
+    buf = _ws.pop(key)
+    if key in _captured:
+        _captured.discard(key)
+        _retired.append(buf)
+        return
+    try:
+        _drain(key)
+    except RuntimeError:            # the device reports an error: keep the buffer rather than risk a reuse race
+        _retired.append(buf)
 
 
 def reserve_workspace(nbytes, device="cuda"):
@@ -62,13 +97,14 @@ def reserve_workspace(nbytes, device="cuda"):
 
 
 def _launch(name, ws, *args):
-    """Calls entry point `name`; on failure the workspace `ws` is set aside before the error propagates."""
+    """Calls entry point `name`; after a launch or runtime failure the workspace `ws` is set aside before the error
+    propagates (a refusal of the arguments launched nothing and leaves it in use)."""
     try:
         lib.call(name, *args)
-    except lib.VmkError:
+    except lib.VmkError as e:
         key = ws.device.index
-        if _ws.get(key) is ws:
-            _retired.append(_ws.pop(key))
+        if e.code != lib.REJECTED and _ws.get(key) is ws:
+            _set_aside(key)
         raise
 
 
@@ -173,8 +209,9 @@ def spec_verify_noalloc(q, k, v, words, out):
     if tuple(words.shape) != (B, kd, (kd + 31) // 32):
         raise ValueError(f"bits shape {tuple(words.shape)} is not (B, kd, ceil(kd/32)) = {(B, kd, (kd + 31) // 32)}")
     _resident(q=q, k=k, v=v, bits=words, out=out)
-    lib.call("vmk_spec_verify_noalloc", q.data_ptr(), k.data_ptr(), v.data_ptr(), words.data_ptr(), out.data_ptr(),
-             B, kd, Hq, Hkv, D, L, words.shape[2], _stream(q))
+    with torch.cuda.device(q.device):           # the scratch of q's GPU, launched on that GPU's current stream
+        lib.call("vmk_spec_verify_noalloc", q.data_ptr(), k.data_ptr(), v.data_ptr(), words.data_ptr(),
+                 out.data_ptr(), B, kd, Hq, Hkv, D, L, words.shape[2], _stream(q))
     return out
 
 

@@ -72,7 +72,15 @@ class DsaProjectWeights(ctypes.Structure):
 
 
 class VmkError(RuntimeError):
-    pass
+    """A failed libvmk call; `code` is the entry point's return value (1 = arguments rejected, nothing launched;
+    2 = HIP launch or runtime error), None for errors raised on the Python side."""
+
+    def __init__(self, msg, code=None):
+        super().__init__(msg)
+        self.code = code
+
+
+REJECTED, LAUNCH_ERROR = 1, 2
 
 
 def load():
@@ -105,7 +113,7 @@ def exported_symbols():
 
 def check(rc):
     if rc != 0:
-        raise VmkError(load().vmk_last_error().decode(errors="replace") or f"libvmk error {rc}")
+        raise VmkError(load().vmk_last_error().decode(errors="replace") or f"libvmk error {rc}", code=rc)
 
 
 def call(name, *args):

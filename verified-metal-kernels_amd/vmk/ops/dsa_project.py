@@ -72,6 +72,12 @@ def _rope(v, c, s):
     return torch.stack([x0 * c - x1 * s, x0 * s + x1 * c], dim=-1).flatten(-2)
 
 
+def _rope_half(v, c, s):
+    n = v.shape[-1] // 2
+    x0, x1 = v[..., :n], v[..., n:]
+    return torch.cat([x0 * c - x1 * s, x0 * s + x1 * c], dim=-1)
+
+
 def torch_ref(x, pos, rope_cos, rope_sin, weights, kv=None, ik=None):
     """The projections as PyTorch ops, the standard op the benchmark times against: the products in x's 16-bit type
     (F.linear, fp32 accumulation), norms and RoPE in float32, the absorbed product as one batched matmul over the
@@ -89,9 +95,9 @@ def torch_ref(x, pos, rope_cos, rope_sin, weights, kv=None, ik=None):
     kvx = lin(x, W["wkv_a"]).float()
     kv_row = torch.cat([_rms(kvx[:, :DC], W["kv_norm"]), _rope(kvx[:, DC:], c, s)], -1)
     yi = lin(cq, W["iwq_b"]).view(-1, HI, DI).float()
-    iq = torch.cat([_rope(yi[..., :DR], c[:, None], s[:, None]), yi[..., DR:]], -1)
+    iq = torch.cat([_rope_half(yi[..., :DR], c[:, None], s[:, None]), yi[..., DR:]], -1)
     ikv = torch.nn.functional.layer_norm(lin(x, W["iwk"]).float(), (DI,), W["ik_norm_w"], W["ik_norm_b"], EPS)
-    ik_row = torch.cat([_rope(ikv[:, :DR], c, s), ikv[:, DR:]], -1)
+    ik_row = torch.cat([_rope_half(ikv[:, :DR], c, s), ikv[:, DR:]], -1)
     w = lin(x, W["iw"]).float() * (HI ** -0.5 * DI ** -0.5)
     return q.to(dt), iq.to(dt), w, kv_row.to(dt), ik_row.to(dt)
 
