@@ -55,6 +55,8 @@ METRIC = "µs/call per op + achieved HBM GB/s (% of MI355X peak) at bench shapes
 HEADLINE = "C4"
 DOMINANT = {"prefix": "prefix_partial", "spec": "spec_partial", "dsa": "dsa_indexer", "decode": "spec_partial",
             "prefix_paged": "prefix_partial", "dsa_project": "dsa_project_q", "decode_paged": "spec_partial"}
+# Configurations whose dominant bracket is another kernel: C5s runs the DSA decode as one launch (the whole op).
+DOMINANT_CFG = {"C5s": "dsa_single"}
 # Inputs the ops write by contract (the projections append the new token's cache rows), left out of the
 # input-mutation check.
 WRITES = {"dsa_project": ("kv", "ik")}
@@ -73,7 +75,7 @@ def config_table():
     from vmk.ops import decode, decode_paged, dsa, dsa_project, prefix, prefix_paged, spec
     return [("C1", "prefix", *prefix.CONFIGS["C1"]), ("C2", "prefix", *prefix.CONFIGS["C2"]),
             ("C3", "spec", *spec.CONFIGS["C3"]), ("C4", "spec", *spec.CONFIGS["C4"]),
-            ("C5", "dsa", *dsa.CONFIGS["C5"]),
+            ("C5", "dsa", *dsa.CONFIGS["C5"]), ("C5s", "dsa", dict(dsa.CONFIGS["C5"][0], single=1), "randn"),
             ("D1", "decode", *decode.CONFIGS["D1"]), ("D2", "decode", *decode.CONFIGS["D2"]),
             ("D3", "decode", *decode.CONFIGS["D3"]), ("P2", "prefix_paged", *prefix_paged.CONFIGS["P2"]),
             ("P2n", "prefix_paged", *prefix_paged.CONFIGS["P2n"]),
@@ -82,7 +84,11 @@ def config_table():
 
 
 class HipEvents:
-    """Raw HIP events (libamdhip64 through ctypes) for the per-kernel brackets recorded inside libvmk."""
+    """Raw HIP events (libamdhip64 through ctypes) for the per-kernel brackets recorded inside libvmk.  They are
+    created with hipEventDisableSystemFence: a timing-only event then skips the system-scope cache writeback and
+    invalidation on recording, which would otherwise land inside the bracket (the elapsed times are read only after
+    a device synchronisation)."""
+    DISABLE_SYSTEM_FENCE = 0x20000000           # hipEventDisableSystemFence of hip_runtime_api.h
 
     def __init__(self, n):
         import ctypes
@@ -90,8 +96,8 @@ class HipEvents:
         self.ev = []
         for _ in range(2 * n):
             e = ctypes.c_void_p()
-            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
-                raise RuntimeError("hipEventCreate failed")
+            if self.hip.hipEventCreateWithFlags(ctypes.byref(e), ctypes.c_uint(self.DISABLE_SYSTEM_FENCE)) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
             self.ev.append(e)
 
     def pair(self, i):
@@ -127,7 +133,8 @@ def call_op(opname, inp):
     if opname == "dsa_project":                           # q stands for the three outputs in the checks
         return vmk.dsa_project(inp["x"], inp["pos"], inp["rope_cos"], inp["rope_sin"], inp["weights"], inp["kv"],
                                inp["ik"])[0]
-    return vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], inp.get("lens"))
+    return vmk.dsa_decode(inp["q"], inp["kv"], inp["iq"], inp["ik"], inp["w"], inp.get("lens"),
+                          single=bool(inp.get("single")))
 
 
 def std_op(opname, inp):
@@ -292,10 +299,15 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     inp0 = {k: to_gpu(v) for k, v in host.items()}
     if opname == "spec":
         inp0["words"] = op.mask_words(inp0["bits"], shape["k"]).contiguous()
+    if shape.get("single"):
+        inp0["single"] = True
+    dom_kernel = DOMINANT_CFG.get(name, DOMINANT[opname])
     total_bytes, dom_bytes, flops = op_bytes_flops(opname, shape, host)
     # FLOPs inside the dominant bracket: all of them for the attention ops, the score GEMM for DSA's indexer.
     dom_flops = {"dsa": lambda: 2 * shape["B"] * shape["L"] * op.HI * op.DI, "dsa_project": lambda: None}.get(
         opname, lambda: flops)()
+    if name in DOMINANT_CFG:                       # the bracket is the whole op
+        dom_bytes, dom_flops = total_bytes, flops
     # Output check on the benchmark inputs and input-mutation check (reference bench.py:180-192).
     snap = {k: v.clone() for k, v in inp0.items() if isinstance(v, torch.Tensor) and k not in WRITES.get(opname, ())}
     out = call_op(opname, inp0)
@@ -313,7 +325,7 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     for i in range(warmup):
         call_op(opname, sets[i % len(sets)])
     torch.cuda.synchronize()
-    kid = lib.KERNEL_IDS[DOMINANT[opname]]
+    kid = lib.KERNEL_IDS[dom_kernel]
     hev = HipEvents(steps)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     L = lib.load()
@@ -336,10 +348,10 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
                pct_peak=round(100 * gbs / PEAK_HBM_GBS, 2), algorithmic_bytes=int(total_bytes),
                tflops=round(flops / us / 1e6, 2), mfma_pct=round(100 * flops / us / 1e6 / PEAK_FP16_TFLOPS, 2),
                eager=dict(us_per_call=round(eager_us, 2), gbs=round(total_bytes / eager_us / 1e3, 1)),
-               dominant=dict(kernel=DOMINANT[opname], us=round(dom_us, 2), bytes=int(dom_bytes),
+               dominant=dict(kernel=dom_kernel, us=round(dom_us, 2), bytes=int(dom_bytes),
                              gbs=round(dom_gbs, 1), frac=round(dom_gbs / PEAK_HBM_GBS, 4),
                              tflops=round(dom_flops / dom_us / 1e6, 2) if dom_flops else None,
-                             sq=measured_mfma(name, DOMINANT[opname])),
+                             sq=measured_mfma(name, dom_kernel)),
                output_check="ok", distinct_input_sets=len(sets))
     if opname not in AB_OPS:                               # no reference A/B for this op: its torch form, graph-timed
         ts = graph_us_per_call(opname, sets, steps, fn=lambda s: std_op(opname, s), check=False)
@@ -347,8 +359,8 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     row["dominant"]["traffic"] = measured_traffic(name, row["dominant"])
     log(f"[{name}] {us:9.2f} us/call (p10 {gt['p10']:.2f}, p90 {gt['p90']:.2f})  {gbs:7.1f} GB/s "
         f"({row['pct_peak']:.1f}% of 8 TB/s)  [median of {gt['n']} replays of a HIP graph of {steps} calls; "
-        f"eager loop {eager_us:.2f} us/call]   dominant {DOMINANT[opname]} {dom_us:.2f} us = {dom_gbs:.0f} GB/s")
-    if do_cpu:
+        f"eager loop {eager_us:.2f} us/call]   dominant {dom_kernel} {dom_us:.2f} us = {dom_gbs:.0f} GB/s")
+    if do_cpu and name not in DOMINANT_CFG:        # C5s is C5's workload: its CPU baseline is C5's
         row["cpu_baseline"] = cpu_baseline(opname, shape, dist, host, total_bytes)
         log(f"[{name}] CPU float64 oracle: {row['cpu_baseline']['us_per_call']:.0f} us/call "
             f"({row['cpu_baseline']['sample']}, {row['cpu_baseline']['cores']} cores)")
@@ -644,7 +656,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,D1,D2,D3,P2,P2n,D1p,D2n,C2b,DP")
+    ap.add_argument("--configs", default="C1,C2,C3,C4,C5,C5s,D1,D2,D3,P2,P2n,D1p,D2n,C2b,DP")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle timings")
     ap.add_argument("--ab-rounds", type=int, default=10,
                     help="shuffled rounds of the A/B comparison with the torch standard ops (0: skip it)")

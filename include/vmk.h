@@ -252,12 +252,26 @@ int vmk_dsa_project_bf16(const void* x, const void* pos, const void* rope_cos, c
 int vmk_dsa_decode(const void* q, const void* kv, const void* iq, const void* ik, const void* w, const void* lens,
                    void* out, void* idx, void* cnt, int64_t B, int64_t L, void* workspace, size_t ws_bytes,
                    void* stream);
+/* The same decode step as ONE kernel launch (the reference's chain of 5-6 launches, dsa_opus55_v7.py:946-977, and
+ * vmk_dsa_decode's four, fused): indexer, select, attention and combine run as phases of one grid of at most one
+ * co-resident round of workgroups, separated by grid barriers.  Same arguments, workspace size and outputs as
+ * vmk_dsa_decode, bit for bit.  Every grid-barrier wait is bounded: if one gives up (workgroups that were not
+ * resident together, e.g. beside another kernel on the device), the call still ends, and reports cnt[b] = -1 for
+ * every request; the workspace then stays marked (every later call on it reports -1 the same way) until its head
+ * is zeroed. */
+int vmk_dsa_decode_single(const void* q, const void* kv, const void* iq, const void* ik, const void* w,
+                          const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L, void* workspace,
+                          size_t ws_bytes, void* stream);
+int vmk_dsa_decode_single_bf16(const void* q, const void* kv, const void* iq, const void* ik, const void* w,
+                               const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L,
+                               void* workspace, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------- measurement hook
  * No reference counterpart (the reference times whole calls only, bench.py:61-96).  The next launch of kernel
  * `kernel_id` on this host thread is bracketed by hipEventRecord(before) and hipEventRecord(after) on its stream.
  * Ids: 0 spec_partial, 1 spec_combine, 2 prefix_partial, 3 prefix_combine, 4 dsa_indexer, 5 dsa_select (final),
- *      6 dsa_attn, 7 dsa_combine, 8 dsa_select_scan, 9 the heads launch of vmk_dsa_project (its q, iq products and the absorbed product). */
+ *      6 dsa_attn, 7 dsa_combine, 8 dsa_select_scan, 9 the heads launch of vmk_dsa_project (its q, iq products and
+ *      the absorbed product), 10 the single-launch DSA decode kernel. */
 int vmk_profile_next(void* before_event, void* after_event, int kernel_id);
 
 /* ---------------------------------------------------------------------------------------------- test hooks

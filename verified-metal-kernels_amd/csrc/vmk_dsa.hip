@@ -57,6 +57,7 @@ struct DsaArgs {
   const float* scores_in;  // (B, L) caller scores for vmk_dsa_topk, copied into `scores` by dsa_scores_hist_kernel
   uint32_t* chist;      // (B, 256) coarse histogram: 32 first-digit bins per coarse bin (zero-invariant like hist)
   float sl2;            // attention scale * log2(e)
+  uint32_t* sync;       // single-launch decode: grid-barrier counters and the timeout flag (workspace head)
 };
 
 // Order-preserving float -> uint32 map: a < b as floats  <=>  fkey(a) < fkey(b) (NaN above +inf).
@@ -134,35 +135,36 @@ struct IkSrc {
 
 // S = iq . ik^T per 32-position tile (M = 64 heads as two 32-row MFMA tiles, N = positions, K = 128 dims), then
 // score = sum_h w[h] * max(S[h], 0) in fp32, and histograms of fkey(score) >> 19 (fine) and >> 24 (coarse) per
-// request.  Each of the 8 waves streams its 4 tiles through a private 2-stage ring of direct-to-LDS loads; the B
-// operand (ik^T) is read from the stage with the attention core's K-operand offsets.
-template <class V>
-__global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) {
-  __shared__ __attribute__((aligned(16))) char ring[kIdxWaves * kIdxStages * kIdxStageBytes];
-  __shared__ uint32_t hist2[kBins / 2];                     // two 16-bit bin counts per word (<= 1024 per bin)
-  __shared__ uint32_t chist[kCBins];
-  const int b = blockIdx.y, tid = threadIdx.x;
+// request.  One item = positions [1024 bx, 1024 bx + 1024) of request b, by NW waves (64 NW threads); each wave
+// streams its 32 / NW tiles through a private NS-stage ring of direct-to-LDS loads; the B operand (ik^T) is read from
+// the stage with the attention core's K-operand offsets.  LDS: ring (NW * NS * 8 KB), hist2 (16 KB), chist (1 KB).
+template <class V, int NW, int NS>
+__device__ __forceinline__ void indexer_item(const DsaArgs& a, int bx, int b, char* __restrict__ ring,
+                                             uint32_t* __restrict__ hist2, uint32_t* __restrict__ chist) {
+  static_assert(NS >= 2 && NS <= 4 && NW * 64 >= kCBins && 16 % NW == 0 && NW >= 3,
+                "iq, w in the last stage of waves 0-2; 16 iq loads split over the waves");
+  const int tid = threadIdx.x;
   const int n = valid_len(a, b);
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, g = lane >> 5;
   // Every wave needs all of iq (16 KB) and w (256 B) as operands.  They are loaded once per workgroup, by direct-to-
-  // LDS loads into ring stages that the walk has not started on (stage 1 of waves 0, 1 and 2), ahead of the ring's
-  // first tiles: per-wave loads would push 8x the bytes through the CU's load path in front of tile 0.  iq row r
-  // lands at byte 256 r of its half (heads 0-31, 32-63) with 16-byte chunk c at position c ^ (r & 15), so the
-  // operand reads below, 32 rows at one chunk, hit 16 distinct bank groups.
+  // LDS loads into the last ring stage of waves 0, 1 and 2 (which the walk fills last), ahead of the ring's first
+  // tiles: per-wave loads would push NW x the bytes through the CU's load path in front of tile 0.  iq row r lands
+  // at byte 256 r of its half (heads 0-31, 32-63) with 16-byte chunk c at position c ^ (r & 15), so the operand
+  // reads below, 32 rows at one chunk, hit 16 distinct bank groups.
   V qa[2][8];                                                // filled from LDS before the walk
   float wv[2][16];
   const f16* iqb = a.iq + (size_t)b * kHI * kDI;
-  char* const iq_lds0 = ring + kIdxStageBytes;
-  char* const iq_lds1 = ring + 3 * kIdxStageBytes;
-  char* const w_lds = ring + 5 * kIdxStageBytes;
-  static_assert(kIdxWaves == 8 && kIdxStages == 2, "16 iq loads of 1 KB, two per wave; stage 1 of waves 0-2 free");
+  char* const iq_lds0 = ring + (0 * NS + NS - 1) * kIdxStageBytes;
+  char* const iq_lds1 = ring + (1 * NS + NS - 1) * kIdxStageBytes;
+  char* const w_lds = ring + (2 * NS + NS - 1) * kIdxStageBytes;
+  constexpr int kIqPerWave = 16 / NW;
   {
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(iqb), 0, kHI * kDI * 2, 0x00020000);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int j = 2 * wave + q;                            // rows 4j .. 4j + 3
+    for (int q = 0; q < kIqPerWave; ++q) {
+      const int j = kIqPerWave * wave + q;                   // rows 4j .. 4j + 3
       const int row = 4 * j + (lane >> 4);
       const uint32_t off = (uint32_t)(row * 256 + (((lane & 15) ^ (row & 15)) << 4));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, VMK_LPTR((j < 8 ? iq_lds0 : iq_lds1) + (j & 7) * 1024), 16, off,
@@ -179,10 +181,10 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
   src.kbase = a.ik + (size_t)b * a.L * kDI;
   src.vbase = src.kbase;
   src.kend = n;
-  constexpr int kTilesPerWave = kIdxWG / kTile / kIdxWaves;
-  const int t0 = blockIdx.x * (kIdxWG / kTile) + wave * kTilesPerWave;   // this wave's first tile
+  constexpr int kTilesPerWave = kIdxWG / kTile / NW;
+  const int t0 = bx * (kIdxWG / kTile) + wave * kTilesPerWave;   // this wave's first tile
   const int nt = max(0, min(kTilesPerWave, (n + kTile - 1) / kTile - t0));
-  const uint32_t ring_off = (uint32_t)wave * kIdxStages * kIdxStageBytes;
+  const uint32_t ring_off = (uint32_t)wave * NS * kIdxStageBytes;
   const TileLanes tl = tile_lanes(lane, ring_off);
   char* wring = ring + ring_off;
   float* sc = a.scores + (size_t)b * a.Ls;
@@ -225,12 +227,13 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
     issue(wring + S * kIdxStageBytes, S);
     return true;
   };
-  unroll_while<0, kIdxStages - 1>(pre);
-  // The histogram is cleared while the loads fly; the wait lets only tile 0's loads (issued last) stay in flight, so
-  // after the barrier every wave's part of iq and w is in LDS.  A second barrier frees stage 1 for the walk.
-  for (int i = tid; i < kBins / 2; i += 64 * kIdxWaves) hist2[i] = 0;
+  unroll_while<0, NS - 1>(pre);
+  // The histogram is cleared while the loads fly; the wait lets only the ring's first tiles (issued after iq and w)
+  // stay in flight, so after the barrier every wave's part of iq and w is in LDS.  A second barrier frees the last
+  // stages for the walk.
+  for (int i = tid; i < kBins / 2; i += 64 * NW) hist2[i] = 0;
   if (tid < kCBins) chist[tid] = 0;
-  wait_vmem_dyn(nt > 0 ? 8 : 0);
+  wait_vmem_dyn(8 * min(NS - 1, nt));
   lds_barrier();
 #pragma unroll
   for (int s = 0; s < 8; ++s) {                              // Q^T operand: head r's dims 64g + 8s .. (chunk 8g + s)
@@ -247,22 +250,22 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
       for (int e = 0; e < 4; ++e) wv[ht][4 * i4 + e] = v[e];
     }
   lds_barrier();
-  for (int j0 = 0; j0 < nt; j0 += kIdxStages) {
+  for (int j0 = 0; j0 < nt; j0 += NS) {
     auto step = [&](auto S) {
-      const int j = j0 + S, jn = j + kIdxStages - 1;
+      const int j = j0 + S, jn = j + NS - 1;
       if (j >= nt) return false;
       asm volatile("" ::: "memory");
-      if (jn < nt) issue(wring + ((S + kIdxStages - 1) % kIdxStages) * kIdxStageBytes, jn);
-      wait_vmem_dyn(8 * min(kIdxStages - 1, nt - 1 - j));
+      if (jn < nt) issue(wring + ((S + NS - 1) % NS) * kIdxStageBytes, jn);
+      wait_vmem_dyn(8 * min(NS - 1, nt - 1 - j));
       compute(ring + S * kIdxStageBytes, j);
       return true;
     };
-    if (!unroll_while<0, kIdxStages>(step)) break;
+    if (!unroll_while<0, NS>(step)) break;
   }
   if (a.scores_only) return;                                // uniform: no histograms to add
   __syncthreads();
   uint32_t* gh = a.hist + (size_t)b * kBins;
-  for (int i = tid; i < kBins / 2; i += 64 * kIdxWaves) {
+  for (int i = tid; i < kBins / 2; i += 64 * NW) {
     const uint32_t c = hist2[i];
     if (c & 0xFFFFu) atomicAdd(&gh[2 * i], c & 0xFFFFu);
     if (c >> 16) atomicAdd(&gh[2 * i + 1], c >> 16);
@@ -271,6 +274,14 @@ __global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) 
     const uint32_t c = chist[tid];
     if (c) atomicAdd(&a.chist[(size_t)b * kCBins + tid], c);
   }
+}
+
+template <class V>
+__global__ __launch_bounds__(64 * kIdxWaves) void dsa_indexer_kernel(DsaArgs a) {
+  __shared__ __attribute__((aligned(16))) char ring[kIdxWaves * kIdxStages * kIdxStageBytes];
+  __shared__ uint32_t hist2[kBins / 2];                     // two 16-bit bin counts per word (<= 1024 per bin)
+  __shared__ uint32_t chist[kCBins];
+  indexer_item<V, kIdxWaves, kIdxStages>(a, blockIdx.x, blockIdx.y, ring, hist2, chist);
 }
 
 // ------------------------------------------------------------------------------------------------ select
@@ -318,9 +329,18 @@ __global__ __launch_bounds__(256) void dsa_scores_hist_kernel(DsaArgs a) {
   if (c) atomicAdd(&a.chist[(size_t)b * kCBins + tid], c);
 }
 
-__global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
-  __shared__ uint32_t cnt[kCBins], red[4], thr[2], b1s;
-  const int b = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
+// LDS of one select_scan item.
+struct ScanShared {
+  uint32_t cnt[kCBins], red[4], thr[2], b1s;
+};
+
+// One select_scan item: slice wg (positions [4096 wg, 4096 wg + 4096)) of request b, by 256 threads.
+__device__ __forceinline__ void select_scan_item(const DsaArgs& a, int wg, int b, ScanShared& sh) {
+  uint32_t* const cnt = sh.cnt;
+  uint32_t* const red = sh.red;
+  uint32_t* const thr = sh.thr;
+  uint32_t& b1s = sh.b1s;
+  const int tid = threadIdx.x;
   const int n = valid_len(a, b);
   const int base = wg * kScanWG;
   if (n <= kTopK || base >= n) {                   // whole workgroup: nothing of this slice is selected
@@ -376,6 +396,11 @@ __global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
     else if (bin == b1) { ek[o_eq] = key[i]; ep[o_eq] = p0 + i; ++o_eq; }
   }
   if (tid == 0) { a.gcnt[b * a.nb + wg] = (int)t_gt; a.ecnt[b * a.nb + wg] = (int)t_eq; }
+}
+
+__global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
+  __shared__ ScanShared sh;
+  select_scan_item(a, blockIdx.x, blockIdx.y, sh);
 }
 
 // LDS of the select: the second and third radix digits' histogram, the threshold bucket's candidates when there are
@@ -600,12 +625,17 @@ __global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
   if (tid == 0) a.cnt[b] = cnt;
 }
 
-// Zero-fills the per-request histograms before the indexer accumulates into them (when they are not in the head).
-__global__ __launch_bounds__(1024) void dsa_hist_zero_kernel(DsaArgs a) {
-  uint32_t* gh = a.hist + (size_t)blockIdx.x * kBins;
-  for (int i = threadIdx.x; i < kBins; i += 1024) gh[i] = 0;
-  if (threadIdx.x < kCBins) a.chist[(size_t)blockIdx.x * kCBins + threadIdx.x] = 0;
+// Zero-fills request b's histograms before the indexer accumulates into them (when they are not in the head), by NT
+// threads (NT >= kCBins).
+template <int NT>
+__device__ __forceinline__ void hist_zero_item(const DsaArgs& a, int b) {
+  static_assert(NT >= kCBins, "one coarse bin per thread");
+  uint32_t* gh = a.hist + (size_t)b * kBins;
+  for (int i = threadIdx.x; i < kBins; i += NT) gh[i] = 0;
+  if (threadIdx.x < kCBins) a.chist[(size_t)b * kCBins + threadIdx.x] = 0;
 }
+
+__global__ __launch_bounds__(1024) void dsa_hist_zero_kernel(DsaArgs a) { hist_zero_item<1024>(a, blockIdx.x); }
 
 // ------------------------------------------------------------------------------------------------ sparse MLA
 // Workgroup = (request b, block of 32 heads, chunk of 128 selected keys); 4 waves.  Wave w computes the share of
@@ -781,13 +811,11 @@ __device__ __forceinline__ void dsa_chunk_walk(char* __restrict__ st0, char* __r
   }
 }
 
+// One attention item = (request b, head block hb, chunk), item = (b * 4 + hb) * kNChunk + chunk, by 256 threads.
 template <class V>
-__global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
-  __shared__ __attribute__((aligned(16))) char st0[kLatStageBytes], st1[kLatStageBytes], st2[kLatStageBytes];
-  __shared__ __attribute__((aligned(16))) float sred[4 * kSSlot];
-  __shared__ int sidx[kChunk];
-  __shared__ SelectShared<kCandAttn> sel;
-  const int item = blockIdx.x;                  // (b * 4 + hb) * kNChunk + chunk
+__device__ __forceinline__ void attn_item(const DsaArgs& a, int item, char* __restrict__ st0,
+                                          char* __restrict__ st1, char* __restrict__ st2, float* __restrict__ sred,
+                                          int* __restrict__ sidx, SelectShared<kCandAttn>& sel) {
   const int chunk = item % kNChunk;
   const int hb = (item / kNChunk) % 4;
   const int b = item / (kNChunk * 4);
@@ -874,10 +902,18 @@ __global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
   }
 }
 
+template <class V>
+__global__ __launch_bounds__(256) void dsa_attn_kernel(DsaArgs a) {
+  __shared__ __attribute__((aligned(16))) char st0[kLatStageBytes], st1[kLatStageBytes], st2[kLatStageBytes];
+  __shared__ __attribute__((aligned(16))) float sred[4 * kSSlot];
+  __shared__ int sidx[kChunk];
+  __shared__ SelectShared<kCandAttn> sel;
+  attn_item<V>(a, blockIdx.x, st0, st1, st2, sred, sidx, sel);
+}
+
 // One workgroup (256 threads, 2 value dims each) per (b, head): LSE merge over the chunks; E is the output type.
 template <class E>
-__global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
-  const int bh = blockIdx.x;
+__device__ __forceinline__ void combine_item(const DsaArgs& a, int bh) {
   const int b = bh / kH, head = bh % kH, hb = head / 32, hr = head % 32;
   const int cnt = min(max(a.cnt[b], 0), kTopK);     // as in dsa_attn_kernel; cnt = 0 merges no chunk (NaN)
   const int nch = (cnt + kChunk - 1) / kChunk;
@@ -890,6 +926,143 @@ __global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
                       },
                       reinterpret_cast<E*>(a.out) + (size_t)bh * kDC);
 }
+
+template <class E>
+__global__ __launch_bounds__(256) void dsa_combine_kernel(DsaArgs a) {
+  combine_item<E>(a, blockIdx.x);
+}
+
+// ------------------------------------------------------------------------------------------------ single launch
+// The whole decode (indexer, select_scan, attention with its own selection, combine) in one launch of at most one
+// 256-thread workgroup per CU, every workgroup taking the items of each phase in turn (item = workgroup id, then
+// + grid size), with a grid barrier between phases.  The phases are the four-launch chain's item bodies, except the
+// indexer, which runs as 4 waves with 4-stage rings (the same arithmetic per position; the chain uses 8 waves with
+// 2-stage rings), so the outputs are bit-identical to vmk_dsa_decode's.
+// Grid barrier k: every workgroup makes its stores visible to the device (agent-scope release: every wave's stores
+// are complete at the workgroup barrier before it, then the L2 is written back), adds 1 to counter k, and waits
+// until the counter reaches the grid size, then acquires (L1 and L2 invalidated) before anyone reads what other
+// workgroups wrote.  The wait is bounded: after kSyncSpinLimit polls the workgroup sets the timeout flag and goes
+// on, and a set flag ends every other wait; the call then reports cnt[b] = -1 for every request, and so does every
+// later call on that workspace (the flag is sticky) until its head is zeroed again.  Counters return to zero within
+// the call: workgroup 0 clears counter k - 1 once barrier k is complete, and the last workgroup to finish clears the
+// last barrier's counter and the exit counter.
+constexpr int kSyncLine = 64;                    // uint32 per 256-byte counter line
+constexpr int kMaxSyncBarriers = 4;              // histogram zero-fill, indexer, select_scan, attention
+constexpr int kSyncExit = kMaxSyncBarriers;      // line of the exit counter
+constexpr int kSyncFlag = kMaxSyncBarriers + 1;  // line of the timeout flag
+constexpr uint32_t kSyncSpinLimit = 1u << 17;    // polls of about 1 us: a wait gives up after ~0.1-0.2 s
+constexpr int kFusedIdxWaves = 4, kFusedIdxStages = 4;
+
+// LDS of the single launch: one pool that every phase carves up in turn.
+constexpr int kFusedAttnSred = 3 * kLatStageBytes;
+constexpr int kFusedAttnSidx = kFusedAttnSred + 4 * kSSlot * 4;
+constexpr int kFusedAttnSel = kFusedAttnSidx + kChunk * 4;
+constexpr int kFusedAttnEnd = kFusedAttnSel + (int)sizeof(SelectShared<kCandAttn>);
+constexpr int kFusedIdxHist = kFusedIdxWaves * kFusedIdxStages * kIdxStageBytes;
+constexpr int kFusedIdxChist = kFusedIdxHist + kBins / 2 * 4;
+constexpr int kFusedIdxEnd = kFusedIdxChist + kCBins * 4;
+constexpr int kFusedPool = kFusedAttnEnd > kFusedIdxEnd ? kFusedAttnEnd : kFusedIdxEnd;
+static_assert(kFusedAttnSel % 16 == 0 && kFusedIdxHist % 16 == 0 && (int)sizeof(ScanShared) <= kFusedPool,
+              "pool layout");
+
+__device__ __forceinline__ uint32_t* sync_line(const DsaArgs& a, int k) { return a.sync + k * kSyncLine; }
+
+// Grid barrier k of the single launch (every thread of every workgroup calls it); *timed_out (LDS) becomes 1 when
+// this workgroup's wait gave up or saw the flag.
+__device__ __forceinline__ void grid_sync(const DsaArgs& a, int k, uint32_t nblocks, int* timed_out) {
+  __syncthreads();                                 // every wave's stores are complete (vmcnt(0) before s_barrier)
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    uint32_t* c = sync_line(a, k);
+    uint32_t* flag = sync_line(a, kSyncFlag);
+    __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int gave_up = 0;
+    uint32_t spins = 0;
+    while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nblocks) {
+      if ((spins & 31) == 31 && __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+        gave_up = 1;
+        break;
+      }
+      if (++spins >= kSyncSpinLimit) {
+        __hip_atomic_fetch_or(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        gave_up = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (!gave_up && k > 0 && blockIdx.x == 0)      // every workgroup has left barrier k - 1's wait
+      __hip_atomic_fetch_and(sync_line(a, k - 1), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (gave_up) *timed_out = 1;
+  }
+  __syncthreads();
+}
+
+template <class V>
+__global__ __launch_bounds__(256) void dsa_decode_single_kernel(DsaArgs a) {
+  __shared__ __attribute__((aligned(16))) char pool[kFusedPool];
+  __shared__ int timed_out;
+  typedef elem_t<V> E;
+  const uint32_t G = gridDim.x;
+  if (threadIdx.x == 0)
+    timed_out = __hip_atomic_load(sync_line(a, kSyncFlag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+  __syncthreads();
+  if (timed_out) {                                 // an earlier call's wait gave up: report it and do nothing
+    if (blockIdx.x == 0)
+      for (int b = threadIdx.x; b < a.B; b += 256) a.cnt[b] = -1;
+    return;
+  }
+  int k = 0;
+  if (a.L > kTopK) {
+    if (!a.hist_in_head) {
+      for (int it = blockIdx.x; it < a.B; it += G) hist_zero_item<256>(a, it);
+      grid_sync(a, k++, G, &timed_out);
+    }
+    const int nblk = (a.L + kIdxWG - 1) / kIdxWG;
+    for (int it = blockIdx.x; it < a.B * nblk; it += G) {
+      indexer_item<V, kFusedIdxWaves, kFusedIdxStages>(a, it % nblk, it / nblk, pool,
+                                                       reinterpret_cast<uint32_t*>(pool + kFusedIdxHist),
+                                                       reinterpret_cast<uint32_t*>(pool + kFusedIdxChist));
+      __syncthreads();
+    }
+    grid_sync(a, k++, G, &timed_out);
+    for (int it = blockIdx.x; it < a.B * a.nb; it += G) {
+      select_scan_item(a, it % a.nb, it / a.nb, *reinterpret_cast<ScanShared*>(pool));
+      __syncthreads();
+    }
+    grid_sync(a, k++, G, &timed_out);
+  }
+  for (int it = blockIdx.x; it < a.B * 4 * kNChunk; it += G) {
+    attn_item<V>(a, it, pool, pool + kLatStageBytes, pool + 2 * kLatStageBytes,
+                 reinterpret_cast<float*>(pool + kFusedAttnSred), reinterpret_cast<int*>(pool + kFusedAttnSidx),
+                 *reinterpret_cast<SelectShared<kCandAttn>*>(pool + kFusedAttnSel));
+    __syncthreads();
+  }
+  grid_sync(a, k++, G, &timed_out);
+  for (int it = blockIdx.x; it < a.B * kH; it += G) {
+    combine_item<E>(a, it);
+    __syncthreads();
+  }
+  // Exit: the last workgroup out clears the last barrier's counter and the exit counter.
+  if (threadIdx.x == 0) {
+    if (!timed_out) {
+      const uint32_t old =
+          __hip_atomic_fetch_add(sync_line(a, kSyncExit), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == G - 1) {
+        __hip_atomic_fetch_and(sync_line(a, k - 1), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_and(sync_line(a, kSyncExit), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (__hip_atomic_load(sync_line(a, kSyncFlag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) timed_out = 1;
+  }
+  __syncthreads();
+  if (timed_out)
+    for (int b = threadIdx.x; b < a.B; b += 256) a.cnt[b] = -1;
+}
+
+// The single-launch decode's grid-barrier block in the workspace head's counter part, past the coarse histograms
+// (B * 1 KB <= 64 KB when they live there): one 256-byte line per counter, then the timeout flag.
+constexpr size_t kSyncOffset = kWsCounters + ((size_t)1 << 20);
 
 struct DsaLayout {
   size_t hist, chist, scores, glist, ekey, epos, gcnt, ecnt, po, pml, total;
@@ -946,6 +1119,7 @@ static int dsa_fill_args(DsaArgs& a, const void* q, const void* kv, const void* 
   a.scores_only = 0;
   a.scores_in = nullptr;
   a.sl2 = (float)(1.0 / sqrt(192.0)) * kLog2e;
+  a.sync = (uint32_t*)(base + kSyncOffset);
   return 0;
 }
 
@@ -1078,6 +1252,72 @@ static int dsa_decode(const void* q, const void* kv, const void* iq, const void*
   hipStream_t s = (hipStream_t)stream;
   if (int rc = launch_index_select<V>(a, s, false)) return rc;
   return launch_attention<V>(a, s);
+}
+
+// Workgroups of the single launch on the stream's device: at most one round of co-resident workgroups (the
+// occupancy of its 256-thread, ~156 KB-LDS workgroup times the CU count, looked up once per device), and no more
+// than the largest phase has items.
+template <class V>
+static int single_grid(hipStream_t s, int64_t items, int* grid) {
+  constexpr int kDevs = 64;
+  static int cap[kDevs];
+  int dev = -1;
+  if (s) {
+    VMK_CHECK_HIP(hipStreamGetDevice(s, &dev));
+  } else {
+    VMK_CHECK_HIP(hipGetDevice(&dev));
+  }
+  VMK_CHECK(dev >= 0 && dev < kDevs, "device index beyond the single-launch table");
+  if (!cap[dev]) {
+    int cur = -1, per_cu = 0, cus = 0;
+    VMK_CHECK_HIP(hipGetDevice(&cur));
+    if (cur != dev) VMK_CHECK_HIP(hipSetDevice(dev));
+    const hipError_t e1 = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, reinterpret_cast<const void*>(dsa_decode_single_kernel<V>), 256, 0);
+    const hipError_t e2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (cur != dev) VMK_CHECK_HIP(hipSetDevice(cur));
+    VMK_CHECK_HIP(e1);
+    VMK_CHECK_HIP(e2);
+    VMK_CHECK(per_cu >= 1 && cus >= 1, "the single-launch kernel cannot be resident on this device");
+    cap[dev] = per_cu * cus;
+  }
+  *grid = (int)std::min<int64_t>(items, cap[dev]);
+  return 0;
+}
+
+template <class V>
+static int dsa_decode_single(const void* q, const void* kv, const void* iq, const void* ik, const void* w,
+                             const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L,
+                             void* workspace, size_t ws_bytes, void* stream) {
+  VMK_CHECK(q && kv && iq && ik && w && out && idx && cnt, "null pointer argument");
+  DSA_COMMON_CHECKS();
+  VMK_CHECK(aligned16(q) && aligned16(kv) && aligned16(iq) && aligned16(ik), "tensors must be 16-byte aligned");
+  VMK_CHECK(L <= kMaxAttnL, "sparse attention needs L * 1152 bytes < 2 GiB per request (L <= 1864134)");
+  DsaArgs a;
+  dsa_fill_args(a, q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace);
+  a.fused_select = 1;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t nblk = (L + kIdxWG - 1) / kIdxWG;
+  const int64_t items = std::max<int64_t>(L > kTopK ? B * nblk : 0, B * (int64_t)kH);
+  int grid = 0;
+  if (int rc = single_grid<V>(s, items, &grid)) return rc;
+  prof_before(kKDsaSingle, s);
+  hipLaunchKernelGGL(dsa_decode_single_kernel<V>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  prof_after(kKDsaSingle, s);
+  VMK_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
+extern "C" int vmk_dsa_decode_single(const void* q, const void* kv, const void* iq, const void* ik, const void* w,
+                                     const void* lens, void* out, void* idx, void* cnt, int64_t B, int64_t L,
+                                     void* workspace, size_t ws_bytes, void* stream) {
+  return dsa_decode_single<half8>(q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace, ws_bytes, stream);
+}
+
+extern "C" int vmk_dsa_decode_single_bf16(const void* q, const void* kv, const void* iq, const void* ik,
+                                          const void* w, const void* lens, void* out, void* idx, void* cnt,
+                                          int64_t B, int64_t L, void* workspace, size_t ws_bytes, void* stream) {
+  return dsa_decode_single<bf16x8>(q, kv, iq, ik, w, lens, out, idx, cnt, B, L, workspace, ws_bytes, stream);
 }
 
 extern "C" int vmk_dsa_indexer(const void* iq, const void* ik, const void* w, const void* lens, void* scores, int64_t B,

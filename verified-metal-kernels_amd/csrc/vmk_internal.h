@@ -11,7 +11,7 @@ void set_error(const char* fmt, ...);
 enum KernelId {
   kKSpecPartial = 0, kKSpecCombine = 1, kKPrefixPartial = 2, kKPrefixCombine = 3,
   kKDsaIndexer = 4, kKDsaSelect = 5, kKDsaAttn = 6, kKDsaCombine = 7, kKDsaSelectScan = 8,
-  kKDsaProjectQ = 9,
+  kKDsaProjectQ = 9, kKDsaSingle = 10,
 };
 void prof_before(int kernel_id, hipStream_t s);
 void prof_after(int kernel_id, hipStream_t s);

@@ -489,9 +489,11 @@ def dsa_sparse_mla(q, kv, idx, cnt, out=None):
     return out
 
 
-def dsa_decode(q, kv, iq, ik, w, lens=None, out=None, idx=None, cnt=None):
+def dsa_decode(q, kv, iq, ik, w, lens=None, out=None, idx=None, cnt=None, single=False):
     """Full DSA decode step (indexer -> top-2048 -> sparse MLA); q, kv, iq, ik all fp16 or all bf16, w fp32.
-    Returns out (B,128,512) of q's dtype; the selected indices land in `idx`/`cnt` when given."""
+    Returns out (B,128,512) of q's dtype; the selected indices land in `idx`/`cnt` when given.  single=True runs
+    the step as one kernel launch (vmk_dsa_decode_single: the same outputs bit for bit; a grid-barrier wait that
+    gave up shows as cnt = -1)."""
     dt, sfx = _elem(q)
     B, L = _dsa_indexer_shapes(iq, ik, w, lens)
     if _dsa_attention_shapes(q, kv, B) != L:
@@ -513,7 +515,8 @@ def dsa_decode(q, kv, iq, ik, w, lens=None, out=None, idx=None, cnt=None):
         idx = torch.empty(B, DSA_TOPK, dtype=torch.int32, device=q.device)
         cnt = torch.empty(B, dtype=torch.int32, device=q.device)
     ws = workspace(lib.load().vmk_dsa_workspace_size(B, L), q.device)
-    _launch("vmk_dsa_decode" + sfx, ws, q.data_ptr(), kv.data_ptr(), iq.data_ptr(), ik.data_ptr(), w.data_ptr(),
+    _launch("vmk_dsa_decode" + ("_single" if single else "") + sfx, ws, q.data_ptr(), kv.data_ptr(), iq.data_ptr(),
+            ik.data_ptr(), w.data_ptr(),
             0 if lens is None else lens.data_ptr(), out.data_ptr(), idx.data_ptr(), cnt.data_ptr(), B, L,
             ws.data_ptr(), ws.numel(), _stream(q))
     return out

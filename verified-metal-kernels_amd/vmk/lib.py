@@ -52,6 +52,8 @@ _SIGS = {
     "vmk_dsa_topk": [_c_vp] * 4 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_sparse_mla": [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_decode": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_decode_single": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
+    "vmk_dsa_decode_single_bf16": [_c_vp] * 9 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
     "vmk_dsa_project_workspace_size": [_c_i64],
     # x, pos, rope_cos, rope_sin, rope_rows, &weights (host struct), q, iq, w, kv, ik, B, L, workspace, bytes, stream
     "vmk_dsa_project": [_c_vp] * 4 + [_c_i64, _c_vp] + [_c_vp] * 5 + [_c_i64] * 2 + [_c_vp, _c_sz, _c_vp],
@@ -104,7 +106,7 @@ def load():
 # Kernel ids of vmk_profile_next (include/vmk.h).
 KERNEL_IDS = {"spec_partial": 0, "spec_combine": 1, "prefix_partial": 2, "prefix_combine": 3,
               "dsa_indexer": 4, "dsa_select": 5, "dsa_attn": 6, "dsa_combine": 7,
-              "dsa_select_scan": 8, "dsa_project_q": 9}
+              "dsa_select_scan": 8, "dsa_project_q": 9, "dsa_single": 10}
 
 
 def exported_symbols():
