@@ -569,18 +569,20 @@ __device__ __forceinline__ void state_to_slot(char* slot, const RowState& st, in
   reinterpret_cast<float2*>(slot + 64 * 64 * 4)[lane] = float2{st.m, st.l};
 }
 
-// Writes one wave's partial (unnormalised O, running max m, row sum l) for its 32 rows:
-//   po[row][d] (row stride 128 floats), pml[row] = (m, l).  Rows >= nvalid are skipped.
-__device__ __forceinline__ void store_partial(float* po, float* pml, const RowState& st, int lane, int nvalid) {
+// Writes one wave's partial for its 32 rows: po[row][d] = O / l in the partial type PT (row stride 128),
+// pml[row] = (m, l).  Rows >= nvalid are skipped.
+template <class PT>
+__device__ __forceinline__ void store_partial(PT* po, float* pml, const RowState& st, int lane, int nvalid) {
   const int r = lane & 31, g = lane >> 5;
   const float ltot = st.l + xor32(st.l);
   if (r >= nvalid) return;
+  const float inv = part_inv(ltot);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
       floatx4 v = floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]};
-      *reinterpret_cast<floatx4*>(po + r * 128 + dt * 32 + 8 * blk + 4 * g) = v;
+      store_part4(po + r * 128 + dt * 32 + 8 * blk + 4 * g, v * inv);
     }
   if (g == 0) {
     pml[2 * r] = st.m;
@@ -598,9 +600,9 @@ constexpr int kAttnSmemBytes = 8 * kStageBytes;
 constexpr int kAttnSlotsEnd = 4 * kSlotBytes;
 static_assert(kAttnSlotsEnd <= kAttnSmemBytes, "merge slots must fit in the stage memory");
 
-template <int WR, int WK, int NSW = 2, class V = half8, class Src, class QRow>
+template <int WR, int WK, int NSW = 2, class V = half8, class Src, class QRow, class PT>
 __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow, int nrows, int kbeg, int ntiles,
-                                          float* po, float* pml) {
+                                          PT* po, float* pml) {
   static_assert(WR * WK == 4 && WR * WK * NSW <= 8, "four waves, rings within the stage memory");
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wr = wave % WR, wk = wave / WR;
@@ -614,7 +616,7 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
   const TileLanes tl = tile_lanes(lane, ring_off);
   wave_walk<NSW>(st, qb, smem + ring_off, smem, tl, src, kbeg, wk, ntiles, WK, lane);
   const int nvalid = nrows - wr * 32;
-  float* pob = po + (size_t)wr * 32 * 128;
+  PT* pob = po + (size_t)wr * 32 * 128;
   float* pmlb = pml + wr * 32 * 2;
   if constexpr (WK == 1) {
     store_partial(pob, pmlb, st, lane, nvalid);
@@ -636,6 +638,8 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
       ak[k] = fast_exp2(mk[k] - muse);
       l += ak[k] * reinterpret_cast<const float2*>(smem + (k * WR + wr) * kSlotBytes + 64 * 64 * 4)[lane].y;
     }
+    const float ltot = l + xor32(l);
+    const float inv = part_inv(ltot);
 #pragma unroll
     for (int j = 0; j < 4 / WK; ++j) {
       const int dt = wk + j * WK;
@@ -650,10 +654,8 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
       }
       if (r < nvalid)
 #pragma unroll
-        for (int blk = 0; blk < 4; ++blk)
-          *reinterpret_cast<floatx4*>(pob + r * 128 + dt * 32 + 8 * blk + 4 * g) = acc[blk];
+        for (int blk = 0; blk < 4; ++blk) store_part4(pob + r * 128 + dt * 32 + 8 * blk + 4 * g, acc[blk] * inv);
     }
-    const float ltot = l + xor32(l);
     if (wk == 0 && g == 0 && r < nvalid) {
       pmlb[2 * r] = M;
       pmlb[2 * r + 1] = ltot;
@@ -662,7 +664,8 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
 }
 
 // ---- log-sum-exp merge of the partials of one output row, NT threads, PER head-dims per thread (d = tid + k*NT).
-// part(i, ml, o) sets ml -> (m, l) and o -> the partial's O row of partial i (0 <= i < nparts).  The m/l of a batch
+// part(i, ml, o) sets ml -> (m, l) and o -> the partial's normalised O row (type PT) of partial i (0 <= i < nparts).
+// Partial i weighs w_i = exp2(m_i - M) * l_i, M the largest m: out = sum_i w_i O_i / sum_i w_i.  The m/l of a batch
 // of NT partials are fetched in parallel and their weights shared through LDS, so that the O loads of the
 // accumulation loop are independent of each other and can all be in flight together.
 //
@@ -671,23 +674,23 @@ __device__ __forceinline__ void attend_wg(char* smem, const Src& src, QRow qrow,
 // (slots past nparts reload the last partial, never used) so that they issue back to back; nparts >= 1 here, which
 // combine_row guarantees.  Both forms add the same terms in the same order (partial 0 first), so they give the same
 // bits.
-template <int NT, int PER, int H, class Part, class E>
+template <int NT, int PER, int H, class PT, class Part, class E>
 __device__ __forceinline__ void combine_row_held(int nparts, Part part, E* out) {
-  __shared__ float sw[H], sl[H], red[NT / 64];
+  __shared__ float sw[H], red[NT / 64];
   const int tid = threadIdx.x;
   float ov[H][PER];
 #pragma unroll
   for (int j = 0; j < H; ++j) {
     const float* ml;
-    const float* o;
+    const PT* o;
     part(min(j, nparts - 1), ml, o);
 #pragma unroll
-    for (int k = 0; k < PER; ++k) ov[j][k] = o[tid + k * NT];
+    for (int k = 0; k < PER; ++k) ov[j][k] = (float)o[tid + k * NT];
   }
   float m0 = kNegInf, l0 = 0.f;
   if (tid < nparts) {
     const float* ml;
-    const float* o;
+    const PT* o;
     part(tid, ml, o);
     m0 = ml[0];
     l0 = ml[1];
@@ -701,11 +704,7 @@ __device__ __forceinline__ void combine_row_held(int nparts, Part part, E* out) 
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) M = fmaxf(M, red[w]);
   const float Muse = (M == kNegInf) ? 0.f : M;
-  if (tid < nparts) {
-    const float w = fast_exp2(m0 - Muse);
-    sw[tid] = w;
-    sl[tid] = w * l0;
-  }
+  if (tid < nparts) sw[tid] = fast_exp2(m0 - Muse) * l0;
   __syncthreads();
   float num[PER], den = 0.f;
 #pragma unroll
@@ -714,7 +713,7 @@ __device__ __forceinline__ void combine_row_held(int nparts, Part part, E* out) 
   for (int j = 0; j < H; ++j) {
     if (j < nparts) {                                  // uniform
       const float w = sw[j];
-      den += sl[j];
+      den += w;
 #pragma unroll
       for (int k = 0; k < PER; ++k) num[k] += w * ov[j][k];
     }
@@ -723,7 +722,7 @@ __device__ __forceinline__ void combine_row_held(int nparts, Part part, E* out) 
   for (int k = 0; k < PER; ++k) out[tid + k * NT] = (E)(num[k] / den);
 }
 
-template <int NT, int PER, class Part, class E>
+template <int NT, int PER, class PT, class Part, class E>
 __device__ __forceinline__ void combine_row(int nparts, Part part, E* out) {
   static_assert(NT >= 32, "one thread per held partial's m/l");
   if (nparts <= 0) {                                 // uniform: no partial to merge, and none is read
@@ -732,16 +731,16 @@ __device__ __forceinline__ void combine_row(int nparts, Part part, E* out) {
     for (int k = 0; k < PER; ++k) out[threadIdx.x + k * NT] = (E)__builtin_nanf("");
     return;
   }
-  if (nparts <= 8) return combine_row_held<NT, PER, 8>(nparts, part, out);
-  if (nparts <= 16) return combine_row_held<NT, PER, 16>(nparts, part, out);
-  if (nparts <= 32) return combine_row_held<NT, PER, 32>(nparts, part, out);
-  __shared__ float sw[NT], sl[NT], red[NT / 64];
+  if (nparts <= 8) return combine_row_held<NT, PER, 8, PT>(nparts, part, out);
+  if (nparts <= 16) return combine_row_held<NT, PER, 16, PT>(nparts, part, out);
+  if (nparts <= 32) return combine_row_held<NT, PER, 32, PT>(nparts, part, out);
+  __shared__ float sw[NT], red[NT / 64];
   const int tid = threadIdx.x;
   float M = kNegInf;
   for (int b0 = 0; b0 < nparts; b0 += NT) {
     if (b0 + tid < nparts) {
       const float* ml;
-      const float* o;
+      const PT* o;
       part(b0 + tid, ml, o);
       M = fmaxf(M, ml[0]);
     }
@@ -762,22 +761,20 @@ __device__ __forceinline__ void combine_row(int nparts, Part part, E* out) {
     __syncthreads();
     if (tid < n) {
       const float* ml;
-      const float* o;
+      const PT* o;
       part(b0 + tid, ml, o);
-      const float w = fast_exp2(ml[0] - Muse);
-      sw[tid] = w;
-      sl[tid] = w * ml[1];
+      sw[tid] = fast_exp2(ml[0] - Muse) * ml[1];
     }
     __syncthreads();
 #pragma unroll 8
     for (int j = 0; j < n; ++j) {
       const float* ml;
-      const float* o;
+      const PT* o;
       part(b0 + j, ml, o);
       const float w = sw[j];
-      den += sl[j];
+      den += w;
 #pragma unroll
-      for (int k = 0; k < PER; ++k) num[k] += w * o[tid + k * NT];
+      for (int k = 0; k < PER; ++k) num[k] += w * (float)o[tid + k * NT];
     }
   }
 #pragma unroll
@@ -794,35 +791,38 @@ constexpr int kRowsStages = 8;
 constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
 
 // The row-split workgroup's partial (NW waves x 32 rows), written through LDS so that every store instruction
-// writes two whole rows (1 KB contiguous) instead of 32-byte pieces of 32 rows.  Each wave parks its O^T registers
-// in its own 16 KB of LDS as 32 rows of 128 floats, the 16-byte chunk c of row r at chunk position (c + r) mod 32
-// (at most two lanes per bank group on the writes, none on the row reads), then stores rows 2i, 2i + 1 per
-// instruction.  Called by every wave of the workgroup (it contains a barrier); rows >= nvalid are not written.
-__device__ __forceinline__ void store_partial_rows(char* smem, float* po, float* pml, const RowState& st, int wave,
+// writes two whole rows (contiguous) instead of pieces of 32 rows.  Each wave parks its O^T registers, normalised by
+// its rows' l, in its own 16 KB of LDS as 32 rows of 128 floats, the 16-byte chunk c of row r at chunk position
+// (c + r) mod 32 (at most two lanes per bank group on the writes, none on the row reads), then stores rows 2i,
+// 2i + 1 per instruction in the partial type PT.  Called by every wave of the workgroup (it contains a barrier);
+// rows >= nvalid are not written.
+template <class PT>
+__device__ __forceinline__ void store_partial_rows(char* smem, PT* po, float* pml, const RowState& st, int wave,
                                                    int lane, int nvalid) {
   __syncthreads();                                          // every wave is done with the ring
   float* lds = reinterpret_cast<float*>(smem) + wave * 32 * 128;
   const int r = lane & 31, g = lane >> 5;
+  const float ltot = st.l + xor32(st.l);
+  const float inv = part_inv(ltot);                         // the lane's row r, normalised before the transpose
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
       *reinterpret_cast<floatx4*>(lds + r * 128 + (((dt * 8 + 2 * blk + g) + r) & 31) * 4) =
-          floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]};
-  const float ltot = st.l + xor32(st.l);
+          floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]} * inv;
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");       // the wave reads back only its own rows
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int row = 2 * i + g;
     const floatx4 v = *reinterpret_cast<const floatx4*>(lds + row * 128 + ((r + row) & 31) * 4);
-    if (row < nvalid) *reinterpret_cast<floatx4*>(po + row * 128 + r * 4) = v;
+    if (row < nvalid) store_part4(po + row * 128 + r * 4, v);
   }
   if (g == 0 && r < nvalid) *reinterpret_cast<float2*>(pml + 2 * r) = float2{st.m, ltot};
 }
 
-template <int NW, class V = half8, class Src, class QRow>
+template <int NW, class V = half8, class Src, class QRow, class PT>
 __device__ __forceinline__ void attend_wg_rows(char* smem, const Src& src, QRow qrow, int nrows, int kbeg,
-                                               int ntiles, float* po, float* pml) {
+                                               int ntiles, PT* po, float* pml) {
   static_assert(16 % NW == 0, "the 16 DMA instructions of a tile must split evenly over the waves");
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row = wave * 32 + (lane & 31);

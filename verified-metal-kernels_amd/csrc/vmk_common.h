@@ -40,6 +40,29 @@ template <> struct ElemOf<half8> { typedef f16 type; };
 template <> struct ElemOf<bf16x8> { typedef bf16 type; };
 template <class V> using elem_t = typename ElemOf<V>::type;
 
+// Storage type of a split partial's row-normalised O (O / l), keyed by the input element type: fp16 for fp16 inputs
+// (a normalised row is a convex combination of value rows, so |O / l| <= max |v| <= 65504 fits, and its rounding
+// is that of one more fp16 result), fp32 for bf16 inputs (whose values can exceed fp16's range).
+template <class E> struct PartOf { typedef float type; };
+template <> struct PartOf<f16> { typedef f16 type; };
+template <class E> using part_t = typename PartOf<E>::type;
+
+// Four floats stored as one piece of a partial row (16 bytes of fp32 or 8 bytes of fp16), and two of them read back.
+__device__ __forceinline__ void store_part4(float* p, floatx4 v) { *reinterpret_cast<floatx4*>(p) = v; }
+__device__ __forceinline__ void store_part4(f16* p, floatx4 v) {
+  *reinterpret_cast<half4*>(p) = half4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+}
+__device__ __forceinline__ float2 load_part2(const float* p) { return *reinterpret_cast<const float2*>(p); }
+__device__ __forceinline__ float2 load_part2(const f16* p) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 v = *reinterpret_cast<const h2*>(p);
+  return float2{(float)v[0], (float)v[1]};
+}
+
+// 1 / l of a partial row, or 0 when the row saw no key (l = 0, O = 0): its normalised O is then 0, not 0/0.  A NaN
+// l gives NaN, which the merge carries into the output.
+__device__ __forceinline__ float part_inv(float l) { return l == 0.f ? 0.f : 1.f / l; }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Value of lane l ^ 32.  v_permlane32_swap exchanges the upper half of its first operand with the lower half of

@@ -42,7 +42,7 @@ struct DsaArgs {
   f16* out;             // (B, 128, 512)
   uint32_t* hist;       // (B, 8192)
   float* scores;        // (B, Ls)
-  float* po;            // (B, 4, kNChunk, 32, 512)
+  void* po;             // (B, 4, kNChunk, 32, 512) normalised O of type part_t
   float* pml;           // (B, 4, kNChunk, 32, 2)
   int* glist;           // (B, L) per scan slice: positions above the threshold bucket, in position order
   uint32_t* ekey;       // (B, L) per scan slice: keys of the threshold bucket's positions, in position order
@@ -874,11 +874,12 @@ __device__ __forceinline__ void attn_item(const DsaArgs& a, int item, char* __re
   RowState st;
   row_state_init(st);
   dsa_chunk_walk(st0, st1, st2, sred, st, qb, rows, sidx, kbeg, kend, ntiles, drow, dchk, a.sl2, lane, w);
-  // Partial: O[head][128w + d'] for this wave's value dims; m and l are identical in all waves.  The wave's 32 x 128
-  // block goes through LDS (stages 0 and 1 are free once every wave is past its last tile), row r's 16-byte chunk c
-  // at position (c + r) & 31, so that every store instruction writes two whole 512-byte pieces of rows instead of
-  // 32-byte pieces of 32 rows.
+  // Partial: O[head][128w + d'] / l for this wave's value dims, in the partial type; m and l are identical in all
+  // waves.  The wave's 32 x 128 block goes through LDS (stages 0 and 1 are free once every wave is past its last
+  // tile), row r's 16-byte chunk c at position (c + r) & 31, so that every store instruction writes two whole pieces
+  // of rows instead of pieces of 32 rows.
   const float ltot = st.l + xor32(st.l);
+  const float inv = part_inv(ltot);
   __syncthreads();
   float* lds = reinterpret_cast<float*>(w < 2 ? st0 : st1) + (w & 1) * 32 * 128;
   static_assert(2 * 32 * 128 * 4 <= kLatStageBytes, "two waves' blocks per stage");
@@ -887,14 +888,13 @@ __device__ __forceinline__ void attn_item(const DsaArgs& a, int item, char* __re
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
       *reinterpret_cast<floatx4*>(lds + r * 128 + (((dt * 8 + 2 * blk + g) + r) & 31) * 4) =
-          floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]};
+          floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]} * inv;
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");       // the wave reads back only its own block
-  float* po = a.po + (size_t)item * 32 * kDC + 128 * w;
+  part_t<elem_t<V>>* po = reinterpret_cast<part_t<elem_t<V>>*>(a.po) + (size_t)item * 32 * kDC + 128 * w;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int row = 2 * i + g;
-    *reinterpret_cast<floatx4*>(po + row * kDC + r * 4) =
-        *reinterpret_cast<const floatx4*>(lds + row * 128 + ((r + row) & 31) * 4);
+    store_part4(po + row * kDC + r * 4, *reinterpret_cast<const floatx4*>(lds + row * 128 + ((r + row) & 31) * 4));
   }
   if (w == 0 && g == 0) {
     a.pml[((size_t)item * 32 + r) * 2] = st.m;
@@ -918,13 +918,14 @@ __device__ __forceinline__ void combine_item(const DsaArgs& a, int bh) {
   const int cnt = min(max(a.cnt[b], 0), kTopK);     // as in dsa_attn_kernel; cnt = 0 merges no chunk (NaN)
   const int nch = (cnt + kChunk - 1) / kChunk;
   const size_t item0 = ((size_t)b * 4 + hb) * kNChunk;
-  combine_row<256, 2>(nch,
-                      [&](int c, const float*& ml, const float*& o) {
-                        const size_t base = (item0 + c) * 32 + hr;
-                        ml = a.pml + base * 2;
-                        o = a.po + base * kDC;
-                      },
-                      reinterpret_cast<E*>(a.out) + (size_t)bh * kDC);
+  typedef part_t<E> PT;
+  combine_row<256, 2, PT>(nch,
+                          [&](int c, const float*& ml, const PT*& o) {
+                            const size_t base = (item0 + c) * 32 + hr;
+                            ml = a.pml + base * 2;
+                            o = reinterpret_cast<const PT*>(a.po) + base * kDC;
+                          },
+                          reinterpret_cast<E*>(a.out) + (size_t)bh * kDC);
 }
 
 template <class E>
@@ -1109,7 +1110,7 @@ static int dsa_fill_args(DsaArgs& a, const void* q, const void* kv, const void* 
   a.epos = (int*)(base + lay.epos);
   a.gcnt = (int*)(base + lay.gcnt);
   a.ecnt = (int*)(base + lay.ecnt);
-  a.po = (float*)(base + lay.po);
+  a.po = base + lay.po;                              // sized for fp32 rows; fp16 partials use the first half
   a.pml = (float*)(base + lay.pml);
   a.B = (int)B; a.L = (int)L;
   a.nb = (int)((L + kScanWG - 1) / kScanWG);

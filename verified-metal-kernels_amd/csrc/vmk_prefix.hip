@@ -31,9 +31,9 @@ struct PrefixArgs {
   int ps, max_sp, num_pages;
   const int* slens;        // (N,) or null
   f16* out;                // (N, Hq, 128)
-  float* po_p;             // prefix partials [h][rb][split][32*WRp][128]
+  void* po_p;              // prefix partials [h][rb][split][32*WRp][128], normalised O of type part_t
   float* pml_p;
-  float* po_s;             // suffix partials [n][h][split][32][128]
+  void* po_s;              // suffix partials [n][h][split][32][128]
   float* pml_s;
   int N, Hq, Hkv, G, P, S;
   int WRp, nrb_p, nsplit_p, chunk_p;   // prefix plan
@@ -77,16 +77,23 @@ __device__ __forceinline__ int suffix_len(const PrefixArgs& a, int n) {
   return a.slens ? min(max(a.slens[n], 0), a.S) : a.S;
 }
 
-// LDS offset of a fused suffix item's partial: past attend_wg's cross-wave merge slots.
+// LDS offset of a fused suffix item's partial: past attend_wg's cross-wave merge slots; its (m, l) pairs follow 16 KB
+// further (room for 32 rows of 128 floats).
 constexpr int kFuseOff = kAttnSlotsEnd;
-static_assert(kFuseOff + (32 * 128 + 64) * 4 <= kAttnSmemBytes, "fused partial must fit in the stage memory");
+constexpr int kFuseMlOff = kFuseOff + 32 * 128 * 4;
+static_assert(kFuseMlOff + 64 * 4 <= kAttnSmemBytes, "fused partial must fit in the stage memory");
 
-// Final output of request n's G rows of KV head h: log-sum-exp merge of the suffix partial (LDS: lpo rows of 128
-// floats, lpml (m, l) pairs) with the prefix partials of those rows.  One wave per row, two head-dims per lane.
+template <class PT> __device__ __forceinline__ const PT* prefix_po(const PrefixArgs& a) {
+  return reinterpret_cast<const PT*>(a.po_p);
+}
+
+// Final output of request n's G rows of KV head h: log-sum-exp merge of the suffix partial (lpo: normalised rows of
+// 128, lpml (m, l) pairs) with the prefix partials of those rows, each weighted exp2(m - M) * l.  One wave per row, two head-dims per lane.
 // Lane s holds the (m, l) of prefix partial b0 + s; the O rows are fetched 16 partials at a time with independent
 // loads (one memory round trip per 16), weighted with the lane-broadcast weights.
 template <class E>
-__device__ void merge_prefix_rows(const PrefixArgs& a, const float* lpo, const float* lpml, int n, int h) {
+__device__ void merge_prefix_rows(const PrefixArgs& a, const part_t<E>* lpo, const float* lpml, int n, int h) {
+  typedef part_t<E> PT;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int np = a.P > 0 ? a.nsplit_p : 0;
   const int rows_p = 32 * a.WRp;
@@ -99,17 +106,17 @@ __device__ void merge_prefix_rows(const PrefixArgs& a, const float* lpo, const f
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
     const float Mu = (M == kNegInf) ? 0.f : M;
-    const float ws = fast_exp2(ms - Mu);
+    const float ws = fast_exp2(ms - Mu) * ls;              // weights exp2(m - M) * l of the normalised partials
     float den = 0.f;                                       // this lane's share of the prefix denominators
-    float2 num = *reinterpret_cast<const float2*>(lpo + gg * 128 + 2 * lane);
+    float2 num = load_part2(lpo + gg * 128 + 2 * lane);
     num.x *= ws;
     num.y *= ws;
     for (int b0 = 0; b0 < np; b0 += 64) {
       float w = 0.f;
       if (b0 + lane < np) {
         const float2 ml = *reinterpret_cast<const float2*>(a.pml_p + (pbase + (size_t)(b0 + lane) * rows_p) * 2);
-        w = fast_exp2(ml.x - Mu);
-        den += w * ml.y;
+        w = fast_exp2(ml.x - Mu) * ml.y;
+        den += w;
       }
       const int nb = min(64, np - b0);
       for (int j0 = 0; j0 < nb; j0 += 16) {
@@ -117,7 +124,7 @@ __device__ void merge_prefix_rows(const PrefixArgs& a, const float* lpo, const f
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
           const int j = b0 + min(j0 + k, nb - 1);          // clamped: in bounds; weight 0 past nb
-          v[k] = *reinterpret_cast<const float2*>(a.po_p + (pbase + (size_t)j * rows_p) * 128 + 2 * lane);
+          v[k] = load_part2(prefix_po<PT>(a) + (pbase + (size_t)j * rows_p) * 128 + 2 * lane);
         }
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -130,7 +137,7 @@ __device__ void merge_prefix_rows(const PrefixArgs& a, const float* lpo, const f
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
-    den += ws * ls;
+    den += ws;
     E* out = reinterpret_cast<E*>(a.out) + ((size_t)n * a.Hq + h * a.G + gg) * 128 + 2 * lane;
     out[0] = (E)(num.x / den);
     out[1] = (E)(num.y / den);
@@ -146,6 +153,7 @@ struct PrefixRow {
   float2 v[kPrefetchSplits];
 };
 
+template <class PT>
 __device__ __forceinline__ void prefetch_prefix_row(const PrefixArgs& a, PrefixRow& pr, int n, int h, int gg,
                                                     int lane) {
   const int np = a.nsplit_p, rows_p = 32 * a.WRp;
@@ -154,21 +162,21 @@ __device__ __forceinline__ void prefetch_prefix_row(const PrefixArgs& a, PrefixR
   pr.ml = *reinterpret_cast<const float2*>(a.pml_p + (pbase + (size_t)min(lane, np - 1) * rows_p) * 2);
 #pragma unroll
   for (int j = 0; j < kPrefetchSplits; ++j)
-    pr.v[j] = *reinterpret_cast<const float2*>(a.po_p + (pbase + (size_t)min(j, np - 1) * rows_p) * 128 + 2 * lane);
+    pr.v[j] = load_part2(prefix_po<PT>(a) + (pbase + (size_t)min(j, np - 1) * rows_p) * 128 + 2 * lane);
 }
 
 // Final output of row gg of request n, KV head h, from the suffix partial in LDS and the prefetched prefix row.
 template <class E>
-__device__ __forceinline__ void merge_prefetched_row(const PrefixArgs& a, const PrefixRow& pr, const float* lpo,
+__device__ __forceinline__ void merge_prefetched_row(const PrefixArgs& a, const PrefixRow& pr, const part_t<E>* lpo,
                                                      const float* lpml, int n, int h, int gg, int lane) {
   const int np = a.nsplit_p;
   const float ms = lpml[2 * gg], ls = lpml[2 * gg + 1];
   const float M = wave_max(lane < np ? fmaxf(ms, pr.ml.x) : ms);
   const float Mu = (M == kNegInf) ? 0.f : M;
-  const float ws = fast_exp2(ms - Mu);
-  const float w = lane < np ? fast_exp2(pr.ml.x - Mu) : 0.f;
-  float den = w * pr.ml.y;
-  float2 num = *reinterpret_cast<const float2*>(lpo + gg * 128 + 2 * lane);
+  const float ws = fast_exp2(ms - Mu) * ls;                // weights exp2(m - M) * l of the normalised partials
+  const float w = lane < np ? fast_exp2(pr.ml.x - Mu) * pr.ml.y : 0.f;
+  float den = w;
+  float2 num = load_part2(lpo + gg * 128 + 2 * lane);
   num.x *= ws;
   num.y *= ws;
 #pragma unroll
@@ -177,7 +185,7 @@ __device__ __forceinline__ void merge_prefetched_row(const PrefixArgs& a, const 
     num.x += wj * pr.v[j].x;
     num.y += wj * pr.v[j].y;
   }
-  den = wave_sum(den) + ws * ls;
+  den = wave_sum(den) + ws;
   E* out = reinterpret_cast<E*>(a.out) + ((size_t)n * a.Hq + h * a.G + gg) * 128 + 2 * lane;
   out[0] = (E)(num.x / den);
   out[1] = (E)(num.y / den);
@@ -189,18 +197,20 @@ __device__ __forceinline__ void suffix_walk(const PrefixArgs& a, char* smem, con
                                             int split, int kbeg) {
   const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
   auto qrow = [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; };
+  typedef part_t<elem_t<V>> PT;
   if (!a.fuse) {
     const size_t pi = (size_t)nh * a.nsplit_s + split;
-    attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, a.po_s + pi * 32 * 128, a.pml_s + pi * 32 * 2);
+    attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, reinterpret_cast<PT*>(a.po_s) + pi * 32 * 128,
+                          a.pml_s + pi * 32 * 2);
     return;
   }
   // Whole suffix: keep the partial in LDS (past the merge slots) and merge it with the prefix partials here.
-  float* lpo = reinterpret_cast<float*>(smem + kFuseOff);
-  float* lpml = lpo + 32 * 128;
+  PT* lpo = reinterpret_cast<PT*>(smem + kFuseOff);
+  float* lpml = reinterpret_cast<float*>(smem + kFuseMlOff);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (a.G <= 4 && a.nsplit_p <= kPrefetchSplits) {          // wave w finishes row w
     PrefixRow pr;
-    if (wave < a.G) prefetch_prefix_row(a, pr, n, h, wave, lane);
+    if (wave < a.G) prefetch_prefix_row<PT>(a, pr, n, h, wave, lane);
     attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
     __syncthreads();
     if (wave < a.G) merge_prefetched_row<elem_t<V>>(a, pr, lpo, lpml, n, h, wave, lane);
@@ -303,7 +313,8 @@ __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem
                          const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
                          return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
                        },
-                       a.N * a.G - row0, kbeg, ntiles, a.po_p + (size_t)item * rows_wg * 128,
+                       a.N * a.G - row0, kbeg, ntiles,
+                       reinterpret_cast<part_t<elem_t<V>>*>(a.po_p) + (size_t)item * rows_wg * 128,
                        a.pml_p + (size_t)item * rows_wg * 2);
   };
   if constexpr (kPaged != kContig) {
@@ -360,7 +371,8 @@ __device__ __forceinline__ void prefix_unit(const PrefixArgs& a, char* smem, int
     walk(src);
   }
   const size_t rows_wg = 32 * a.WRp;
-  store_partial(a.po_p + (size_t)u * rows_wg * 128, a.pml_p + (size_t)u * rows_wg * 2, st, lane, nrows);
+  store_partial(reinterpret_cast<part_t<elem_t<V>>*>(a.po_p) + (size_t)u * rows_wg * 128,
+                a.pml_p + (size_t)u * rows_wg * 2, st, lane, nrows);
 }
 
 // Both item kinds in one grid when a KV head has at most 128 rows: prefix items first (row blocks of 4 waves
@@ -393,13 +405,14 @@ __global__ __launch_bounds__(256) void prefix_mixed_kernel(PrefixArgs a) {
 template <class E>
 __global__ __launch_bounds__(256) void prefix_merge_kernel(PrefixArgs a) {
   const int nh = blockIdx.x, n = nh / a.Hkv, h = nh % a.Hkv;
-  const float* lpo = a.po_s + (size_t)nh * 32 * 128;        // one suffix split per (request, KV head)
+  typedef part_t<E> PT;
+  const PT* lpo = reinterpret_cast<const PT*>(a.po_s) + (size_t)nh * 32 * 128;   // one suffix split per (n, h)
   const float* lpml = a.pml_s + (size_t)nh * 32 * 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (a.G <= 4 && a.nsplit_p <= kPrefetchSplits) {
     if (wave < a.G) {
       PrefixRow pr;
-      prefetch_prefix_row(a, pr, n, h, wave, lane);
+      prefetch_prefix_row<PT>(a, pr, n, h, wave, lane);
       merge_prefetched_row<E>(a, pr, lpo, lpml, n, h, wave, lane);
     }
   } else {
@@ -422,19 +435,20 @@ __global__ __launch_bounds__(128) void prefix_combine_kernel(PrefixArgs a) {
   const int sn = suffix_len(a, n);
   const int ns = (sn + a.chunk_s - 1) / a.chunk_s;
   const size_t sitem0 = ((size_t)n * a.Hkv + h) * a.nsplit_s;
-  combine_row<128, 1>(np + ns,
-                      [&](int s, const float*& ml, const float*& o) {
-                        if (s < np) {
-                          const size_t base = (pitem0 + s) * rows_p + rl;
-                          ml = a.pml_p + base * 2;
-                          o = a.po_p + base * 128;
-                        } else {
-                          const size_t base = (sitem0 + (s - np)) * 32 + gg;
-                          ml = a.pml_s + base * 2;
-                          o = a.po_s + base * 128;
-                        }
-                      },
-                      reinterpret_cast<E*>(a.out) + (size_t)rowg * 128);
+  typedef part_t<E> PT;
+  combine_row<128, 1, PT>(np + ns,
+                          [&](int s, const float*& ml, const PT*& o) {
+                            if (s < np) {
+                              const size_t base = (pitem0 + s) * rows_p + rl;
+                              ml = a.pml_p + base * 2;
+                              o = reinterpret_cast<const PT*>(a.po_p) + base * 128;
+                            } else {
+                              const size_t base = (sitem0 + (s - np)) * 32 + gg;
+                              ml = a.pml_s + base * 2;
+                              o = reinterpret_cast<const PT*>(a.po_s) + base * 128;
+                            }
+                          },
+                          reinterpret_cast<E*>(a.out) + (size_t)rowg * 128);
 }
 
 struct PrefixPlan {
@@ -497,10 +511,11 @@ static int prefix_launch(PrefixArgs& a, const void* q, void* out, const void* sl
   a.q = (const f16*)q;
   a.slens = ragged ? (const int*)slens : nullptr;
   a.out = (f16*)out;
-  a.po_p = (float*)align_up((char*)workspace + kWsHead, 256);
-  a.pml_p = (float*)align_up(a.po_p + p.po_p, 256);
-  a.po_s = (float*)align_up(a.pml_p + p.pml_p, 256);
-  a.pml_s = (float*)align_up(a.po_s + p.po_s, 256);
+  // Partial regions are sized for fp32 rows; fp16 partials use the first half of theirs.
+  a.po_p = align_up((char*)workspace + kWsHead, 256);
+  a.pml_p = (float*)align_up((float*)a.po_p + p.po_p, 256);
+  a.po_s = align_up(a.pml_p + p.pml_p, 256);
+  a.pml_s = (float*)align_up((float*)a.po_s + p.po_s, 256);
   // Up to 128 rows per KV head, prefix and suffix items share one launch; a merge (or combine) launch follows.
   // Beyond, the prefix launch runs first and whole-suffix items merge its partials themselves.
   const bool mixed = p.WRp == 4;

@@ -16,7 +16,7 @@ struct SpecArgs {
   const f16* v;
   const uint32_t* bits;    // (B, kd, W), or null: every cache position visible to every query row (plain decode)
   const int* lens;         // (B,) cache positions in use per batch entry (clamped to [kd, L]), or null: all L
-  float* part_o;           // [item][32*WR][128], item = (grp * nrb + rb) * nsplit + split
+  void* part_o;            // [item][32*WR][128] normalised O of type part_t, item = (grp * nrb + rb) * nsplit + split
   float* part_ml;          // [item][32*WR][2]
   f16* out;                // (B, kd, Hq, 128)
   int B, kd, Hq, Hkv, G, L, W;
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void spec_partial_kernel(SpecArgs a) {
     const int qr = row0 + r, i = qr / a.G, gg = qr % a.G;
     return a.q + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128;
   };
-  float* po = a.part_o + (size_t)item * rows_wg * 128;
+  part_t<elem_t<V>>* po = reinterpret_cast<part_t<elem_t<V>>*>(a.part_o) + (size_t)item * rows_wg * 128;
   float* pml = a.part_ml + (size_t)item * rows_wg * 2;
   if (a.WK == 4)
     attend_wg<1, 4, 2, V>(smem, src, qrow, R - row0, kbeg, ntiles, po, pml);
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) void decode_paged_kernel(SpecArgs a) {
   const PagedSrc<kNHD> src = paged_src<kNHD>(a.k, a.v, a.ps, a.Hkv, a.num_pages, a.sl2,
                                              a.pages + (size_t)b * a.max_pages, a.max_pages, h, kbeg, kend);
   auto qrow = [&](int r) { return a.q + ((size_t)b * a.Hq + h * a.G + r) * 128; };
-  float* po = a.part_o + (size_t)item * 32 * 128;
+  part_t<elem_t<V>>* po = reinterpret_cast<part_t<elem_t<V>>*>(a.part_o) + (size_t)item * 32 * 128;
   float* pml = a.part_ml + (size_t)item * 32 * 2;
   attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, po, pml);
 }
@@ -176,7 +176,8 @@ __global__ __launch_bounds__(64 * NW) void spec_partial_rows_kernel(SpecArgs a) 
                        const int qr = row0 + r, i = qr / a.G, gg = qr % a.G;
                        return a.q + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128;
                      },
-                     R - row0, kbeg, ntiles, a.part_o + (size_t)item * rows_wg * 128,
+                     R - row0, kbeg, ntiles,
+                     reinterpret_cast<part_t<elem_t<V>>*>(a.part_o) + (size_t)item * rows_wg * 128,
                      a.part_ml + (size_t)item * rows_wg * 2);
 }
 
@@ -192,13 +193,14 @@ __global__ __launch_bounds__(128) void spec_combine_kernel(SpecArgs a) {
   const size_t item0 = (size_t)(grp * a.nrb + rb) * a.nsplit;
   const int b = grp / a.Hkv, h = grp % a.Hkv;
   const int i = row / a.G, gg = row % a.G;
-  combine_row<128, 1>(a.nsplit,
-                      [&](int s, const float*& ml, const float*& o) {
-                        const size_t base = (item0 + s) * rows_wg + rl;
-                        ml = a.part_ml + base * 2;
-                        o = a.part_o + base * 128;
-                      },
-                      reinterpret_cast<E*>(a.out) + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128);
+  typedef part_t<E> PT;
+  combine_row<128, 1, PT>(a.nsplit,
+                          [&](int s, const float*& ml, const PT*& o) {
+                            const size_t base = (item0 + s) * rows_wg + rl;
+                            ml = a.part_ml + base * 2;
+                            o = reinterpret_cast<const PT*>(a.part_o) + base * 128;
+                          },
+                          reinterpret_cast<E*>(a.out) + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128);
 }
 
 struct SpecPlan {
@@ -249,8 +251,8 @@ static size_t spec_partials_bytes(const SpecPlan& p) { return (p.po_floats + p.p
 
 template <class V>
 static int spec_launch(SpecArgs& a, const SpecPlan& p, void* partials, hipStream_t s) {
-  a.part_o = (float*)partials;
-  a.part_ml = a.part_o + p.po_floats;
+  a.part_o = partials;                         // sized for fp32 rows; fp16 partials use the first half of each
+  a.part_ml = (float*)partials + p.po_floats;
   a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;
   a.sl2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
   const unsigned items = (unsigned)(a.B * a.Hkv * p.nrb * p.nsplit);
@@ -387,8 +389,8 @@ static int decode_paged(const void* q, const void* k_pages, const void* v_pages,
   a.B = (int)B; a.kd = 1; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = 1;
   a.pages = (const int*)page_table;
   a.ps = (int)page_size; a.max_pages = (int)max_pages; a.num_pages = (int)num_pages;
-  a.part_o = (float*)align_up((char*)workspace + kWsHead, 256);
-  a.part_ml = a.part_o + p.po_floats;
+  a.part_o = align_up((char*)workspace + kWsHead, 256);
+  a.part_ml = (float*)a.part_o + p.po_floats;
   a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;
   a.sl2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
   hipStream_t s = (hipStream_t)stream;
