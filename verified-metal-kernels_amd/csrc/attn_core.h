@@ -794,8 +794,8 @@ constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
 // writes two whole rows (contiguous) instead of pieces of 32 rows.  Each wave parks its O^T registers, normalised by
 // its rows' l, in its own 16 KB of LDS as 32 rows of 128 floats, the 16-byte chunk c of row r at chunk position
 // (c + r) mod 32 (at most two lanes per bank group on the writes, none on the row reads), then stores rows 2i,
-// 2i + 1 per instruction in the partial type PT.  Called by every wave of the workgroup (it contains a barrier);
-// rows >= nvalid are not written.
+// 2i + 1 per instruction in the partial type PT, as non-temporal stores (the row split's partials are read by a
+// later launch).  Called by every wave of the workgroup (it contains a barrier); rows >= nvalid are not written.
 template <class PT>
 __device__ __forceinline__ void store_partial_rows(char* smem, PT* po, float* pml, const RowState& st, int wave,
                                                    int lane, int nvalid) {
@@ -815,7 +815,7 @@ __device__ __forceinline__ void store_partial_rows(char* smem, PT* po, float* pm
   for (int i = 0; i < 16; ++i) {
     const int row = 2 * i + g;
     const floatx4 v = *reinterpret_cast<const floatx4*>(lds + row * 128 + ((r + row) & 31) * 4);
-    if (row < nvalid) store_part4(po + row * 128 + r * 4, v);
+    if (row < nvalid) store_part4_nt(po + row * 128 + r * 4, v);
   }
   if (g == 0 && r < nvalid) *reinterpret_cast<float2*>(pml + 2 * r) = float2{st.m, ltot};
 }

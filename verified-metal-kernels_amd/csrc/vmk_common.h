@@ -52,6 +52,15 @@ __device__ __forceinline__ void store_part4(float* p, floatx4 v) { *reinterpret_
 __device__ __forceinline__ void store_part4(f16* p, floatx4 v) {
   *reinterpret_cast<half4*>(p) = half4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
 }
+// The same as non-temporal stores, for partials that are read back only by a later launch: they stream to memory
+// instead of waiting in L2 for the end-of-kernel writeback (C2's prefix partials -2 %; partials that a combine reads
+// right after, as C3's, lose by it).
+__device__ __forceinline__ void store_part4_nt(float* p, floatx4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(p));
+}
+__device__ __forceinline__ void store_part4_nt(f16* p, floatx4 v) {
+  __builtin_nontemporal_store(half4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]}, reinterpret_cast<half4*>(p));
+}
 __device__ __forceinline__ float2 load_part2(const float* p) { return *reinterpret_cast<const float2*>(p); }
 __device__ __forceinline__ float2 load_part2(const f16* p) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
