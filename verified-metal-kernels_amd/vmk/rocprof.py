@@ -3,6 +3,11 @@
     python -m vmk.rocprof kernels <run_results.db> [name-substring]      per kernel and grid: calls, avg/min/max us
     python -m vmk.rocprof pmc <run_results.db> [name-substring]          per kernel: average counter value per dispatch
     python -m vmk.rocprof traffic <fetch.db> <write.db> <copy_bytes>     HBM bytes per call of the dominant kernels
+    python -m vmk.rocprof trafficjson <fetch.db> <write.db> <copy_bytes> <config> <bracket> <algorithmic_bytes>
+                          <out.json> <kernel-prefix>...      one configuration's bracket (the kernels whose names
+                                                             start with a prefix), as bench.py reads it
+    python -m vmk.rocprof mfmajson <sq.db> <config> <bracket> <kernel-prefix> <out.json>
+                          MFMA-busy share, co-issue and VALU per MFMA of one kernel from an SQ counter run
 
 `traffic` reads one FETCH_SIZE run and one WRITE_SIZE run of the same command (rocprofv3 collects each in its own
 pass).  The command must include a plain streaming kernel that reads `copy_bytes` bytes and writes as many
@@ -123,6 +128,44 @@ def traffic(fetch_db, write_db, copy_bytes):
     return "\n".join(out), res, (kf, kw)
 
 
+def traffic_json(fetch_db, write_db, copy_bytes, config, bracket, algorithmic, prefixes, commands=()):
+    """The HBM bytes per call of one configuration's dominant bracket from a FETCH_SIZE and a WRITE_SIZE run of that
+    configuration alone: the per-dispatch averages of the bracket's kernels (names starting with one of
+    `prefixes`) summed, as the dict bench.py reads from profiles/<config>_traffic.json."""
+    _, res, (kf, kw) = traffic(fetch_db, write_db, copy_bytes)
+    names = sorted(n for n in res if any(n.startswith(p) for p in prefixes))
+    if not names:
+        raise SystemExit(f"no kernel of the run starts with {prefixes}")
+    rd = sum(res[n]["read"] for n in names)
+    wr = sum(res[n]["write"] for n in names)
+    return dict(workload=config, kernel=bracket,
+                note=f"HBM bytes per call of the {bracket} bracket: {' + '.join(names)}; FETCH_SIZE and WRITE_SIZE "
+                     f"scaled by the calibration kernel's reading (read x{kf:.3f}, write x{kw:.3f} of true bytes)",
+                read_bytes=int(round(rd, -4)), write_bytes=int(round(wr, -4)), algorithmic_bytes=int(algorithmic),
+                ratio=round((rd + wr) / algorithmic, 3), commands=list(commands))
+
+
+SIMDS = 1024                   # MI355X: 8 XCDs x 32 CUs x 4 SIMDs
+
+
+def mfma_json(sq_db, config, bracket, prefix):
+    """MFMA utilisation of the kernel whose name starts with `prefix`, from one SQ counter run: busy share =
+    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024 SIMDs) (GRBM_GUI_ACTIVE is summed over the 8 XCDs),
+    co-issue = SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES, VALU per MFMA = SQ_INSTS_VALU /
+    SQ_INSTS_MFMA; per-dispatch averages."""
+    t = pmc_table(sq_db)
+    names = [n for n in t if n.startswith(prefix)]
+    if len(names) != 1:
+        raise SystemExit(f"{len(names)} kernels start with {prefix!r}: {names}")
+    c = {k: sum(v) / len(v) for k, v in t[names[0]].items()}
+    busy = c["SQ_VALU_MFMA_BUSY_CYCLES"]
+    return dict(workload=config, kernel=bracket, kernel_name=names[0],
+                mfma_busy=round(busy / (c["GRBM_GUI_ACTIVE"] / 8 * SIMDS), 4),
+                coexec=round(c["SQ_VALU_MFMA_COEXEC_CYCLES"] / busy, 4) if busy else None,
+                valu_per_mfma=round(c["SQ_INSTS_VALU"] / c["SQ_INSTS_MFMA"], 2) if c.get("SQ_INSTS_MFMA") else None,
+                counters={k: round(v, 1) for k, v in sorted(c.items())})
+
+
 if __name__ == "__main__":
     cmd = sys.argv[1] if len(sys.argv) > 1 else ""
     if cmd == "kernels":
@@ -131,5 +174,23 @@ if __name__ == "__main__":
         print(pmc(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else KERNEL_PREFIX))
     elif cmd == "traffic":
         print(traffic(sys.argv[2], sys.argv[3], int(sys.argv[4]))[0])
+    elif cmd == "trafficjson":
+        import json
+        fdb, wdb, cb, config, bracket, algo, out = sys.argv[2:9]
+        cmds = [f"cd /tmp && rocprofv3 --pmc {c} -d <dir> -o run -- python3 $R/bench.py --configs {config} --no-cpu "
+                f"--ab-rounds 0 --steps 3 --warmup 1 --calibrate-copy {cb} --results ''" for c in ("FETCH_SIZE",
+                                                                                                  "WRITE_SIZE")]
+        cmds.append(f"PYTHONPATH=$R/verified-metal-kernels_amd python3 -m vmk.rocprof trafficjson <fetch db> "
+                    f"<write db> {cb} {config} {bracket} {algo} profiles/{config}_traffic.json {' '.join(sys.argv[9:])}")
+        d = traffic_json(fdb, wdb, int(cb), config, bracket, int(algo), sys.argv[9:], cmds)
+        with open(out, "w") as f:
+            json.dump(d, f, indent=1)
+        print(json.dumps(d))
+    elif cmd == "mfmajson":
+        import json
+        d = mfma_json(*sys.argv[2:6])
+        with open(sys.argv[6], "w") as f:
+            json.dump(d, f, indent=1)
+        print(json.dumps(d))
     else:
         raise SystemExit(__doc__)
