@@ -310,7 +310,7 @@ def test_noalloc_entry_point_refuses_oversized_shapes_without_a_gpu():
     partials exceed the static scratch is refused here, on a machine without a GPU (dummy aligned pointers)."""
     from vmk import lib
     L = lib.load()
-    assert L.vmk_spec_noalloc_max_bytes() == 64 << 20
+    assert L.vmk_spec_noalloc_max_bytes() == 32 << 20
     p = 1 << 20                                        # never dereferenced: the call is refused first
     rc = L.vmk_spec_verify_noalloc(p, p, p, p, p, 8, 64, 32, 8, 128, 64 << 20, 2, None)
     assert rc == 1 and b"static scratch" in L.vmk_last_error()

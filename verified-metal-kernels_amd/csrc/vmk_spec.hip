@@ -240,19 +240,25 @@ using namespace vmk;
 extern "C" size_t vmk_spec_workspace_size(int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L) {
   if (B <= 0 || kd <= 0 || Hkv <= 0 || Hq % Hkv || D != 128 || L < kd) return 0;
   SpecPlan p = spec_plan(B, kd, Hq, Hkv, L);
-  return kWsHead + (p.po_floats + p.pml_floats) * sizeof(float) + 256;
+  return kWsHead + (p.po_floats + p.pml_floats) * sizeof(float) + 512;   // fits either partial type
 }
 
 // Partial launch (key split or row split by the plan) and LSE-combine launch of one spec/decode call; V is the
 // operand type of the inputs (half8: fp16, bf16x8: bf16).  `partials` is the 256-byte aligned region of
-// spec_partials_bytes(p) bytes that receives the partials: every partial the combine reads is written first, so the
-// region needs no initialisation.
-static size_t spec_partials_bytes(const SpecPlan& p) { return (p.po_floats + p.pml_floats) * sizeof(float); }
+// spec_partials_bytes<V>(p) bytes that receives the partials: every partial the combine reads is written first, so
+// the region needs no initialisation.  Layout: the normalised O rows in the partial type of V's inputs, then the
+// (m, l) pairs from the next 256-byte boundary.
+template <class V>
+static size_t spec_ml_offset(const SpecPlan& p) {
+  return (p.po_floats * sizeof(part_t<elem_t<V>>) + 255) / 256 * 256;
+}
+template <class V>
+static size_t spec_partials_bytes(const SpecPlan& p) { return spec_ml_offset<V>(p) + p.pml_floats * sizeof(float); }
 
 template <class V>
 static int spec_launch(SpecArgs& a, const SpecPlan& p, void* partials, hipStream_t s) {
-  a.part_o = partials;                         // sized for fp32 rows; fp16 partials use the first half of each
-  a.part_ml = (float*)partials + p.po_floats;
+  a.part_o = partials;
+  a.part_ml = reinterpret_cast<float*>((char*)partials + spec_ml_offset<V>(p));
   a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;
   a.sl2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
   const unsigned items = (unsigned)(a.B * a.Hkv * p.nrb * p.nsplit);
@@ -390,7 +396,7 @@ static int decode_paged(const void* q, const void* k_pages, const void* v_pages,
   a.pages = (const int*)page_table;
   a.ps = (int)page_size; a.max_pages = (int)max_pages; a.num_pages = (int)num_pages;
   a.part_o = align_up((char*)workspace + kWsHead, 256);
-  a.part_ml = (float*)a.part_o + p.po_floats;
+  a.part_ml = reinterpret_cast<float*>((char*)a.part_o + spec_ml_offset<V>(p));
   a.WR = p.WR; a.WK = p.WK; a.nrb = p.nrb; a.nsplit = p.nsplit; a.chunk = p.chunk;
   a.sl2 = (float)(1.0 / sqrt(128.0)) * kLog2e;
   hipStream_t s = (hipStream_t)stream;
@@ -428,7 +434,7 @@ VMK_DECODE_PAGED_ENTRY(vmk_decode_paged_nhd_bf16, true, bf16x8)
 // race; the array keeps the last call's partials, and no part of it must start at zero (every partial the combine
 // reads is written first).
 namespace vmk {
-constexpr size_t kScratchBytes = (size_t)64 << 20;   // partials of every bench shape (C4: 32.5 MiB)
+constexpr size_t kScratchBytes = (size_t)32 << 20;   // fp16 partials of every bench shape (C4: 16.5 MiB)
 constexpr int kScratchDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 static void* g_scratch_ptr[kScratchDevices];
@@ -469,7 +475,7 @@ extern "C" int vmk_spec_verify_noalloc(const void* q, const void* k, const void*
   // Every check comes before the first HIP call: a rejected call touches no device.
   if (int rc = spec_check_args(q, k, v, mask_words, out, B, kd, Hq, Hkv, D, L, W)) return rc;
   const SpecPlan p = spec_plan(B, kd, Hq, Hkv, L);
-  const size_t need = spec_partials_bytes(p);
+  const size_t need = spec_partials_bytes<half8>(p);
   if (need > kScratchBytes) {
     set_error("vmk_spec_verify_noalloc: this shape needs %zu bytes of partials, more than the %zu bytes of static "
               "scratch; call vmk_spec_verify with a workspace instead", need, kScratchBytes);
