@@ -20,10 +20,11 @@ Method:
     256 MB Infinity Cache cannot serve a repeat;
   * W untimed warm-up calls, then the per-call time: the K calls captured once in a HIP graph, replayed 15 times,
     each replay between two HIP events (synchronised before and after); the median is `us_per_call`, with p10/p90.
-    Before timing, 3 replays are checked bit for bit against an eager call.  `eager` gives the same K calls
+    Before timing, 3 replays are checked bit for bit against an eager call.  Then `eager` gives the same K calls
     launched one by one from Python, which adds the host's per-call overhead;
-  * the dominant kernel of each op is bracketed by its own pair of HIP events on its launch stream inside the eager
-    loop (libvmk's vmk_profile_next hook), which gives the roofline figure;
+  * the dominant kernel of each op is bracketed by its own pair of HIP events on its launch stream inside that eager
+    loop (libvmk's vmk_profile_next hook), which gives the roofline figure; the loop runs after the graph replays, in
+    the steady state (a power-bound op's first calls after a short warm-up vary by +-25 %);
   * A/B against the torch standard ops (the reference's headline form, bench.py:99-126, 157-236): each kernel
     module is screened by the verifier's static gate before it is imported (reference bench.py:159-161); on the
     reference's BENCH_SHAPES and on this build's configurations, the output is checked against the standard op
@@ -325,6 +326,9 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     for i in range(warmup):
         call_op(opname, sets[i % len(sets)])
     torch.cuda.synchronize()
+    gt = graph_us_per_call(opname, sets, steps)
+    # The eager loop with the dominant bracket runs after the graph replays: right after a short warm-up, a
+    # power-bound op's first eager calls still vary by +-25 % (C4: 149-240 us against 163-172 once settled).
     kid = lib.KERNEL_IDS[dom_kernel]
     hev = HipEvents(steps)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -339,7 +343,6 @@ def bench_config(name, opname, shape, dist, steps, warmup, do_cpu):
     eager_us = e0.elapsed_time(e1) * 1e3 / steps
     dom_us = sum(hev.elapsed_ms(i) for i in range(steps)) * 1e3 / steps
     hev.close()
-    gt = graph_us_per_call(opname, sets, steps)
     us = gt["median"]
     gbs = total_bytes / us / 1e3
     dom_gbs = dom_bytes / dom_us / 1e3
