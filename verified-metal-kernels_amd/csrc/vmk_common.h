@@ -111,6 +111,25 @@ __device__ __forceinline__ float wave_sum(float x) {
   return wave_reduce(x, 0.f, [](float a, float b) { return a + b; });
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves (VALU only, no LDS round trips): row_shr:1, 2, 4
+// and 8 scan each row of 16 lanes (lanes shifted in from before the row's start read 0), then row_bcast:15 adds
+// row 0's and row 2's totals into rows 1 and 3, and row_bcast:31 adds lane 31's prefix into rows 2 and 3.  A lane
+// a DPP move does not write adds 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  x += dpp_u32<0x111, 0xF>(x);
+  x += dpp_u32<0x112, 0xF>(x);
+  x += dpp_u32<0x114, 0xF>(x);
+  x += dpp_u32<0x118, 0xF>(x);
+  x += dpp_u32<0x142, 0xA>(x);
+  x += dpp_u32<0x143, 0xC>(x);
+  return x;
+}
+
 __device__ __forceinline__ half8 zero_h8() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
 
 __device__ __forceinline__ half8 as_h8(u32x4 u) { return __builtin_bit_cast(half8, u); }

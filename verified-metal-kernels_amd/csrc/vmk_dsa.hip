@@ -77,12 +77,7 @@ __device__ __forceinline__ int valid_len(const DsaArgs& a, int b) {
 template <int NT>
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;  // inclusive prefix within the wave
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const uint32_t x = wave_incl_scan(v);  // inclusive prefix within the wave
   if (lane == 63) red[wave] = x;
   lds_barrier();
   uint32_t before = 0, all = 0;
@@ -97,27 +92,33 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
   return before + x - v;
 }
 
-// Finds, in hist[0..nbins) (nbins a multiple of NT), the bin holding the need-th largest element: out[0] = bin,
-// out[1] = need minus the count strictly above that bin.  Every thread of the block must call it.  The per-thread
-// arithmetic is select_math.h's, which vmk_debug_select_threshold replays on the host.
-template <int NT>
-__device__ void find_threshold(const uint32_t* hist, int nbins, uint32_t need, uint32_t* red, uint32_t* out) {
+// Finds, in hist[0..NBINS) (NBINS a multiple of NT), the bin holding the need-th largest element: out[0] = bin,
+// out[1] = need minus the count strictly above that bin.  Every thread of the block must call it.  Each thread reads
+// its NBINS / NT bins once into registers.  The per-thread arithmetic is select_math.h's, which
+// vmk_debug_select_threshold replays on the host.
+template <int NT, int NBINS>
+__device__ void find_threshold(const uint32_t* hist, uint32_t need, uint32_t* red, uint32_t* out) {
+  static_assert(NBINS % NT == 0, "whole bins per thread");
+  constexpr int kPer = NBINS / NT;
   // Defaults (bin 0) for a histogram that holds fewer than `need` elements, so callers that index with out[0]
   // stay in bounds; the barriers of the scan below order these writes before the finder's.
   if (threadIdx.x == 0) {
     out[0] = 0;
     out[1] = 0;
   }
-  const int per = nbins / NT;
-  const int lo = threshold_range_lo(threadIdx.x, NT, per);   // a prefix scan over thread ids runs top-down
-  uint32_t local = 0;
-  for (int i = 0; i < per; ++i) local += hist[lo + i];
+  const int lo = threshold_range_lo(threadIdx.x, NT, kPer);   // a prefix scan over thread ids runs top-down
+  uint32_t bins[kPer], local = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    bins[i] = hist[lo + i];
+    local += bins[i];
+  }
   uint32_t total;
   const uint32_t above = block_excl_scan<NT>(local, red, &total);
   Threshold t;
   // A range whose counts cannot reach the need-th element from `above` has no hit; skip its walk.
-  if (above < need && above + local >= need && threshold_in_range(hist, lo, per, above, need, &t)) {
-    out[0] = t.bin;
+  if (above < need && above + local >= need && threshold_in_range(bins, 0, kPer, above, need, &t)) {
+    out[0] = (uint32_t)lo + t.bin;
     out[1] = t.rest;
   }
   lds_barrier();
@@ -362,16 +363,11 @@ __device__ __forceinline__ void select_scan_item(const DsaArgs& a, int wg, int b
   cnt[tid] = a.chist[(size_t)b * kCBins + tid];
   if (tid == 0) b1s = 0;
   __syncthreads();
-  find_threshold<256>(cnt, kCBins, kTopK, red, thr);
+  find_threshold<256, kCBins>(cnt, kTopK, red, thr);
   if (tid < 64) {
     const uint32_t* fine = a.hist + (size_t)b * kBins + coarse_bin_clamped(thr[0]) * 32;
-    uint32_t v = tid < 32 ? fine[31 - tid] : 0u;            // lane i: fine bin 31 - i (top first)
-    uint32_t x = v;                                          // inclusive prefix from the top
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-      const uint32_t y = __shfl_up(x, o, 64);
-      if ((tid & 63) >= o) x += y;
-    }
+    const uint32_t v = tid < 32 ? fine[31 - tid] : 0u;      // lane i: fine bin 31 - i (top first)
+    const uint32_t x = wave_incl_scan(v);                    // inclusive prefix from the top
     if (tid < 32 && fine_hit(x, v, thr[1])) b1s = fine_bin(thr[0], tid);
   }
   __syncthreads();
@@ -408,7 +404,7 @@ __global__ __launch_bounds__(256) void dsa_select_scan_kernel(DsaArgs a) {
 template <int CAND>
 struct SelectShared {
   uint32_t hist[2048];           // second digit (bits 18..8)
-  uint32_t hist3[1024];          // third digit (bits 7..0); the upper bins stay zero (a bin per thread and more)
+  uint32_t hist3[1024];          // third digit (bits 7..0): 256 bins, or one per thread of a larger block
   uint32_t cand_key[CAND];
   int cand_pos[CAND];
   uint32_t goff[kMaxSlices + 1], eoff[kMaxSlices + 1];
@@ -438,10 +434,14 @@ struct BoolC {
 // bucket is refined to T by the second (bits 18..8) and third (bits 7..0) digits over LDS histograms.  None of this
 // depends on NT, the block size, or on which window is asked for: every result is an integer count or a position.
 // emit(slot, position) is called for each slot of the window that holds a pick (every slot, for consistent inputs).
-// Returns the request's count, min(n, 2048).  Every thread of the block calls it.
-template <int NT, int CAND, class Emit>
+// The window holds at most W slots (hi - lo <= W).  Returns the request's count, min(n, 2048).  Every thread of the
+// block calls it.
+template <int NT, int W, int CAND, class Emit>
 __device__ int select_window(const DsaArgs& a, SelectShared<CAND>& sh, int b, int lo, int hi, Emit emit) {
   static_assert(kMaxSlices % NT == 0, "slices per thread");
+  // The third digit's histogram: 256 bins, or one per thread when the block is larger (the upper bins stay zero).
+  constexpr int kH3 = NT > 256 ? NT : 256;
+  static_assert(kH3 <= (int)(sizeof(sh.hist3) / sizeof(sh.hist3[0])), "third-digit bins");
   const int tid = threadIdx.x;
   const int n = valid_len(a, b);
   if (n <= kTopK) {
@@ -450,7 +450,7 @@ __device__ int select_window(const DsaArgs& a, SelectShared<CAND>& sh, int b, in
   }
   // The digits' histograms are cleared while the first loads fly (the scans' barriers below order it).
   for (int i = tid; i < 2048; i += NT) sh.hist[i] = 0;
-  for (int i = tid; i < 1024; i += NT) sh.hist3[i] = 0;
+  for (int i = tid; i < kH3; i += NT) sh.hist3[i] = 0;
   const int ns = (n + kScanWG - 1) / kScanWG;
   const int* glb = a.glist + (size_t)b * a.Ls;
   const uint32_t* ekb = a.ekey + (size_t)b * a.Ls;
@@ -501,13 +501,30 @@ __device__ int select_window(const DsaArgs& a, SelectShared<CAND>& sh, int b, in
     sh.eoff[ns] = ncand;
   }
   lds_barrier();
-  // Positions above the bucket.
+  // Positions above the bucket: loaded now, emitted once the bucket's picks are known too, so that a window that
+  // also refines the bucket does so while these loads fly (the refine's barriers wait for LDS only).
+  constexpr int kGPer = (W + NT - 1) / NT;
   const int gend = min(hi, (int)min(n_gt, (uint32_t)kTopK));
-  for (int s = lo + tid; s < gend; s += NT) {
-    const int sl = slice_of(sh.goff, ns, (uint32_t)s);
-    emit(s, glb[sl * kScanWG + (s - (int)sh.goff[sl])]);
+  int gpos[kGPer];
+#pragma unroll
+  for (int k = 0; k < kGPer; ++k) {
+    const int s = lo + tid + k * NT;
+    if (s < gend) {
+      const int sl = slice_of(sh.goff, ns, (uint32_t)s);
+      gpos[k] = glb[sl * kScanWG + (s - (int)sh.goff[sl])];
+    }
   }
-  if (n_gt >= (uint32_t)hi) return kTopK;                     // the window holds no pick from the bucket
+  auto emit_above = [&]() {
+#pragma unroll
+    for (int k = 0; k < kGPer; ++k) {
+      const int s = lo + tid + k * NT;
+      if (s < gend) emit(s, gpos[k]);
+    }
+  };
+  if (n_gt >= (uint32_t)hi) {                                 // the window holds no pick from the bucket
+    emit_above();
+    return kTopK;
+  }
   // The bucket's candidates in position order.
   const bool in_lds = ncand <= (uint32_t)CAND;
   if (in_lds) {
@@ -563,14 +580,14 @@ __device__ int select_window(const DsaArgs& a, SelectShared<CAND>& sh, int b, in
     };
     for_each([&](uint32_t key, int) { atomicAdd(&sh.hist[(key >> 8) & 0x7FF], 1u); });
     lds_barrier();
-    find_threshold<NT>(sh.hist, 2048, need, sh.red, sh.thr);
+    find_threshold<NT, 2048>(sh.hist, need, sh.red, sh.thr);
     const uint32_t b2 = sh.thr[0];
     const uint32_t need2 = sh.thr[1];
     for_each([&](uint32_t key, int) {
       if (((key >> 8) & 0x7FF) == b2) atomicAdd(&sh.hist3[key & 0xFF], 1u);
     });
     lds_barrier();
-    find_threshold<NT>(sh.hist3, 1024, need2, sh.red, sh.thr);
+    find_threshold<NT, kH3>(sh.hist3, need2, sh.red, sh.thr);
     const uint32_t T = (b1 << 19) | (b2 << 8) | sh.thr[0];
     const uint32_t need_eq = sh.thr[1];
     // Bucket picks: keys above T, then the first need_eq keys equal to T in position order.  With the candidates
@@ -602,7 +619,9 @@ __device__ int select_window(const DsaArgs& a, SelectShared<CAND>& sh, int b, in
     });
     return kTopK;
   };
-  return in_lds ? refine(BoolC<true>{}) : refine(BoolC<false>{});
+  const int count = in_lds ? refine(BoolC<true>{}) : refine(BoolC<false>{});
+  emit_above();
+  return count;
 }
 
 // Leaves request b's histograms zero for the next call, after the indexer ran: fine bins [fine0, fine1) and the
@@ -620,7 +639,7 @@ __global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
   __shared__ SelectShared<kCand> sh;
   const int b = blockIdx.x, tid = threadIdx.x;
   int* idx = a.idx + (size_t)b * kTopK;
-  const int cnt = select_window<1024>(a, sh, b, 0, kTopK, [&](int s, int p) { idx[s] = p; });
+  const int cnt = select_window<1024, kTopK>(a, sh, b, 0, kTopK, [&](int s, int p) { idx[s] = p; });
   clear_histograms(a, b, 0, kBins, tid, 1024);
   if (tid == 0) a.cnt[b] = cnt;
 }
@@ -838,7 +857,7 @@ __device__ __forceinline__ void attn_item(const DsaArgs& a, int item, char* __re
   int cnt;
   if (a.fused_select) {
     int* idxo = a.idx + (size_t)b * kTopK;
-    cnt = select_window<256>(a, sel, b, kbeg, kbeg + kChunk, [&](int s, int p) {
+    cnt = select_window<256, kChunk>(a, sel, b, kbeg, kbeg + kChunk, [&](int s, int p) {
       sidx[s - kbeg] = p;
       if (hb == 0) idxo[s] = p;
     });
@@ -846,7 +865,7 @@ __device__ __forceinline__ void attn_item(const DsaArgs& a, int item, char* __re
       clear_histograms(a, b, chunk * (kBins / kNChunk), (chunk + 1) * (kBins / kNChunk), threadIdx.x, 256);
       if (chunk == 0 && threadIdx.x == 0) a.cnt[b] = cnt;
     }
-    __syncthreads();
+    lds_barrier();                              // sidx; the Q loads and the idx and histogram stores stay in flight
     // Clamped into the cache; keys past kend read the zero row whatever their entry holds.
     if (threadIdx.x < kChunk) sidx[threadIdx.x] = min(max(sidx[threadIdx.x], 0), a.L - 1);
   } else {
