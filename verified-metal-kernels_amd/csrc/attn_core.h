@@ -781,6 +781,133 @@ __device__ __forceinline__ void combine_row(int nparts, Part part, E* out) {
   for (int k = 0; k < PER; ++k) out[tid + k * NT] = (E)(num[k] / den);
 }
 
+// ---- the same merge by a group of lanes per output row, eight head-dims per lane (one 16-byte load of an fp16
+// partial row, two of an fp32 one, instead of a 2-byte load per thread and partial).  part(i, ml, o) sets ml -> the
+// (m, l) pair of partial i and o -> this lane's eight elements of partial i's normalised O row.  Every lane loads the
+// (m, l) of every partial itself (the lanes of a row read the same addresses), so the weights need no exchange
+// between lanes.  The maximum, the weights exp2(m_i - M) * l_i, their order (partial 0 first) and the arithmetic are
+// those of combine_row, so both give the same bits.
+template <class PT>
+struct Part8 {
+  static constexpr int kWords = sizeof(PT) / 2;              // 16-byte words of eight elements
+  u32x4 w[kWords];
+  __device__ __forceinline__ void load(const PT* p) {
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) w[i] = ldg16(reinterpret_cast<const char*>(p) + 16 * i);
+  }
+  __device__ __forceinline__ float get(int k) const {
+    if constexpr (kWords == 1)
+      return (float)as_h8(w[0])[k];
+    else
+      return __uint_as_float(w[k >> 2][k & 3]);
+  }
+};
+
+template <class E>
+__device__ __forceinline__ void store_out8(E* out, const float (&num)[8], float den) {
+  typedef E e8 __attribute__((ext_vector_type(8)));
+  e8 v;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = (E)(num[k] / den);
+  *reinterpret_cast<e8*>(out) = v;
+}
+
+// Weight exp2(m - M) * l of a partial, rounded before it is used: the product is not fused into the sum of the
+// weights (combine_row rounds it through LDS), so both merges add the same rounded weights.
+__device__ __forceinline__ float part_weight(float2 ml, float Muse) {
+#pragma clang fp contract(off)
+  return fast_exp2(ml.x - Muse) * ml.y;
+}
+
+// Up to H partials, all loaded before the first is used (one memory round trip).  nparts >= 1.
+template <int H, class PT, class Part, class E>
+__device__ __forceinline__ void combine_vec_held(int nparts, Part part, E* out) {
+  Part8<PT> ov[H];
+  float2 ml[H];
+#pragma unroll
+  for (int j = 0; j < H; ++j) {                      // slots past nparts reload the last partial, never used
+    const float* mlp;
+    const PT* o;
+    part(min(j, nparts - 1), mlp, o);
+    ml[j] = *reinterpret_cast<const float2*>(mlp);
+    ov[j].load(o);
+  }
+  float M = kNegInf;
+#pragma unroll
+  for (int j = 0; j < H; ++j)
+    if (j < nparts) M = fmaxf(M, ml[j].x);
+  const float Muse = (M == kNegInf) ? 0.f : M;
+  float num[8], den = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) num[k] = 0.f;
+#pragma unroll
+  for (int j = 0; j < H; ++j) {
+    if (j < nparts) {
+      const float w = part_weight(ml[j], Muse);
+      den += w;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) num[k] += w * ov[j].get(k);
+    }
+  }
+  store_out8(out, num, den);
+}
+
+template <class PT, class Part, class E>
+__device__ __forceinline__ void combine_vec(int nparts, Part part, E* out) {
+  if (nparts <= 0) {                                 // the softmax of no keys is 0 / 0
+    float num[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) num[k] = __builtin_nanf("");
+    store_out8(out, num, 1.f);
+    return;
+  }
+  if (nparts <= 8) return combine_vec_held<8, PT>(nparts, part, out);
+  if (nparts <= 16) return combine_vec_held<16, PT>(nparts, part, out);
+  if (nparts <= 32 && sizeof(PT) == 2) return combine_vec_held<32, PT>(nparts, part, out);
+  // More partials: the maximum over all of them first, then the weighted sum in batches of 16, in order.
+  constexpr int kB = 16;
+  float M = kNegInf;
+  for (int b0 = 0; b0 < nparts; b0 += kB) {
+    float mb[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const float* mlp;
+      const PT* o;
+      part(min(b0 + j, nparts - 1), mlp, o);
+      mb[j] = mlp[0];
+    }
+#pragma unroll
+    for (int j = 0; j < kB; ++j)
+      if (b0 + j < nparts) M = fmaxf(M, mb[j]);
+  }
+  const float Muse = (M == kNegInf) ? 0.f : M;
+  float num[8], den = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) num[k] = 0.f;
+  for (int b0 = 0; b0 < nparts; b0 += kB) {
+    Part8<PT> ov[kB];
+    float2 ml[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const float* mlp;
+      const PT* o;
+      part(min(b0 + j, nparts - 1), mlp, o);
+      ml[j] = *reinterpret_cast<const float2*>(mlp);
+      ov[j].load(o);
+    }
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      if (b0 + j < nparts) {
+        const float w = part_weight(ml[j], Muse);
+        den += w;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) num[k] += w * ov[j].get(k);
+      }
+    }
+  }
+  store_out8(out, num, den);
+}
+
 // ---- one workgroup of NW waves sharing a ring of kRowsStages stages: wave w owns rows [32w, 32w+32) and every wave
 // consumes every tile of [kbeg, kbeg + 32*ntiles).  Writes the WG's partial (32*NW rows) like attend_wg.
 // Eight stages (128 KB): six tiles in flight beside the pair being computed, and one workgroup per CU (two would not

@@ -203,6 +203,42 @@ __global__ __launch_bounds__(128) void spec_combine_kernel(SpecArgs a) {
                           reinterpret_cast<E*>(a.out) + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128);
 }
 
+// The same merge for many rows (at least kCombineVecRows): one wave per 4 rows, 16 lanes per row, each lane 8
+// head-dims loaded 16 bytes at a time, so the partials stream with a quarter of the load instructions per byte.  Few
+// rows take spec_combine_kernel: there the merge is latency-bound, and one thread per head-dim keeps each thread's
+// chain of products short.  Both give the same bits.
+constexpr int kCombineVecRows = 1024;
+template <class E>
+__global__ __launch_bounds__(64) void spec_combine_vec_kernel(SpecArgs a) {
+  const int R = a.kd * a.G;
+  const int lane = threadIdx.x, c = lane & 15;
+  const int rowg = blockIdx.x * 4 + (lane >> 4);                    // grp * R + row
+  if (rowg >= a.B * a.Hkv * R) return;                              // a whole row group of lanes
+  const int grp = rowg / R, row = rowg % R;
+  const int rb = row / (32 * a.WR), rl = row % (32 * a.WR);
+  const size_t rows_wg = 32 * a.WR;
+  const size_t item0 = (size_t)(grp * a.nrb + rb) * a.nsplit;
+  const int b = grp / a.Hkv, h = grp % a.Hkv;
+  const int i = row / a.G, gg = row % a.G;
+  typedef part_t<E> PT;
+  combine_vec<PT>(a.nsplit,
+                  [&](int s, const float*& ml, const PT*& o) {
+                    const size_t base = (item0 + s) * rows_wg + rl;
+                    ml = a.part_ml + base * 2;
+                    o = reinterpret_cast<const PT*>(a.part_o) + base * 128 + 8 * c;
+                  },
+                  reinterpret_cast<E*>(a.out) + ((size_t)(b * a.kd + i) * a.Hq + h * a.G + gg) * 128 + 8 * c);
+}
+
+// The combine launch for `rows` output rows.
+template <class E>
+static void launch_spec_combine(const SpecArgs& a, int64_t rows, hipStream_t s) {
+  if (rows >= kCombineVecRows)
+    hipLaunchKernelGGL(spec_combine_vec_kernel<E>, dim3((unsigned)((rows + 3) / 4)), dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL(spec_combine_kernel<E>, dim3((unsigned)rows), dim3(128), 0, s, a);
+}
+
 struct SpecPlan {
   bool rows_mode;
   int WR, WK, nrb, nsplit, chunk;
@@ -272,8 +308,7 @@ static int spec_launch(SpecArgs& a, const SpecPlan& p, void* partials, hipStream
   prof_after(kKSpecPartial, s);
   VMK_CHECK_HIP(hipGetLastError());
   prof_before(kKSpecCombine, s);
-  hipLaunchKernelGGL(spec_combine_kernel<elem_t<V>>, dim3((unsigned)(a.B * a.Hkv * a.kd * a.G)), dim3(128), 0, s,
-                     a);
+  launch_spec_combine<elem_t<V>>(a, (int64_t)a.B * a.Hkv * a.kd * a.G, s);
   prof_after(kKSpecCombine, s);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
@@ -405,7 +440,7 @@ static int decode_paged(const void* q, const void* k_pages, const void* v_pages,
   prof_after(kKSpecPartial, s);
   VMK_CHECK_HIP(hipGetLastError());
   prof_before(kKSpecCombine, s);
-  hipLaunchKernelGGL(spec_combine_kernel<elem_t<V>>, dim3((unsigned)(B * Hq)), dim3(128), 0, s, a);
+  launch_spec_combine<elem_t<V>>(a, B * Hq, s);
   prof_after(kKSpecCombine, s);
   VMK_CHECK_HIP(hipGetLastError());
   return 0;
