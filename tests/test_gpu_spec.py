@@ -24,7 +24,12 @@ CASES = [(dict(B=1, L=8, k=8), "randn", 7), (dict(B=1, L=9, k=1), "randn", 8), (
          (dict(B=1, L=3000, k=16, Hq=64, Hkv=4), "chain", 23),
          # the benchmark configurations at full size (seed 0, as bench.py draws them): C3 is the key-split walk with
          # 8 splits per row group, C4 the row-split walk with 16 splits merged by the combine launch
-         (dict(B=4, L=32768, k=8), "chain", 0), (dict(B=2, L=65536, k=64), "tree_bd", 0)]
+         (dict(B=4, L=32768, k=8), "chain", 0), (dict(B=2, L=65536, k=64), "tree_bd", 0),
+         # 1024 output rows, so the four-rows-per-wave combine merges them, with more partials than it holds in
+         # registers: 33 splits of fp16 partials (more than 32) and, for bf16 inputs, 18 of fp32 partials (more
+         # than 16), both merged in batches
+         (dict(B=1, L=135000, k=64, Hq=16, Hkv=4), "tree_bd", 26),
+         (dict(B=1, L=70000, k=64, Hq=16, Hkv=4, dtype="bf16"), "tree_bd", 27)]
 
 
 def test_mfma32_lane_layout():
