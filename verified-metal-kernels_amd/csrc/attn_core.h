@@ -570,8 +570,8 @@ __device__ __forceinline__ void state_to_slot(char* slot, const RowState& st, in
 }
 
 // Writes one wave's partial for its 32 rows: po[row][d] = O / l in the partial type PT (row stride 128),
-// pml[row] = (m, l).  Rows >= nvalid are skipped.
-template <class PT>
+// pml[row] = (m, l).  Rows >= nvalid are skipped.  kCoherent: agent-coherent stores, for a reader in the same kernel.
+template <bool kCoherent = false, class PT>
 __device__ __forceinline__ void store_partial(PT* po, float* pml, const RowState& st, int lane, int nvalid) {
   const int r = lane & 31, g = lane >> 5;
   const float ltot = st.l + xor32(st.l);
@@ -582,11 +582,18 @@ __device__ __forceinline__ void store_partial(PT* po, float* pml, const RowState
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
       floatx4 v = floatx4{st.o[dt][4 * blk], st.o[dt][4 * blk + 1], st.o[dt][4 * blk + 2], st.o[dt][4 * blk + 3]};
-      store_part4(po + r * 128 + dt * 32 + 8 * blk + 4 * g, v * inv);
+      if constexpr (kCoherent)
+        store_part4_coherent(po + r * 128 + dt * 32 + 8 * blk + 4 * g, v * inv);
+      else
+        store_part4(po + r * 128 + dt * 32 + 8 * blk + 4 * g, v * inv);
     }
   if (g == 0) {
-    pml[2 * r] = st.m;
-    pml[2 * r + 1] = ltot;
+    if constexpr (kCoherent) {
+      store_u64_coherent(pml + 2 * r, __builtin_bit_cast(uint64_t, float2{st.m, ltot}));
+    } else {
+      pml[2 * r] = st.m;
+      pml[2 * r + 1] = ltot;
+    }
   }
 }
 
@@ -923,7 +930,8 @@ constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
 // (c + r) mod 32 (at most two lanes per bank group on the writes, none on the row reads), then stores rows 2i,
 // 2i + 1 per instruction in the partial type PT, as non-temporal stores (the row split's partials are read by a
 // later launch).  Called by every wave of the workgroup (it contains a barrier); rows >= nvalid are not written.
-template <class PT>
+// kCoherent: agent-coherent stores instead, for a reader in the same kernel.
+template <bool kCoherent = false, class PT>
 __device__ __forceinline__ void store_partial_rows(char* smem, PT* po, float* pml, const RowState& st, int wave,
                                                    int lane, int nvalid) {
   __syncthreads();                                          // every wave is done with the ring
@@ -942,12 +950,22 @@ __device__ __forceinline__ void store_partial_rows(char* smem, PT* po, float* pm
   for (int i = 0; i < 16; ++i) {
     const int row = 2 * i + g;
     const floatx4 v = *reinterpret_cast<const floatx4*>(lds + row * 128 + ((r + row) & 31) * 4);
-    if (row < nvalid) store_part4_nt(po + row * 128 + r * 4, v);
+    if (row < nvalid) {
+      if constexpr (kCoherent)
+        store_part4_coherent(po + row * 128 + r * 4, v);
+      else
+        store_part4_nt(po + row * 128 + r * 4, v);
+    }
   }
-  if (g == 0 && r < nvalid) *reinterpret_cast<float2*>(pml + 2 * r) = float2{st.m, ltot};
+  if (g == 0 && r < nvalid) {
+    if constexpr (kCoherent)
+      store_u64_coherent(pml + 2 * r, __builtin_bit_cast(uint64_t, float2{st.m, ltot}));
+    else
+      *reinterpret_cast<float2*>(pml + 2 * r) = float2{st.m, ltot};
+  }
 }
 
-template <int NW, class V = half8, class Src, class QRow, class PT>
+template <int NW, class V = half8, bool kCoherent = false, class Src, class QRow, class PT>
 __device__ __forceinline__ void attend_wg_rows(char* smem, const Src& src, QRow qrow, int nrows, int kbeg,
                                                int ntiles, PT* po, float* pml) {
   static_assert(16 % NW == 0, "the 16 DMA instructions of a tile must split evenly over the waves");
@@ -967,7 +985,7 @@ __device__ __forceinline__ void attend_wg_rows(char* smem, const Src& src, QRow 
       compute_tile_lds(st, qb, smem + (S & 3) * kStageBytes, S < 4 ? tl : tl_hi, src, kbeg + t * kTile, lane);
   });
   static_assert(NW * 32 * 128 * 4 <= kRowsSmemBytes, "the partial's transpose fits in the ring");
-  store_partial_rows(smem, po + (size_t)wave * 32 * 128, pml + wave * 32 * 2, st, wave, lane,
+  store_partial_rows<kCoherent>(smem, po + (size_t)wave * 32 * 128, pml + wave * 32 * 2, st, wave, lane,
                                 nrows - wave * 32);
 }
 

@@ -61,10 +61,34 @@ __device__ __forceinline__ void store_part4_nt(float* p, floatx4 v) {
 __device__ __forceinline__ void store_part4_nt(f16* p, floatx4 v) {
   __builtin_nontemporal_store(half4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]}, reinterpret_cast<half4*>(p));
 }
+// The same as agent-coherent (sc1) stores: they reach the device's coherence point, so another XCD may read them in
+// the same kernel with agent-coherent loads (load_part2_coherent) once the storing waves' counters have drained.
+__device__ __forceinline__ void store_u64_coherent(void* p, uint64_t v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_part4_coherent(float* p, floatx4 v) {
+  store_u64_coherent(p, __builtin_bit_cast(uint64_t, float2{v[0], v[1]}));
+  store_u64_coherent(p + 2, __builtin_bit_cast(uint64_t, float2{v[2], v[3]}));
+}
+__device__ __forceinline__ void store_part4_coherent(f16* p, floatx4 v) {
+  store_u64_coherent(p, __builtin_bit_cast(uint64_t, half4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]}));
+}
 __device__ __forceinline__ float2 load_part2(const float* p) { return *reinterpret_cast<const float2*>(p); }
 __device__ __forceinline__ float2 load_part2(const f16* p) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const h2 v = *reinterpret_cast<const h2*>(p);
+  return float2{(float)v[0], (float)v[1]};
+}
+
+// Agent-coherent (sc1) loads of two partial elements and of an (m, l) pair.
+__device__ __forceinline__ float2 load_part2_coherent(const float* p) {
+  return __builtin_bit_cast(float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ float2 load_part2_coherent(const f16* p) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 v = __builtin_bit_cast(h2, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT));
   return float2{(float)v[0], (float)v[1]};
 }
 

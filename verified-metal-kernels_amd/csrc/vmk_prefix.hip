@@ -13,8 +13,9 @@
 // Launch 3 (prefix_combine_kernel, only when a suffix spans several chunks or there is no prefix): per output row,
 //   the log-sum-exp merge of its prefix and suffix partials.
 // With at most 128 rows per KV head, launches 1 and 2 are one grid (prefix_mixed_kernel; with at most 32 rows and
-// more items than CUs, its prefix items are single-wave units packed 2 or 4 per workgroup) and prefix_merge_kernel
-// does the whole-suffix merges.
+// more items than CUs, its prefix items are single-wave units packed 2 or 4 per workgroup).  Its whole-suffix items
+// wait for their KV head's prefix partials and merge them in the same launch when G <= 4 and there are at most 32
+// prefix chunks (mfuse below); otherwise prefix_merge_kernel does the whole-suffix merges.
 #include "attn_core.h"
 #include "vmk_internal.h"
 
@@ -43,8 +44,59 @@ struct PrefixArgs {
   int fuse;                // 1: suffix items are whole suffixes and merge the (finished) prefix partials themselves
   int merge;               // 1: whole-suffix partials are merged with the prefix partials by prefix_merge_kernel
   int units;               // mixed launch, N*G <= 32: prefix units (one wave each) per workgroup; 0: row blocks
+  int mfuse;               // 1: mixed launch whose whole-suffix items wait for their KV head's prefix partials and
+                           //    merge them themselves (no merge launch)
+  uint32_t* sync;          // mfuse: the sticky timeout flag, then per KV head the prefix arrivals and the finished
+                           //        suffix items (workspace head, zero between calls)
   float sl2;
 };
+
+// The in-kernel merge of a mixed launch (mfuse).  Prefix producers store their partials with agent-coherent stores
+// and, once every wave's stores have completed (the workgroup barrier waits for them), add 1 to their KV head's
+// arrival counter.  A whole-suffix item keeps its partial in LDS, waits until the arrivals of its head reach the
+// head's producer count (nrb_p * nsplit_p), then fetches the prefix rows with agent-coherent loads and merges them
+// with the functions the fused suffix items of the two-launch path use, on the same values, so the output bits are
+// those of the merge launch.  The last suffix item of a head returns both of its counters to zero.  The wait is
+// safe from deadlock: the producers never wait and come first in the grid, so each XCD dispatches them before any
+// suffix item.  It is still bounded: after kPrefixSpinLimit polls the item sets the sticky flag and writes NaN rows,
+// and every later mixed launch on that workspace sees the flag and writes NaN rows at once, until its head is zeroed.
+// Layout, in the counter part of the workspace head (clear of the DSA histograms and barrier lines): the flag, then
+// 128 bytes per KV head (arrivals, then 64 bytes on, finished suffix items).
+constexpr size_t kPrefixSync = kWsCounters + ((size_t)3 << 19);
+constexpr int kPrefixSyncHeads = (int)((((size_t)1 << 19) - 256) / 128);
+constexpr uint32_t kPrefixSpinLimit = 1u << 20;
+__device__ __forceinline__ uint32_t* pfx_arrivals(const PrefixArgs& a, int h) { return a.sync + 64 + 32 * h; }
+__device__ __forceinline__ uint32_t* pfx_finished(const PrefixArgs& a, int h) { return a.sync + 64 + 32 * h + 16; }
+__device__ __forceinline__ uint32_t ld_coherent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool pfx_poisoned(const PrefixArgs& a) { return ld_coherent(a.sync) != 0; }
+
+// A prefix producer of KV head h has stored its partial: every wave of the workgroup (kWave: only the calling wave,
+// a unit) waits until its stores have completed, then one lane counts the arrival.
+template <bool kWave>
+__device__ __forceinline__ void pfx_arrive(const PrefixArgs& a, int h) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (!kWave) __syncthreads();
+  if ((kWave ? (threadIdx.x & 63) : threadIdx.x) == 0)
+    __hip_atomic_fetch_add(pfx_arrivals(a, h), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Thread 0 of a suffix item: waits for the prefix partials of KV head h; false when it gave up or the flag is set
+// (poisoned: the flag as read when the item started).
+__device__ __forceinline__ bool pfx_wait(const PrefixArgs& a, int h, bool poisoned) {
+  if (poisoned) return false;
+  const uint32_t need = (uint32_t)(a.nrb_p * a.nsplit_p);
+  for (uint32_t spin = 0;; ++spin) {
+    if (ld_coherent(pfx_arrivals(a, h)) >= need) return true;
+    if ((spin & 31) == 31 && pfx_poisoned(a)) return false;
+    if (spin >= kPrefixSpinLimit) {
+      __hip_atomic_fetch_or(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
 
 struct RangeSrc {
   const f16* kbase;
@@ -153,16 +205,19 @@ struct PrefixRow {
   float2 v[kPrefetchSplits];
 };
 
-template <class PT>
+template <class PT, bool kCoherent = false>
 __device__ __forceinline__ void prefetch_prefix_row(const PrefixArgs& a, PrefixRow& pr, int n, int h, int gg,
                                                     int lane) {
   const int np = a.nsplit_p, rows_p = 32 * a.WRp;
   const int prow = n * a.G + gg, rb = prow / rows_p, rl = prow % rows_p;
   const size_t pbase = ((size_t)h * a.nrb_p + rb) * a.nsplit_p * rows_p + rl;
-  pr.ml = *reinterpret_cast<const float2*>(a.pml_p + (pbase + (size_t)min(lane, np - 1) * rows_p) * 2);
+  const float* mlp = a.pml_p + (pbase + (size_t)min(lane, np - 1) * rows_p) * 2;
+  pr.ml = kCoherent ? load_part2_coherent(mlp) : *reinterpret_cast<const float2*>(mlp);
 #pragma unroll
-  for (int j = 0; j < kPrefetchSplits; ++j)
-    pr.v[j] = load_part2(prefix_po<PT>(a) + (pbase + (size_t)min(j, np - 1) * rows_p) * 128 + 2 * lane);
+  for (int j = 0; j < kPrefetchSplits; ++j) {
+    const PT* vp = prefix_po<PT>(a) + (pbase + (size_t)min(j, np - 1) * rows_p) * 128 + 2 * lane;
+    pr.v[j] = kCoherent ? load_part2_coherent(vp) : load_part2(vp);
+  }
 }
 
 // Final output of row gg of request n, KV head h, from the suffix partial in LDS and the prefetched prefix row.
@@ -191,6 +246,25 @@ __device__ __forceinline__ void merge_prefetched_row(const PrefixArgs& a, const 
   out[1] = (E)(num.y / den);
 }
 
+// Row gg of request n, KV head h, as NaN (the mixed launch's merge gave up: the workspace's flag is set).
+template <class E>
+__device__ __forceinline__ void pfx_nan_row(const PrefixArgs& a, int n, int h, int gg, int lane) {
+  E* out = reinterpret_cast<E*>(a.out) + ((size_t)n * a.Hq + h * a.G + gg) * 128 + 2 * lane;
+  out[0] = (E)__builtin_nanf("");
+  out[1] = (E)__builtin_nanf("");
+}
+
+// A suffix item of KV head h is done with its head's counters; the last of the head's N items clears them.
+__device__ __forceinline__ void pfx_finish(const PrefixArgs& a, int h) {
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(pfx_finished(a, h), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == (uint32_t)(a.N * a.nsplit_s) - 1) {
+      __hip_atomic_store(pfx_arrivals(a, h), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(pfx_finished(a, h), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 // The walk and merge of a suffix item over key source src (keys [kbeg, src.kend)).
 template <class V, class Src>
 __device__ __forceinline__ void suffix_walk(const PrefixArgs& a, char* smem, const Src& src, int n, int h, int nh,
@@ -198,7 +272,7 @@ __device__ __forceinline__ void suffix_walk(const PrefixArgs& a, char* smem, con
   const int ntiles = max(0, (src.kend - kbeg + kTile - 1) / kTile);
   auto qrow = [&](int r) { return a.q + ((size_t)n * a.Hq + h * a.G + r) * 128; };
   typedef part_t<elem_t<V>> PT;
-  if (!a.fuse) {
+  if (!a.fuse && !a.mfuse) {
     const size_t pi = (size_t)nh * a.nsplit_s + split;
     attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, reinterpret_cast<PT*>(a.po_s) + pi * 32 * 128,
                           a.pml_s + pi * 32 * 2);
@@ -208,6 +282,24 @@ __device__ __forceinline__ void suffix_walk(const PrefixArgs& a, char* smem, con
   PT* lpo = reinterpret_cast<PT*>(smem + kFuseOff);
   float* lpml = reinterpret_cast<float*>(smem + kFuseMlOff);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (a.mfuse) {                                            // mixed launch: the prefix partials arrive meanwhile
+    __shared__ int ready;
+    const bool poisoned = threadIdx.x == 0 && pfx_poisoned(a);   // read now, used after the walk
+    attend_wg<1, 4, 2, V>(smem, src, qrow, a.G, kbeg, ntiles, lpo, lpml);
+    if (threadIdx.x == 0) ready = pfx_wait(a, h, poisoned);
+    __syncthreads();                                        // the partial in LDS, and the wait's outcome
+    if (wave < a.G) {
+      if (ready) {
+        PrefixRow pr;
+        prefetch_prefix_row<PT, true>(a, pr, n, h, wave, lane);
+        merge_prefetched_row<elem_t<V>>(a, pr, lpo, lpml, n, h, wave, lane);
+      } else {
+        pfx_nan_row<elem_t<V>>(a, n, h, wave, lane);
+      }
+    }
+    pfx_finish(a, h);
+    return;
+  }
   if (a.G <= 4 && a.nsplit_p <= kPrefetchSplits) {          // wave w finishes row w
     PrefixRow pr;
     if (wave < a.G) prefetch_prefix_row<PT>(a, pr, n, h, wave, lane);
@@ -238,7 +330,7 @@ __device__ __forceinline__ void suffix_item(const PrefixArgs& a, char* smem, int
   const int n = nh / a.Hkv, h = nh % a.Hkv;
   const int kbeg = split * a.chunk_s;
   if (!a.order) sn = suffix_len(a, n);
-  if (kbeg >= sn && !a.fuse && !a.merge) return;        // whole workgroup: nothing of this suffix is here
+  if (kbeg >= sn && !a.fuse && !a.merge && !a.mfuse) return;   // whole workgroup: nothing of this suffix is here
   const int kend = min(sn, kbeg + a.chunk_s);
   if constexpr (kPaged != kContig) {
     const int* table = a.suffix_pages + (size_t)n * a.max_sp;
@@ -297,7 +389,7 @@ __device__ void build_suffix_order(const PrefixArgs& a, uint32_t* cnt /* LDS, 25
 
 // Prefix item (KV head h, row block rb, prefix chunk): NW waves own 32 of the N*G rows each and share one LDS ring,
 // so the prefix chunk is streamed from HBM once per 32*NW rows.
-template <int NW, int kPaged, class V>
+template <int NW, int kPaged, class V, bool kMF = false>
 __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem, int item) {
   const int split = item % a.nsplit_p;
   const int rb = (item / a.nsplit_p) % a.nrb_p;
@@ -308,7 +400,7 @@ __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem
   const int row0 = rb * NW * 32;
   const size_t rows_wg = 32 * NW;
   auto walk = [&](const auto& src) {
-    attend_wg_rows<NW, V>(smem, src,
+    attend_wg_rows<NW, V, kMF>(smem, src,
                        [&](int r) {
                          const int qr = row0 + r, n = qr / a.G, gg = qr % a.G;
                          return a.q + ((size_t)n * a.Hq + h * a.G + gg) * 128;
@@ -328,6 +420,7 @@ __device__ __forceinline__ void prefix_rows_item(const PrefixArgs& a, char* smem
     src.kend = kend;
     walk(src);
   }
+  if constexpr (kMF) pfx_arrive<false>(a, h);
 }
 
 template <int NW, int kPaged, class V>
@@ -342,7 +435,7 @@ __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
 // arithmetic is that of a row-block wave (the same tiles in the same order through the same tile function), so the
 // output bits do not depend on which form ran; several units share a workgroup so that the grid stays within one
 // dispatch round when the row-block grid would not.
-template <int NS, int kPaged, class V>
+template <int NS, int kPaged, class V, bool kMF>
 __device__ __forceinline__ void prefix_unit(const PrefixArgs& a, char* smem, int u, int w) {
   const int lane = threadIdx.x & 63;
   const int split = u % a.nsplit_p, h = u / a.nsplit_p;            // one row block (nrb_p == 1)
@@ -371,15 +464,17 @@ __device__ __forceinline__ void prefix_unit(const PrefixArgs& a, char* smem, int
     walk(src);
   }
   const size_t rows_wg = 32 * a.WRp;
-  store_partial(reinterpret_cast<part_t<elem_t<V>>*>(a.po_p) + (size_t)u * rows_wg * 128,
-                a.pml_p + (size_t)u * rows_wg * 2, st, lane, nrows);
+  store_partial<kMF>(reinterpret_cast<part_t<elem_t<V>>*>(a.po_p) + (size_t)u * rows_wg * 128,
+                     a.pml_p + (size_t)u * rows_wg * 2, st, lane, nrows);
+  if constexpr (kMF) pfx_arrive<true>(a, h);
 }
 
 // Both item kinds in one grid when a KV head has at most 128 rows: prefix items first (row blocks of 4 waves
-// sharing a ring, or a.units single-wave units per workgroup), then suffix items writing their partials.  No item
-// depends on another.
+// sharing a ring, or a.units single-wave units per workgroup), then suffix items.  kMF: whole-suffix items wait for
+// their head's prefix partials and write the outputs (a.mfuse); otherwise no item depends on another and the suffix
+// items write partials for the merge launch.
 constexpr int kMixedSmemBytes = kRowsSmemBytes > kAttnSmemBytes ? kRowsSmemBytes : kAttnSmemBytes;
-template <int kPaged, class V>
+template <int kPaged, class V, bool kMF>
 __global__ __launch_bounds__(256) void prefix_mixed_kernel(PrefixArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kMixedSmemBytes];
   const int upw = a.units;
@@ -387,15 +482,15 @@ __global__ __launch_bounds__(256) void prefix_mixed_kernel(PrefixArgs a) {
   if ((int)blockIdx.x >= npw) {
     suffix_item<kPaged, V>(a, smem, blockIdx.x - npw);
   } else if (upw == 0) {
-    prefix_rows_item<4, kPaged, V>(a, smem, blockIdx.x);
+    prefix_rows_item<4, kPaged, V, kMF>(a, smem, blockIdx.x);
   } else {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), u = (int)blockIdx.x * upw + w;
     if (w < upw && u < a.n_prefix_items) {
       static_assert(2 * 4 * kStageBytes <= kMixedSmemBytes && 4 * 2 * kStageBytes <= kMixedSmemBytes, "unit rings");
       if (upw == 2)
-        prefix_unit<4, kPaged, V>(a, smem, u, w);                   // the whole 128-key chunk in flight
+        prefix_unit<4, kPaged, V, kMF>(a, smem, u, w);              // the whole 128-key chunk in flight
       else
-        prefix_unit<2, kPaged, V>(a, smem, u, w);
+        prefix_unit<2, kPaged, V, kMF>(a, smem, u, w);
     }
   }
 }
@@ -522,7 +617,11 @@ static int prefix_launch(PrefixArgs& a, const void* q, void* out, const void* sl
   // The schedule order is built by the prefix launch, so only when that runs before the suffix items.
   a.order = (ragged && p.n_prefix_items > 0 && !mixed) ? (int2*)align_up(a.pml_s + p.pml_s, 256) : nullptr;
   a.fuse = p.fuse && !mixed ? 1 : 0;
-  a.merge = p.fuse && mixed ? 1 : 0;
+  // Mixed with whole suffixes: the suffix items merge in the same launch when each wave finishes one row from
+  // registers (the form the two-launch fused path uses); else a merge launch follows.
+  a.mfuse = p.fuse && mixed && Hq / Hkv <= 4 && p.nsplit_p <= kPrefetchSplits && Hkv <= kPrefixSyncHeads ? 1 : 0;
+  a.merge = p.fuse && mixed && !a.mfuse ? 1 : 0;
+  a.sync = (uint32_t*)((char*)workspace + kPrefixSync);
   a.units = mixed ? p.units : 0;
   a.N = (int)N; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.P = (int)P; a.S = (int)S;
   a.WRp = p.WRp; a.nrb_p = p.nrb_p; a.nsplit_p = p.nsplit_p; a.chunk_p = p.chunk_p;
@@ -530,7 +629,10 @@ static int prefix_launch(PrefixArgs& a, const void* q, void* out, const void* sl
   a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
   prof_before(kKPrefixPartial, s);
   if (mixed) {
-    hipLaunchKernelGGL((prefix_mixed_kernel<kPaged, V>), dim3((unsigned)p.n_wg_mixed), dim3(256), 0, s, a);
+    if (a.mfuse)
+      hipLaunchKernelGGL((prefix_mixed_kernel<kPaged, V, true>), dim3((unsigned)p.n_wg_mixed), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((prefix_mixed_kernel<kPaged, V, false>), dim3((unsigned)p.n_wg_mixed), dim3(256), 0, s, a);
     VMK_CHECK_HIP(hipGetLastError());
   } else {
     if (p.n_prefix_items > 0) {
@@ -549,7 +651,7 @@ static int prefix_launch(PrefixArgs& a, const void* q, void* out, const void* sl
     hipLaunchKernelGGL(prefix_merge_kernel<elem_t<V>>, dim3((unsigned)(N * Hkv)), dim3(256), 0, s, a);
     prof_after(kKPrefixCombine, s);
     VMK_CHECK_HIP(hipGetLastError());
-  } else if (!a.fuse) {
+  } else if (!a.fuse && !a.mfuse) {
     prof_before(kKPrefixCombine, s);
     hipLaunchKernelGGL(prefix_combine_kernel<elem_t<V>>, dim3((unsigned)(N * Hq)), dim3(128), 0, s, a);
     prof_after(kKPrefixCombine, s);
