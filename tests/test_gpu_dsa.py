@@ -42,6 +42,9 @@ def test_dsa_parity(shape, dist, seed):
     em, ea = nerr(o, r)
     print(f"  err max {em:.3e} mean {ea:.3e}")
     assert em <= 1e-2
+    # The attention workgroups' arrival counters (and the histograms) are back to zero after the call.
+    from vmk import api
+    assert int(api.workspace(0, "cuda")[: 4 << 20].count_nonzero().item()) == 0
 
 
 def test_dsa_kernel_module_matches_entry_points():
