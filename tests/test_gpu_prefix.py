@@ -100,3 +100,33 @@ def test_prefix_rows_empty_suffixes():
     em, _ = nerr(o, r)
     assert em <= 1e-2
     assert _head_is_zero()
+
+
+def test_prefix_in_launch_merge_flag():
+    """At most 128 rows per KV head with G <= 4 and one suffix chunk, the suffix workgroups wait (bounded) for their
+    KV head's prefix partials inside the one launch.  A wait that gives up sets a sticky flag in the workspace head,
+    and every later such call on that workspace writes NaN rows at once instead of waiting.  The flag is set here
+    from the host (no wait is made to give up): the call writes NaN rows and the flag stays set (the arrival
+    counters may be left behind too, as the suffix workgroups no longer wait for them); once the head is zeroed,
+    the same call is exact again."""
+    import prefix_mi355x
+    from vmk import api
+    # The flag word: workspace byte 2 MiB (the head's counter part) + 1.5 MiB (the prefix op's block), as in
+    # vmk_prefix.hip (kPrefixSync).
+    flag = (2 << 20) + (3 << 19)
+    inp = prefix.make_inputs(dict(N=8, P=2048, S=256), seed=130, device="cuda")
+    r = oracle.prefix.ref64(**inp)
+    out = prefix_mi355x.kernel(**inp)
+    torch.cuda.synchronize()
+    assert nerr(out.float().cpu().numpy().astype(np.float64), r)[0] <= 1e-2
+    ws = api.workspace(0, "cuda")
+    ws[flag:flag + 4] = torch.tensor([1, 0, 0, 0], dtype=torch.uint8, device="cuda")
+    out = prefix_mi355x.kernel(**inp)
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(out.float()).all())
+    assert int(ws[flag].item()) == 1, "the flag stays set"
+    ws[: 4 << 20].zero_()
+    out = prefix_mi355x.kernel(**inp)
+    torch.cuda.synchronize()
+    assert nerr(out.float().cpu().numpy().astype(np.float64), r)[0] <= 1e-2
+    assert _head_is_zero()
