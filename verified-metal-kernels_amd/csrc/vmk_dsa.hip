@@ -40,7 +40,7 @@ struct DsaArgs {
   int* idx;             // (B, 2048)
   int* cnt;             // (B,)
   f16* out;             // (B, 128, 512)
-  uint32_t* hist;       // (B, 8192)
+  uint32_t* hist;       // (B, hcopies, 8192): the fine histogram of request b is the sum of its hcopies copies
   float* scores;        // (B, Ls)
   void* po;             // (B, 4, kNChunk, 32, 512) normalised O of type part_t
   float* pml;           // (B, 4, kNChunk, 32, 2)
@@ -52,6 +52,7 @@ struct DsaArgs {
   int B, L, nb;         // nb = scan slices per request
   int Ls;               // row stride of scores and the scan lists: nb * kScanWG
   int hist_in_head;     // 1: hist lives in the zero-invariant workspace head (no zero-fill launch needed)
+  int hcopies;          // copies of each request's fine histogram (workgroup w of a request adds into copy w % hcopies)
   int fused_select;     // 1: every attention workgroup selects its own chunk (decode entry); 0: idx/cnt are inputs
   int scores_only;      // 1: the indexer writes scores (row stride Ls) and no histograms (vmk_dsa_indexer)
   const float* scores_in;  // (B, L) caller scores for vmk_dsa_topk, copied into `scores` by dsa_scores_hist_kernel
@@ -68,6 +69,14 @@ __device__ __forceinline__ uint32_t fkey(float f) {
 
 __device__ __forceinline__ int valid_len(const DsaArgs& a, int b) {
   return a.lens ? min(max(a.lens[b], 0), a.L) : a.L;
+}
+
+// Copy c of request b's fine histogram.  The workgroups of a request add their counts into hcopies copies instead
+// of one, so that fewer of them add into the same words at once (device-scope adds to one word are serialised: in a
+// microbenchmark, 64 workgroups adding into the same 300 bins take about 4.5 us longer than an empty launch, into 8
+// copies 1.4 us); a reader sums the copies, which gives the same integers.
+__device__ __forceinline__ uint32_t* fine_hist(const DsaArgs& a, int b, int c) {
+  return a.hist + ((size_t)b * a.hcopies + c) * kBins;
 }
 
 // ------------------------------------------------------------------------------------------------ indexer
@@ -265,7 +274,7 @@ __device__ __forceinline__ void indexer_item(const DsaArgs& a, int bx, int b, ch
   }
   if (a.scores_only) return;                                // uniform: no histograms to add
   __syncthreads();
-  uint32_t* gh = a.hist + (size_t)b * kBins;
+  uint32_t* gh = fine_hist(a, b, bx % a.hcopies);
   for (int i = tid; i < kBins / 2; i += 64 * NW) {
     const uint32_t c = hist2[i];
     if (c & 0xFFFFu) atomicAdd(&gh[2 * i], c & 0xFFFFu);
@@ -320,7 +329,7 @@ __global__ __launch_bounds__(256) void dsa_scores_hist_kernel(DsaArgs a) {
     }
   }
   __syncthreads();
-  uint32_t* gh = a.hist + (size_t)b * kBins;
+  uint32_t* gh = fine_hist(a, b, blockIdx.x % a.hcopies);
   for (int i = tid; i < kBins / 2; i += 256) {
     const uint32_t c = hist2[i];
     if (c & 0xFFFFu) atomicAdd(&gh[2 * i], c & 0xFFFFu);
@@ -365,8 +374,10 @@ __device__ __forceinline__ void select_scan_item(const DsaArgs& a, int wg, int b
   __syncthreads();
   find_threshold<256, kCBins>(cnt, kTopK, red, thr);
   if (tid < 64) {
-    const uint32_t* fine = a.hist + (size_t)b * kBins + coarse_bin_clamped(thr[0]) * 32;
-    const uint32_t v = tid < 32 ? fine[31 - tid] : 0u;      // lane i: fine bin 31 - i (top first)
+    const int f0 = coarse_bin_clamped(thr[0]) * 32;
+    uint32_t v = 0u;                                         // lane i: fine bin 31 - i (top first)
+    if (tid < 32)
+      for (int c = 0; c < a.hcopies; ++c) v += fine_hist(a, b, c)[f0 + 31 - tid];
     const uint32_t x = wave_incl_scan(v);                    // inclusive prefix from the top
     if (tid < 32 && fine_hit(x, v, thr[1])) b1s = fine_bin(thr[0], tid);
   }
@@ -628,8 +639,10 @@ __device__ int select_window(const DsaArgs& a, SelectShared<CAND>& sh, int b, in
 // coarse bins they make up, by nthr threads.
 __device__ __forceinline__ void clear_histograms(const DsaArgs& a, int b, int fine0, int fine1, int tid, int nthr) {
   if (a.L <= kTopK) return;
-  uint32_t* gh = a.hist + (size_t)b * kBins;
-  for (int i = fine0 + tid; i < fine1; i += nthr) gh[i] = 0;
+  for (int c = 0; c < a.hcopies; ++c) {
+    uint32_t* gh = fine_hist(a, b, c);
+    for (int i = fine0 + tid; i < fine1; i += nthr) gh[i] = 0;
+  }
   for (int i = fine0 / 32 + tid; i < fine1 / 32; i += nthr) a.chist[(size_t)b * kCBins + i] = 0;
 }
 
@@ -649,8 +662,10 @@ __global__ __launch_bounds__(1024) void dsa_select_final_kernel(DsaArgs a) {
 template <int NT>
 __device__ __forceinline__ void hist_zero_item(const DsaArgs& a, int b) {
   static_assert(NT >= kCBins, "one coarse bin per thread");
-  uint32_t* gh = a.hist + (size_t)b * kBins;
-  for (int i = threadIdx.x; i < kBins; i += NT) gh[i] = 0;
+  for (int c = 0; c < a.hcopies; ++c) {
+    uint32_t* gh = fine_hist(a, b, c);
+    for (int i = threadIdx.x; i < kBins; i += NT) gh[i] = 0;
+  }
   if (threadIdx.x < kCBins) a.chist[(size_t)b * kCBins + threadIdx.x] = 0;
 }
 
@@ -1087,6 +1102,7 @@ constexpr size_t kSyncOffset = kWsCounters + ((size_t)1 << 20);
 struct DsaLayout {
   size_t hist, chist, scores, glist, ekey, epos, gcnt, ecnt, po, pml, total;
   bool hist_in_head;
+  int hcopies;
 };
 
 // The per-request histograms live in the zero-invariant workspace head when they fit (B <= 64: fine histograms in
@@ -1094,8 +1110,15 @@ struct DsaLayout {
 static DsaLayout dsa_layout(int64_t B, int64_t L) {
   DsaLayout l;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
-  const size_t hist_bytes = (size_t)B * kBins * 4;
+  // Fine-histogram copies per request: two while they fit in the head's histogram part (B <= 32; C5: 42.3 us against
+  // 43.7 with 8 copies, 44.5 with one, and 46.6 with 16, whose clearing costs more than it saves), else one.
+  l.hcopies = (int)std::max<int64_t>(1, std::min<int64_t>(2, (int64_t)(kWsCounters / ((size_t)B * kBins * 4))));
+  size_t hist_bytes = (size_t)B * l.hcopies * kBins * 4;
   l.hist_in_head = hist_bytes <= kWsCounters;
+  if (!l.hist_in_head) {
+    l.hcopies = 1;
+    hist_bytes = (size_t)B * kBins * 4;
+  }
   size_t o = kWsHead;
   l.hist = l.hist_in_head ? 0 : o;
   if (!l.hist_in_head) o = up(o + hist_bytes);
@@ -1135,6 +1158,7 @@ static int dsa_fill_args(DsaArgs& a, const void* q, const void* kv, const void* 
   a.nb = (int)((L + kScanWG - 1) / kScanWG);
   a.Ls = a.nb * kScanWG;
   a.hist_in_head = lay.hist_in_head ? 1 : 0;
+  a.hcopies = lay.hcopies;
   a.fused_select = 0;
   a.scores_only = 0;
   a.scores_in = nullptr;
