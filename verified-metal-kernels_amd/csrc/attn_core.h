@@ -437,16 +437,33 @@ __device__ __forceinline__ void ring_walk(char* ring, const Src& src, int kbeg, 
     issue(ring + S * kStageBytes, S);
     return true;
   };
-  unroll_while<0, NS - 2>(pre);
+  // Tiles requested before the first pair: with four waves (the mixed prefix launch's short walks of 128 rows) only
+  // two, so that the first tiles land sooner (C1 12.16 against 12.49 us); the rest of the ring is requested at the
+  // first barrier.  Eight waves request NS - 2 at once (fewer gave no gain at C2 and C4).
+  constexpr int KI = NW == 4 ? 2 : NS - 2;
+  unroll_while<0, KI>(pre);
   for (int t0 = 0; t0 < ntiles; t0 += NS) {
     auto step = [&](auto P) {
       constexpr int S = 2 * P;
       const int t = t0 + S;
       if (t >= ntiles) return false;
-      wait_vmem_dyn(DPW * max(0, min(NS - 4, ntiles - 2 - t)));
-      lds_barrier();
-      if (t + NS - 2 < ntiles) issue(ring + ((S + NS - 2) % NS) * kStageBytes, t + NS - 2);
-      if (t + NS - 1 < ntiles) issue(ring + ((S + NS - 1) % NS) * kStageBytes, t + NS - 1);
+      bool first = false;                                   // first pair: the tiles after the KI requested
+      if constexpr (KI < NS - 2) first = S == 0 && t == 0;
+      if (first) {
+        wait_vmem_dyn(DPW * max(0, min(KI, ntiles) - 2));
+        lds_barrier();
+        auto late = [&](auto S2) {
+          if (S2 >= ntiles) return false;
+          issue(ring + S2 * kStageBytes, S2);
+          return true;
+        };
+        unroll_while<KI, NS>(late);
+      } else {
+        wait_vmem_dyn(DPW * max(0, min(NS - 4, ntiles - 2 - t)));
+        lds_barrier();
+        if (t + NS - 2 < ntiles) issue(ring + ((S + NS - 2) % NS) * kStageBytes, t + NS - 2);
+        if (t + NS - 1 < ntiles) issue(ring + ((S + NS - 1) % NS) * kStageBytes, t + NS - 1);
+      }
       compute(std::integral_constant<int, S>(), t);
       if (t + 1 < ntiles) compute(std::integral_constant<int, S + 1>(), t + 1);
       return true;
