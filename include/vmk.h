@@ -54,7 +54,8 @@ int vmk_spec_verify(const void* q, const void* k, const void* v, const void* mas
 /* Allocation-free form of vmk_spec_verify.  No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same inputs,
  * output and result as vmk_spec_verify (same kernels and plan, so the same bits); the partials go to a static
- * device array of vmk_spec_noalloc_max_bytes() bytes (32 MiB) that each GPU holds until the process ends, so it
+ * device array of vmk_spec_noalloc_max_bytes() bytes (32 MiB) that each GPU holds from this entry point's first
+ * call on it until the process ends (the array has a code object of its own, loaded on that first call), so it
  * calls no hipMalloc/hipFree.  Shapes whose partials exceed it are rejected (return 1, nothing launched).  All calls
  * on one GPU share that GPU's array: calls that overlap on one GPU (two streams or threads) race. */
 size_t vmk_spec_noalloc_max_bytes(void);

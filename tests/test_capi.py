@@ -244,8 +244,9 @@ def test_dsa_wrappers_check_every_shape_before_the_device():
 
 
 def test_failed_call_sets_the_workspace_aside(monkeypatch):
-    """A call that fails leaves the cached workspace retired (kept alive, not reused): the next call gets a fresh,
-    zeroed one.  Forced on the CPU by a failing stand-in for the library call."""
+    """A call that fails leaves the cached workspace out of use (the next call gets a fresh, zeroed one), and kept
+    alive when the device then reports an error too.  Forced on the CPU by failing stand-ins for the library call and
+    for the device drain, so the test means the same with or without a GPU."""
     import torch
     from vmk import api, lib
     buf = torch.zeros(16, dtype=torch.uint8)
@@ -254,7 +255,11 @@ def test_failed_call_sets_the_workspace_aside(monkeypatch):
 
     def fail(*a):
         raise lib.VmkError("launch failed")
+
+    def drain_fails(key):
+        raise RuntimeError("device error")
     monkeypatch.setattr(lib, "call", fail)
+    monkeypatch.setattr(api, "_drain", drain_fails)
     with pytest.raises(lib.VmkError):
         api._launch("vmk_spec_verify", buf)
     assert buf.device.index not in api._ws and api._retired == [buf]

@@ -21,6 +21,12 @@ void prof_after(int kernel_id, hipStream_t s);
 // Layout of the head: [0, 2 MiB) histograms, [2 MiB, 4 MiB) counters.
 constexpr size_t kWsHead = (size_t)4 << 20;
 constexpr size_t kWsCounters = (size_t)2 << 20;
+// The spec half of the allocation-free entry point (vmk_spec.hip): argument checks and the bytes of partials a shape
+// needs (no HIP call), then the launches with the partials at `partials`.
+int spec_noalloc_need(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
+                      int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, size_t* need);
+int spec_noalloc_launch(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
+                        int64_t kd, int64_t Hq, int64_t Hkv, int64_t L, int64_t W, void* partials, hipStream_t s);
 // Compute units of the target GPU (MI355X): plans size their grids to one dispatch round of one workgroup per CU.
 constexpr int kDeviceCUs = 256;
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

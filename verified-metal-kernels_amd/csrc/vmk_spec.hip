@@ -6,7 +6,6 @@
 #include "attn_core.h"
 #include "vmk_internal.h"
 
-#include <mutex>
 
 namespace vmk {
 
@@ -461,67 +460,25 @@ VMK_DECODE_PAGED_ENTRY(vmk_decode_paged_nhd_bf16, true, bf16x8)
 #undef VMK_DECODE_PAGED_ENTRY
 
 // ---------------------------------------------------------------------------------------------- allocation-free
-// vmk_spec_verify without a workspace argument, for callers that cannot allocate device memory.  The partials go to
-// `scratch`, a file-scope device array that every GPU the library is loaded on holds until the process ends.  Host
-// code never passes the array's name to a kernel (on the host it is only a stand-in for the symbol): the device
-// address comes from hipGetSymbolAddress, looked up once per device with that device current, and kept per device.
-// Every call on one GPU uses that GPU's one array, so calls that overlap on a GPU (two streams, two host threads)
-// race; the array keeps the last call's partials, and no part of it must start at zero (every partial the combine
-// reads is written first).
+// The spec half of vmk_spec_verify_noalloc.  The entry point and its static scratch live in vmk_noalloc.hip, a code
+// object of their own, which the HIP runtime loads onto a device (and so allocates the scratch on) only when the
+// scratch is first looked up there.
 namespace vmk {
-constexpr size_t kScratchBytes = (size_t)32 << 20;   // fp16 partials of every bench shape (C4: 16.5 MiB)
-constexpr int kScratchDevices = 64;
-static __device__ __align__(256) unsigned char scratch[kScratchBytes];
-static void* g_scratch_ptr[kScratchDevices];
-static std::mutex g_scratch_mu;
-
-// Device address of `scratch` on the device that `stream` belongs to (the current device for the null stream),
-// looked up on the first call on that device with that device made current, and kept per device; 0 on success.
-static int scratch_address(hipStream_t stream, void** ptr) {
-  int dev = -1;
-  if (stream) {
-    VMK_CHECK_HIP(hipStreamGetDevice(stream, &dev));
-  } else {
-    VMK_CHECK_HIP(hipGetDevice(&dev));
-  }
-  VMK_CHECK(dev >= 0 && dev < kScratchDevices, "device index beyond the per-device scratch table");
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    int cur = -1;
-    VMK_CHECK_HIP(hipGetDevice(&cur));
-    if (cur != dev) VMK_CHECK_HIP(hipSetDevice(dev));
-    void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (cur != dev) VMK_CHECK_HIP(hipSetDevice(cur));
-    VMK_CHECK_HIP(e);
-    VMK_CHECK(p != nullptr && ((uintptr_t)p & 255u) == 0, "scratch symbol address missing or misaligned");
-    g_scratch_ptr[dev] = p;
-  }
-  *ptr = g_scratch_ptr[dev];
+int spec_noalloc_need(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
+                      int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L, int64_t W, size_t* need) {
+  if (int rc = spec_check_args(q, k, v, mask_words, out, B, kd, Hq, Hkv, D, L, W)) return rc;
+  *need = spec_partials_bytes<half8>(spec_plan(B, kd, Hq, Hkv, L));
   return 0;
 }
-}  // namespace vmk
 
-extern "C" size_t vmk_spec_noalloc_max_bytes(void) { return vmk::kScratchBytes; }
-
-extern "C" int vmk_spec_verify_noalloc(const void* q, const void* k, const void* v, const void* mask_words, void* out,
-                                       int64_t B, int64_t kd, int64_t Hq, int64_t Hkv, int64_t D, int64_t L,
-                                       int64_t W, void* stream) {
-  // Every check comes before the first HIP call: a rejected call touches no device.
-  if (int rc = spec_check_args(q, k, v, mask_words, out, B, kd, Hq, Hkv, D, L, W)) return rc;
+int spec_noalloc_launch(const void* q, const void* k, const void* v, const void* mask_words, void* out, int64_t B,
+                        int64_t kd, int64_t Hq, int64_t Hkv, int64_t L, int64_t W, void* partials, hipStream_t s) {
   const SpecPlan p = spec_plan(B, kd, Hq, Hkv, L);
-  const size_t need = spec_partials_bytes<half8>(p);
-  if (need > kScratchBytes) {
-    set_error("vmk_spec_verify_noalloc: this shape needs %zu bytes of partials, more than the %zu bytes of static "
-              "scratch; call vmk_spec_verify with a workspace instead", need, kScratchBytes);
-    return 1;
-  }
-  void* partials = nullptr;
-  if (int rc = scratch_address((hipStream_t)stream, &partials)) return rc;
   SpecArgs a;
   a.q = (const f16*)q; a.k = (const f16*)k; a.v = (const f16*)v; a.bits = (const uint32_t*)mask_words;
   a.lens = nullptr;
   a.out = (f16*)out;
   a.B = (int)B; a.kd = (int)kd; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.L = (int)L; a.W = (int)W;
-  return spec_launch<half8>(a, p, partials, (hipStream_t)stream);
+  return spec_launch<half8>(a, p, partials, s);
 }
+}  // namespace vmk
