@@ -78,6 +78,18 @@ __device__ __forceinline__ int valid_len(const DsaArgs& a, int b) {
 __device__ __forceinline__ uint32_t* fine_hist(const DsaArgs& a, int b, int c) {
   return a.hist + ((size_t)b * a.hcopies + c) * kBins;
 }
+constexpr int kMaxFineCopies = 2;
+// Bin `bin` of request b's fine histogram, summed over its copies.  Every copy's word is loaded before the first is
+// added: a loop over the run-time count would wait for each load before issuing the next.
+__device__ __forceinline__ uint32_t fine_bin_sum(const DsaArgs& a, int b, int bin) {
+  uint32_t v[kMaxFineCopies];
+#pragma unroll
+  for (int c = 0; c < kMaxFineCopies; ++c) v[c] = fine_hist(a, b, min(c, a.hcopies - 1))[bin];
+  uint32_t t = v[0];
+#pragma unroll
+  for (int c = 1; c < kMaxFineCopies; ++c) t += c < a.hcopies ? v[c] : 0u;
+  return t;
+}
 
 // ------------------------------------------------------------------------------------------------ indexer
 // Block-wide exclusive prefix sum of v over thread ids (NT threads); *total receives the sum of all v.  The block
@@ -376,8 +388,7 @@ __device__ __forceinline__ void select_scan_item(const DsaArgs& a, int wg, int b
   if (tid < 64) {
     const int f0 = coarse_bin_clamped(thr[0]) * 32;
     uint32_t v = 0u;                                         // lane i: fine bin 31 - i (top first)
-    if (tid < 32)
-      for (int c = 0; c < a.hcopies; ++c) v += fine_hist(a, b, c)[f0 + 31 - tid];
+    if (tid < 32) v = fine_bin_sum(a, b, f0 + 31 - tid);
     const uint32_t x = wave_incl_scan(v);                    // inclusive prefix from the top
     if (tid < 32 && fine_hit(x, v, thr[1])) b1s = fine_bin(thr[0], tid);
   }
@@ -1112,7 +1123,8 @@ static DsaLayout dsa_layout(int64_t B, int64_t L) {
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   // Fine-histogram copies per request: two while they fit in the head's histogram part (B <= 32; C5: 42.3 us against
   // 43.7 with 8 copies, 44.5 with one, and 46.6 with 16, whose clearing costs more than it saves), else one.
-  l.hcopies = (int)std::max<int64_t>(1, std::min<int64_t>(2, (int64_t)(kWsCounters / ((size_t)B * kBins * 4))));
+  l.hcopies = (int)std::max<int64_t>(1, std::min<int64_t>(kMaxFineCopies,
+                                                           (int64_t)(kWsCounters / ((size_t)B * kBins * 4))));
   size_t hist_bytes = (size_t)B * l.hcopies * kBins * 4;
   l.hist_in_head = hist_bytes <= kWsCounters;
   if (!l.hist_in_head) {
