@@ -492,7 +492,7 @@ __global__ __launch_bounds__(256) void prefix_mixed_kernel(PrefixArgs a) {
     if (w < upw && u < a.n_prefix_items) {
       static_assert(2 * 4 * kStageBytes <= kMixedSmemBytes && 4 * 2 * kStageBytes <= kMixedSmemBytes, "unit rings");
       if (upw == 2)
-        prefix_unit<4, kPaged, V, kMF>(a, smem, u, w);              // the whole 128-key chunk in flight
+        prefix_unit<4, kPaged, V, kMF>(a, smem, u, w);              // a whole chunk of up to 128 keys in flight
       else
         prefix_unit<2, kPaged, V, kMF>(a, smem, u, w);
     }
@@ -568,10 +568,13 @@ static PrefixPlan prefix_plan(int64_t N, int64_t Hq, int64_t Hkv, int64_t P, int
   p.WRp = R <= 128 ? 4 : 8;                                  // waves sharing one ring, 32 rows each
   const int64_t rows_wg = 32 * p.WRp;
   p.nrb_p = (int)((R + rows_wg - 1) / rows_wg);
-  // Prefix chunks of P/32 keys in whole tiles, within [128, 1024] (C1: 128, C2: 512).
+  // Prefix chunks of P/32 keys in whole tiles, within [64, 1024] (C1: 64, C2: 512).  The 64-key floor halves each
+  // busy wave's serial walk for short prefixes: N = 1, P = 2048, S = 256 takes 9.98 us against 11.18 with a 128-key
+  // floor, N = 32, P = 1024, S = 512 21.45 against 22.73; C1 12.18 against 12.13, N = 64 at P = 2048 34.04 against
+  // 34.16 (one process, A/B).
   int64_t chunk = (P + 31) / 32;
   chunk = (chunk + kTile - 1) / kTile * kTile;
-  chunk = std::min<int64_t>(1024, std::max<int64_t>(128, chunk));
+  chunk = std::min<int64_t>(1024, std::max<int64_t>(64, chunk));
   p.chunk_p = (int)chunk;
   p.nsplit_p = P > 0 ? (int)((P + chunk - 1) / chunk) : 0;
   p.n_prefix_items = (int)(Hkv * p.nrb_p * p.nsplit_p);
