@@ -948,11 +948,12 @@ constexpr int kRowsSmemBytes = kRowsStages * kStageBytes;
 // 2i + 1 per instruction in the partial type PT, as non-temporal stores (the row split's partials are read by a
 // later launch).  Called by every wave of the workgroup (it contains a barrier); rows >= nvalid are not written.
 // kCoherent: agent-coherent stores instead, for a reader in the same kernel.
+// store_partial_rows_wave is the same for one wave alone, through the 16 KB of LDS at wlds that no other wave uses
+// (a single-wave unit's own ring, once its walk is done): no workgroup barrier.
 template <bool kCoherent = false, class PT>
-__device__ __forceinline__ void store_partial_rows(char* smem, PT* po, float* pml, const RowState& st, int wave,
-                                                   int lane, int nvalid) {
-  __syncthreads();                                          // every wave is done with the ring
-  float* lds = reinterpret_cast<float*>(smem) + wave * 32 * 128;
+__device__ __forceinline__ void store_partial_rows_wave(char* wlds, PT* po, float* pml, const RowState& st, int lane,
+                                                        int nvalid) {
+  float* lds = reinterpret_cast<float*>(wlds);
   const int r = lane & 31, g = lane >> 5;
   const float ltot = st.l + xor32(st.l);
   const float inv = part_inv(ltot);                         // the lane's row r, normalised before the transpose
@@ -980,6 +981,13 @@ __device__ __forceinline__ void store_partial_rows(char* smem, PT* po, float* pm
     else
       *reinterpret_cast<float2*>(pml + 2 * r) = float2{st.m, ltot};
   }
+}
+
+template <bool kCoherent = false, class PT>
+__device__ __forceinline__ void store_partial_rows(char* smem, PT* po, float* pml, const RowState& st, int wave,
+                                                   int lane, int nvalid) {
+  __syncthreads();                                          // every wave is done with the ring
+  store_partial_rows_wave<kCoherent>(smem + wave * 32 * 128 * 4, po, pml, st, lane, nvalid);
 }
 
 template <int NW, class V = half8, bool kCoherent = false, class Src, class QRow, class PT>

@@ -435,10 +435,11 @@ __global__ __launch_bounds__(64 * NW) void prefix_rows_kernel(PrefixArgs a) {
 }
 
 // Prefix unit u (KV head h, prefix chunk) of a mixed launch when a KV head has at most 32 rows: one wave walks the
-// chunk for all rows through a private ring of NS stages and writes rows 0..31 of the row-block partial.  A row's
-// arithmetic is that of a row-block wave (the same tiles in the same order through the same tile function), so the
-// output bits do not depend on which form ran; several units share a workgroup so that the grid stays within one
-// dispatch round when the row-block grid would not.
+// chunk for all rows through a private ring of NS stages and writes rows 0..31 of the row-block partial, transposed
+// through that ring as the row blocks do (whole rows per store instruction).  A row's arithmetic is that of a
+// row-block wave (the same tiles in the same order through the same tile function), so the output bits do not depend
+// on which form ran; several units share a workgroup so that the grid stays within one dispatch round when the
+// row-block grid would not.
 template <int NS, int kPaged, class V, bool kMF>
 __device__ __forceinline__ void prefix_unit(const PrefixArgs& a, char* smem, int u, int w) {
   const int lane = threadIdx.x & 63;
@@ -468,8 +469,16 @@ __device__ __forceinline__ void prefix_unit(const PrefixArgs& a, char* smem, int
     walk(src);
   }
   const size_t rows_wg = 32 * a.WRp;
-  store_partial<kMF>(reinterpret_cast<part_t<elem_t<V>>*>(a.po_p) + (size_t)u * rows_wg * 128,
-                     a.pml_p + (size_t)u * rows_wg * 2, st, lane, nrows);
+  static_assert(NS * kStageBytes >= 32 * 128 * 4, "a unit's ring holds its 32 rows of 128 floats");
+  part_t<elem_t<V>>* po = reinterpret_cast<part_t<elem_t<V>>*>(a.po_p) + (size_t)u * rows_wg * 128;
+  float* pml = a.pml_p + (size_t)u * rows_wg * 2;
+  // Whole rows per store beyond 16 rows (C1, 32 rows: 11.52 us against 12.00, half the written bytes; N = 6 at G = 4:
+  // 10.96 against 11.11); up to 16 rows half of each transposed pass would be empty, and the LDS round trip costs more
+  // than it saves (N = 4 at G = 4: 10.70 against 10.35 us when every unit transposed).  Both store the same values.
+  if (nrows > 16)
+    store_partial_rows_wave<kMF>(smem + ring_off, po, pml, st, lane, nrows);
+  else
+    store_partial<kMF>(po, pml, st, lane, nrows);
   if constexpr (kMF) pfx_arrive<true>(a, h);
 }
 
