@@ -144,7 +144,9 @@ EXTRA = [(dict(N=5, P=700, S=300, S_min=1), "randn"), (dict(N=16, P=2048, S=512,
 # Row invariance (L4, ONE-PAGER.md:13-14): every request computed alone (N = 1) must give the same bits as in the
 # batch.  The C2 and C1 shapes, a prefix of many chunks with suffixes split over two chunks, and odd sizes.
 L4_CASES = [(dict(N=64, P=16384, S=2048, S_min=128), "outlier"), (dict(N=8, P=2048, S=256), "randn"),
-            (dict(N=20, P=40000, S=3000, S_min=1), "randn"), (dict(N=33, P=300, S=10), "randn")]
+            (dict(N=20, P=40000, S=3000, S_min=1), "randn"), (dict(N=33, P=300, S=10), "randn"),
+            # 64-key prefix chunks: the batch runs eight-wave row blocks, each request alone single-wave units
+            (dict(N=64, P=2048, S=256), "randn")]
 
 
 def row_inputs(inp, i):
