@@ -31,7 +31,9 @@ def run(kernel, op, shape, dist, seed):
                                         # the batch runs single-wave prefix units, a request alone the row blocks
                                         (dict(N=8, P=3000, S=2500, S_min=1), "randn"),
                                         (dict(N=4, P=8192, S=256), "randn"),
-                                        (dict(N=3, P=0, S=300), "randn"), (dict(N=5, P=700, S=0), "randn")])
+                                        (dict(N=3, P=0, S=300), "randn"), (dict(N=5, P=700, S=0), "randn"),
+                                        # 64-key chunks: the batch runs eight-wave row blocks, a request alone units
+                                        (dict(N=64, P=2048, S=256), "randn")])
 def test_prefix_rows_alone_equal_batch(shape, dist):
     import prefix_mi355x
     print(f"prefix L4 {shape} {dist}", flush=True)
